@@ -1,0 +1,288 @@
+"""Benchmark: paged decode-attention KV GB/s on one MI355X.
+
+Workload (the headline metric's configuration): one layer of Qwen3-8B-shaped
+decode attention — batch 1, 32 query / 8 KV heads, head_dim 128, bf16 KV,
+32,768-token context in 2,048 pages of 16 tokens under a seeded random page
+table, q/K/V ~ N(0,1), scale 1/sqrt(128), all pages resident.  A step is one
+attention call over the whole context.  Eight independent 128 MiB pools are
+rotated so the 256 MB Infinity Cache cannot serve the KV.
+
+Also measured (extra keys of the one JSON line):
+* the same workload with the oldest 50% of pages in pinned host RAM (host
+  link GB/s against the measured pinned H2D copy bandwidth);
+* the CPU baseline: HELM's CPU streaming attention restated by the oracle
+  (torch CPU, HELM's Path 2 and masked online-softmax loop) on the same
+  shape, timed on this host's cores for a bounded sample;
+* decode steps/s at 32k = 1 / (36 layers x per-layer call time).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "paged decode-attn KV GB/s (% HBM peak) + decode steps/s at 32k ctx"
+HBM_PEAK_GBS = 8000.0
+PCIE5_X16_GBS = 63.0
+QWEN3_8B_LAYERS = 36
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--pools", type=int, default=8, help="rotated KV pools (MALL hygiene)")
+    ap.add_argument("--offload-steps", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-offload", action="store_true")
+    ap.add_argument("--pps", type=int, default=0, help="pages per split (0 = auto)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device copy (PMC byte-count calibration)")
+    return ap.parse_args()
+
+
+def gpu_headline(args, torch, W, paged):
+    w = W.WORKLOADS["qwen3-8b-32k"]
+    dev = torch.device("cuda:0")
+    case = W.make_pool_case(w, seed=1, device=dev)
+    pools = [case["pool"]] + [torch.empty_like(case["pool"]).copy_(case["pool"])
+                              for _ in range(args.pools - 1)]
+    lens = case["lens_list"]
+    alg = W.algorithmic_bytes(w, lens)
+    out = torch.empty_like(case["q"])
+
+    def step(i):
+        p = pools[i % len(pools)]
+        paged.paged_decode_attention(case["q"], p[:, 0], p[:, 1], case["table"], case["lens"],
+                                     max_pages=case["max_pages"], out=out,
+                                     pages_per_split=args.pps)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_events = e0.elapsed_time(e1)
+    per_call_s = ms_events / 1e3 / args.steps
+    return {
+        "w": w, "case": case, "alg_bytes": alg, "kv_bytes": W.kv_bytes(w, lens),
+        "per_call_s": per_call_s, "wall_ms_per_step": wall * 1e3 / args.steps,
+        "ms_per_step": ms_events / args.steps,
+    }
+
+
+def h2d_peak(torch):
+    """Pinned host -> device copy bandwidth (256 MiB, best of 5)."""
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8).pin_memory()
+    dst = torch.empty(n, dtype=torch.uint8, device="cuda")
+    best = 0.0
+    for _ in range(6):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dst.copy_(src, non_blocking=True)
+        e1.record()
+        torch.cuda.synchronize()
+        best = max(best, n / (e0.elapsed_time(e1) / 1e3) / 1e9)
+    return best
+
+
+def gpu_offload(args, torch, W):
+    """Oldest 50% of the 32k context in pinned host pages, streamed through
+    the engine's staging ring while the resident half is attended."""
+    from helm_amd import _native
+    from helm_amd.runtime import engine
+    w = W.WORKLOADS["qwen3-8b-32k-offload50"]
+    dev = torch.device("cuda:0")
+    case = W.make_pool_case(w, seed=2, device=dev)
+    n = case["n_pages"][0]
+    n_host = int(n * w.offload_frac)
+    slot_b = 2 * w.Hkv * w.page_size * w.D * 2
+    host = torch.empty((n_host, 2, w.Hkv, w.page_size, w.D), dtype=w.dtype).pin_memory()
+    table = case["table_cpu"][0, :n].long()
+    host.copy_(case["pool"][table[:n_host].to(dev)].cpu())
+    pages = np.zeros(n, dtype=_native.PAGE_DTYPE)
+    for j in range(n):
+        if j < n_host:
+            base = host.data_ptr() + j * slot_b
+            flags = _native.HELM_PAGE_HOST
+        else:
+            base = case["pool"].data_ptr() + int(table[j]) * slot_b
+            flags = 0
+        pages[j] = (base, base + slot_b // 2, w.page_size, j * w.page_size,
+                    w.page_size * w.D, flags)
+    seq_off = np.array([0, n], dtype=np.int32)
+    eng = engine.get_engine(dev)
+    out = torch.empty_like(case["q"])
+    stream = torch.cuda.current_stream(dev)
+
+    def call():
+        _native.call("helm_stream_attn", eng, case["q"].data_ptr(), out.data_ptr(), 1, w.Hq,
+                     w.Hkv, 1, w.D, _native.ptr(pages), _native.ptr(seq_off), case["scale"], 0.0,
+                     None, 0, 0, 0, 0, _native.HELM_BF16, _native.HELM_BF16, stream.cuda_stream)
+
+    for _ in range(3):
+        call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.offload_steps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    per = e0.elapsed_time(e1) / 1e3 / args.offload_steps
+    host_bytes = n_host * slot_b
+    peak = h2d_peak(torch)
+    # parity spot check of this exact configuration against the oracle
+    from oracle.attention import attention_fp64_batched
+    K = case["pool"][table.to(dev), 0].permute(1, 0, 2, 3).reshape(w.Hkv, -1, w.D).cpu()
+    V = case["pool"][table.to(dev), 1].permute(1, 0, 2, 3).reshape(w.Hkv, -1, w.D).cpu()
+    ref = attention_fp64_batched(case["q"][0].cpu(), K, V)
+    err = (out[0].double().cpu() - ref).abs().max().item()
+    return {
+        "host_pages": n_host, "host_bytes": host_bytes, "ms_per_call": per * 1e3,
+        "host_link_GBs": host_bytes / per / 1e9, "measured_h2d_GBs": peak,
+        "frac_of_measured_h2d": host_bytes / per / 1e9 / peak,
+        "pcie5_x16_theoretical_GBs": PCIE5_X16_GBS, "max_abs_err_vs_fp64": err,
+    }
+
+
+def cpu_baseline(args, torch, W):
+    """The oracle's restatement of HELM's CPU streaming attention (torch CPU)
+    on the headline shape; bounded to about args.cpu_seconds."""
+    from oracle import attention as A
+    w = W.WORKLOADS["qwen3-8b-32k"]
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(1)
+    P, n = w.page_size, w.T // w.page_size
+    k = torch.randn(n, 1, w.Hkv, P, w.D, generator=g).to(w.dtype)
+    v = torch.randn(n, 1, w.Hkv, P, w.D, generator=g).to(w.dtype)
+    q = torch.randn(1, w.Hq, 1, w.D, generator=g).to(w.dtype)
+    pages = [(k[i], v[i]) for i in range(n)]
+    mask = torch.zeros(1, 1, 1, w.T)
+    alg = W.algorithmic_bytes(w, [w.T])
+    res = {}
+    budget = args.cpu_seconds / 2
+    for name, fn in (("path2_concat_sdpa", lambda: A.concat_sdpa(q, pages)),
+                     ("masked_online_softmax", lambda: A.online_softmax_pages(
+                         q, pages, attention_mask=mask))):
+        fn()
+        t0, calls = time.perf_counter(), 0
+        while True:
+            fn()
+            calls += 1
+            if time.perf_counter() - t0 > budget:
+                break
+        per = (time.perf_counter() - t0) / calls
+        res[name] = {"s_per_call": per, "GBs": alg / per / 1e9, "calls": calls}
+    return res, threads
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the paged decode "
+              "attention shards by sequence / KV head with no exchange, see DESIGN.md",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from helm_amd import workloads as W
+    from helm_amd import paged
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        sys.exit(1)
+    log("headline: qwen3-8b-32k all resident")
+    h = gpu_headline(args, torch, W, paged)
+    value = h["alg_bytes"] / h["per_call_s"] / 1e9
+    log(f"per call {h['per_call_s'] * 1e6:.2f} us, {value:.1f} GB/s")
+
+    if args.copy_calibration:
+        n = 1 << 30
+        a = torch.empty(n, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 1 GiB device copies done")
+
+    off = None
+    if not args.no_offload:
+        log("offload: qwen3-8b-32k, oldest 50% in pinned host")
+        off = gpu_offload(args, torch, W)
+        log(f"offload {off['ms_per_call']:.3f} ms/call, host link {off['host_link_GBs']:.1f} GB/s "
+            f"({off['frac_of_measured_h2d'] * 100:.1f}% of measured {off['measured_h2d_GBs']:.1f})")
+
+    cpu = None
+    threads = 0
+    if not args.no_cpu:
+        log("cpu baseline (oracle restatement of HELM's CPU path)")
+        cpu, threads = cpu_baseline(args, torch, W)
+        log(json.dumps(cpu))
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "paged_attn_qwen3-8b-32k_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(h["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) q/K/V, seeded random page table, 8 rotated pools",
+        "config": {"workload": "qwen3-8b-32k: 1 layer decode attention, B=1, Hq=32, Hkv=8, "
+                               "D=128, bf16, 32768 tokens in 2048 pages of 16, all resident",
+                   "global_batch": 1, "seq_len": 32768, "page_size": 16},
+        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "decode_steps_per_s_32k": round(1.0 / (QWEN3_8B_LAYERS * h["per_call_s"]), 2),
+        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "alg_bytes_per_launch": h["alg_bytes"],
+                     "avg_launch_us": round(h["per_call_s"] * 1e6, 3)},
+        "offload50": off,
+        "cpu_baseline": None if cpu is None else {
+            "value": round(cpu["path2_concat_sdpa"]["GBs"], 3), "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": (f"qwen3-8b-32k shape on host cores, HELM Path 2 (cat + fp32 SDPA) "
+                       f"{cpu['path2_concat_sdpa']['calls']} calls; masked online-softmax loop "
+                       f"{cpu['masked_online_softmax']['calls']} calls at "
+                       f"{cpu['masked_online_softmax']['GBs']:.3f} GB/s")},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,64 @@
+// Kernel instantiation + dispatch for one KV element type.  Each including
+// file defines HELM_TKV (the KV element type), HELM_TKV_IS_16BIT and
+// HELM_LAUNCH_NAME, so the instantiations compile in parallel per dtype.
+#pragma once
+
+#include "attn_kernel.h"
+
+namespace helm {
+namespace {
+
+template <typename TKV, typename TQ, int EPL, int GM, bool DOT2>
+hipError_t launch_one(const LaunchSpec& s, hipStream_t st) {
+  if (s.mode == 0) {
+    hipLaunchKernelGGL((paged_attn_kernel<TKV, TQ, EPL, GM, DOT2, PoolSrc>),
+                       s.grid, dim3(kThreads), 0, st, s.p, s.pool);
+  } else {
+    hipLaunchKernelGGL((paged_attn_kernel<TKV, TQ, EPL, GM, DOT2, DescSrc>),
+                       s.grid, dim3(kThreads), 0, st, s.p, s.desc);
+  }
+  return hipGetLastError();
+}
+
+// Generic kernels: any D <= 16*EPL, runtime G tiled by 4 rows.
+template <typename TKV, typename TQ>
+hipError_t launch_generic(const LaunchSpec& s, hipStream_t st) {
+  switch (s.epl) {
+    case 1: return launch_one<TKV, TQ, 1, 4, false>(s, st);
+    case 2: return launch_one<TKV, TQ, 2, 4, false>(s, st);
+    case 4: return launch_one<TKV, TQ, 4, 4, false>(s, st);
+    case 8: return launch_one<TKV, TQ, 8, 4, false>(s, st);
+    case 16: return launch_one<TKV, TQ, 16, 4, false>(s, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+#if HELM_TKV_IS_16BIT
+// Fast kernels: D = 128, q and KV of the same 16-bit type, exact G rows.
+template <typename T>
+hipError_t launch_fast(const LaunchSpec& s, hipStream_t st) {
+  switch (s.gm) {
+    case 1: return launch_one<T, T, 8, 1, true>(s, st);
+    case 2: return launch_one<T, T, 8, 2, true>(s, st);
+    case 3: return launch_one<T, T, 8, 3, true>(s, st);
+    case 4: return launch_one<T, T, 8, 4, true>(s, st);
+    case 5: return launch_one<T, T, 8, 5, true>(s, st);
+    case 6: return launch_one<T, T, 8, 6, true>(s, st);
+    case 7: return launch_one<T, T, 8, 7, true>(s, st);
+    case 8: return launch_one<T, T, 8, 8, true>(s, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+#endif
+
+}  // namespace
+
+hipError_t HELM_LAUNCH_NAME(const LaunchSpec& s, hipStream_t st) {
+#if HELM_TKV_IS_16BIT
+  if (s.fast) return launch_fast<HELM_TKV>(s, st);
+#endif
+  if (s.q_dtype == HELM_F32) return launch_generic<HELM_TKV, float>(s, st);
+  return launch_generic<HELM_TKV, HELM_TKV>(s, st);
+}
+
+}  // namespace helm

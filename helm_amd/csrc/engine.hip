@@ -1,0 +1,776 @@
+// C-ABI of libhelm_amd.so: launch planning, the per-device engine (copy
+// stream, workspace, staging ring, descriptor uploads), page append and the
+// evict / prefetch copies.  Declarations and contracts: include/helm_amd.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "attn_kernel.h"
+#include "helm_amd.h"
+
+namespace helm {
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  g_err = std::string(what) + ": " + hipGetErrorString(e);
+  return static_cast<int>(e);
+}
+
+#define HELM_HIP(call)                                 \
+  do {                                                 \
+    hipError_t e_ = (call);                            \
+    if (e_ != hipSuccess) return hip_fail(e_, #call);  \
+  } while (0)
+
+int elem_bytes(int dt) {
+  switch (dt) {
+    case HELM_F16:
+    case HELM_BF16: return 2;
+    case HELM_F32: return 4;
+    default: return 0;
+  }
+}
+
+int device_cus() {
+  static int cus = 0;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) {
+      int n = 0;
+      if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
+                                dev) == hipSuccess)
+        cus = n;
+    }
+    if (cus <= 0) cus = 256;
+  });
+  return cus;
+}
+
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  if (!v || !*v) return dflt;
+  return std::atoi(v);
+}
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// ---- kernel choice and split planning -----------------------------------
+struct Plan {
+  int fast, gm, epl, n_qtiles, bpp, pps, max_splits;
+  size_t ticket_bytes, ml_bytes, o_bytes;
+  size_t total() const { return ticket_bytes + ml_bytes + o_bytes; }
+};
+
+int pick_epl(int D) {
+  for (int e : {1, 2, 4, 8, 16})
+    if (16 * e >= D) return e;
+  return 0;
+}
+
+// Smallest pages-per-split the automatic choice uses: every wave gets at
+// least two 16-token blocks.
+int min_pps(int bpp) { return std::max(1, (2 * kWaves + bpp - 1) / bpp); }
+
+void size_plan(Plan& pl, int B, int Hkv, int D) {
+  const size_t tiles = (size_t)B * Hkv * pl.n_qtiles;
+  pl.ticket_bytes = align_up(tiles * 4, 256);
+  pl.ml_bytes = align_up(tiles * pl.max_splits * pl.gm * 2 * 4, 256);
+  pl.o_bytes = align_up(tiles * pl.max_splits * pl.gm * (size_t)D * 4, 256);
+}
+
+// work_pages: pages one (sequence, head, tile) walks on average; max_pages:
+// the longest sequence (bounds the split count).
+int make_plan(Plan& pl, int kv_dtype, int q_dtype, int B, int Hq, int Hkv,
+              int q_len, int D, int max_tok_per_page, int max_pages,
+              double avg_pages, int pps_req, bool aligned16) {
+  if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0)
+    return fail(HELM_E_INVALID, "Hq must be a positive multiple of Hkv");
+  if (D <= 0 || D > 256)
+    return fail(HELM_E_UNSUPPORTED, "head_dim must be in [1, 256]");
+  if (q_len <= 0 || B <= 0) return fail(HELM_E_INVALID, "empty query");
+  if (elem_bytes(kv_dtype) == 0 || elem_bytes(q_dtype) == 0)
+    return fail(HELM_E_INVALID, "unknown dtype");
+  if (q_dtype != kv_dtype && q_dtype != HELM_F32)
+    return fail(HELM_E_UNSUPPORTED,
+                "query dtype must equal the KV dtype or be float32");
+  const int G = Hq / Hkv;
+  pl.fast = (kv_dtype == q_dtype && kv_dtype != HELM_F32 && D == 128 &&
+             G <= 8 && aligned16 && env_int("HELM_AMD_GENERIC", 0) == 0)
+                ? 1 : 0;
+  pl.gm = pl.fast ? G : 4;
+  pl.epl = pl.fast ? 8 : pick_epl(D);
+  pl.n_qtiles = (G * q_len + pl.gm - 1) / pl.gm;
+  pl.bpp = std::max(1, (max_tok_per_page + kBlockTok - 1) / kBlockTok);
+  int pps = pps_req > 0 ? pps_req : env_int("HELM_AMD_PPS", 0);
+  if (pps <= 0) {
+    const double units = (double)B * Hkv * pl.n_qtiles;
+    const int target = env_int("HELM_AMD_WG_PER_CU", 2) * device_cus();
+    const double splits = std::max(1.0, target / units);
+    pps = (int)std::ceil(std::max(1.0, avg_pages) / splits);
+    pps = std::max(pps, min_pps(pl.bpp));
+  }
+  pl.pps = std::min(std::max(pps, 1), kMaxPps);
+  pl.max_splits = std::max(1, (max_pages + pl.pps - 1) / pl.pps);
+  size_plan(pl, B, Hkv, D);
+  return HELM_OK;
+}
+
+// Bytes from a page's head-0 token-0 element to the end of its last used
+// token of the last head: what a host page's K (or V) copy must cover.
+size_t page_extent(const helm_page& p, int Hkv, int D, int eb) {
+  return ((size_t)(Hkv - 1) * p.head_stride + (size_t)p.used * D) * eb;
+}
+
+bool aligned(const void* p, size_t a) {
+  return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+void fill_params(AttnParams& a, const Plan& pl, const void* q, void* out,
+                 int B, int Hq, int Hkv, int q_len, int D, float scale,
+                 float softcap, const float* mask, int64_t mbs, int64_t mhs,
+                 int64_t mqs, int causal, char* ws) {
+  a.q = q;
+  a.out = out;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  a.S = q_len;
+  a.D = D;
+  a.rows_per_tile = pl.gm;
+  a.n_qtiles = pl.n_qtiles;
+  a.scale = scale;
+  a.softcap = softcap;
+  a.mask = mask;
+  a.mask_bstride = mbs;
+  a.mask_hstride = mhs;
+  a.mask_qstride = mqs;
+  a.causal = causal;
+  a.pps = pl.pps;
+  a.bpp = pl.bpp;
+  a.lo = 0;
+  a.hi = 0x7fffffff;
+  a.split_base = 0;
+  a.total_splits = 0;
+  a.max_splits = pl.max_splits;
+  a.full_d = 0;
+  a.tickets = reinterpret_cast<uint32_t*>(ws);
+  a.ws_ml = reinterpret_cast<float*>(ws + pl.ticket_bytes);
+  a.ws_o = reinterpret_cast<float*>(ws + pl.ticket_bytes + pl.ml_bytes);
+}
+
+hipError_t dispatch(const LaunchSpec& s, hipStream_t st) {
+  switch (s.kv_dtype) {
+    case HELM_F16: return launch_attn_f16(s, st);
+    case HELM_BF16: return launch_attn_bf16(s, st);
+    case HELM_F32: return launch_attn_f32(s, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---- page append kernel -----------------------------------------------------
+constexpr int kAppendSegsPerLaunch = 24;
+struct AppendArgs {
+  helm_append_seg seg[kAppendSegsPerLaunch];
+  int n_seg;
+  int D;
+  int eb;  // element bytes
+};
+
+// grid = (segment, kv head); copies n_tok x D elements of one head, 16 bytes
+// per thread-step when every address and row is 16-byte aligned.
+__global__ __launch_bounds__(256) void page_append_kernel(AppendArgs a) {
+  const helm_append_seg& sg = a.seg[blockIdx.x];
+  const int h = blockIdx.y;
+  const int eb = a.eb;
+  const int64_t row_b = (int64_t)a.D * eb;
+  const char* sk = reinterpret_cast<const char*>(sg.src_k) +
+                   (int64_t)h * sg.src_head_stride * eb;
+  const char* sv = reinterpret_cast<const char*>(sg.src_v) +
+                   (int64_t)h * sg.src_head_stride * eb;
+  char* dk = reinterpret_cast<char*>(sg.dst_k) +
+             ((int64_t)h * sg.dst_head_stride + (int64_t)sg.dst_tok * a.D) * eb;
+  char* dv = reinterpret_cast<char*>(sg.dst_v) +
+             ((int64_t)h * sg.dst_head_stride + (int64_t)sg.dst_tok * a.D) * eb;
+  const int64_t sstride_b = sg.src_tok_stride * eb;
+  const bool vec = (row_b % 16 == 0) && (sstride_b % 16 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(sk) |
+                     reinterpret_cast<uintptr_t>(sv) |
+                     reinterpret_cast<uintptr_t>(dk) |
+                     reinterpret_cast<uintptr_t>(dv)) % 16 == 0);
+  if (vec) {
+    const int per_row = (int)(row_b / 16);
+    const int n = sg.n_tok * per_row;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int s = i / per_row;
+      const int c = i - s * per_row;
+      const uint4 kx =
+          *reinterpret_cast<const uint4*>(sk + s * sstride_b + c * 16);
+      const uint4 vx =
+          *reinterpret_cast<const uint4*>(sv + s * sstride_b + c * 16);
+      *reinterpret_cast<uint4*>(dk + s * row_b + c * 16) = kx;
+      *reinterpret_cast<uint4*>(dv + s * row_b + c * 16) = vx;
+    }
+  } else {
+    const int n = sg.n_tok * a.D;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int s = i / a.D;
+      const int d = i - s * a.D;
+      if (eb == 4) {
+        *reinterpret_cast<uint32_t*>(dk + s * row_b + d * 4) =
+            *reinterpret_cast<const uint32_t*>(sk + s * sstride_b + d * 4);
+        *reinterpret_cast<uint32_t*>(dv + s * row_b + d * 4) =
+            *reinterpret_cast<const uint32_t*>(sv + s * sstride_b + d * 4);
+      } else {
+        *reinterpret_cast<uint16_t*>(dk + s * row_b + d * 2) =
+            *reinterpret_cast<const uint16_t*>(sk + s * sstride_b + d * 2);
+        *reinterpret_cast<uint16_t*>(dv + s * row_b + d * 2) =
+            *reinterpret_cast<const uint16_t*>(sv + s * sstride_b + d * 2);
+      }
+    }
+  }
+}
+
+}  // namespace
+}  // namespace helm
+
+using namespace helm;
+
+// ---- engine -------------------------------------------------------------------
+struct helm_engine {
+  int device = 0;
+  hipStream_t copy = nullptr;
+  // workspace (tickets zeroed at allocation, left zero by every call)
+  char* ws = nullptr;
+  size_t ws_bytes = 0;
+  // staging ring for host pages
+  char* ring = nullptr;
+  size_t chunk_bytes = 0;
+  int ring_slots = 0;
+  std::vector<hipEvent_t> copy_done, slot_free;
+  std::vector<int> slot_used;
+  int next_slot = 0;
+  // descriptor uploads (pinned host -> device), a ring so the host can run ahead
+  static constexpr int kUp = 8;
+  char* up_host[kUp] = {};
+  char* up_dev[kUp] = {};
+  size_t up_bytes[kUp] = {};
+  hipEvent_t up_done[kUp] = {};
+  int up_used[kUp] = {};
+  int up_next = 0;
+  hipEvent_t ev_a = nullptr, ev_b = nullptr;
+};
+
+namespace {
+
+int engine_ensure_ws(helm_engine* e, size_t need, hipStream_t st) {
+  if (need <= e->ws_bytes) return HELM_OK;
+  HELM_HIP(hipStreamSynchronize(st));
+  HELM_HIP(hipDeviceSynchronize());
+  if (e->ws) HELM_HIP(hipFree(e->ws));
+  e->ws = nullptr;
+  e->ws_bytes = 0;
+  const size_t sz = align_up(std::max(need, (size_t)(1 << 20)) * 3 / 2, 1 << 20);
+  HELM_HIP(hipMalloc(&e->ws, sz));
+  HELM_HIP(hipMemset(e->ws, 0, sz));
+  e->ws_bytes = sz;
+  return HELM_OK;
+}
+
+int engine_ensure_ring(helm_engine* e, size_t min_chunk) {
+  if (min_chunk <= e->chunk_bytes && e->ring) return HELM_OK;
+  HELM_HIP(hipDeviceSynchronize());
+  if (e->ring) HELM_HIP(hipFree(e->ring));
+  e->ring = nullptr;
+  e->chunk_bytes = align_up(std::max(min_chunk, e->chunk_bytes), 1 << 20);
+  HELM_HIP(hipMalloc(&e->ring, e->chunk_bytes * e->ring_slots));
+  std::fill(e->slot_used.begin(), e->slot_used.end(), 0);
+  return HELM_OK;
+}
+
+// Returns a device buffer holding `n` bytes copied from `src`, uploaded on
+// `st` through a pinned staging buffer.
+int engine_upload(helm_engine* e, const void* src, size_t n, hipStream_t st,
+                  char** dev_out) {
+  const int i = e->up_next;
+  e->up_next = (e->up_next + 1) % helm_engine::kUp;
+  if (e->up_used[i]) HELM_HIP(hipEventSynchronize(e->up_done[i]));
+  if (n > e->up_bytes[i]) {
+    if (e->up_host[i]) HELM_HIP(hipHostFree(e->up_host[i]));
+    if (e->up_dev[i]) HELM_HIP(hipFree(e->up_dev[i]));
+    e->up_host[i] = nullptr;
+    e->up_dev[i] = nullptr;
+    const size_t sz = align_up(std::max(n, (size_t)65536) * 2, 4096);
+    HELM_HIP(hipHostMalloc(reinterpret_cast<void**>(&e->up_host[i]), sz,
+                           hipHostMallocDefault));
+    HELM_HIP(hipMalloc(&e->up_dev[i], sz));
+    e->up_bytes[i] = sz;
+  }
+  std::memcpy(e->up_host[i], src, n);
+  HELM_HIP(hipMemcpyAsync(e->up_dev[i], e->up_host[i], n,
+                          hipMemcpyHostToDevice, st));
+  *dev_out = e->up_dev[i];
+  e->up_used[i] = 1;
+  // the event is recorded by the caller after the consuming kernels
+  return HELM_OK;
+}
+
+int engine_mark_upload_consumed(helm_engine* e, hipStream_t st) {
+  const int i = (e->up_next + helm_engine::kUp - 1) % helm_engine::kUp;
+  HELM_HIP(hipEventRecord(e->up_done[i], st));
+  return HELM_OK;
+}
+
+// D2H / H2D copies on the engine's copy stream, ordered after `st`.
+int engine_copies(helm_engine* e, int n, const uint64_t* src,
+                  const uint64_t* dst, const uint64_t* bytes, hipMemcpyKind kind,
+                  int sync, hipStream_t st) {
+  if (n < 0) return fail(HELM_E_INVALID, "negative region count");
+  if (n == 0) return HELM_OK;
+  for (int i = 0; i < n; ++i)
+    if (!src[i] || !dst[i]) return fail(HELM_E_INVALID, "null copy address");
+  std::vector<int> idx(n);
+  for (int i = 0; i < n; ++i) idx[i] = i;
+  std::sort(idx.begin(), idx.end(),
+            [&](int a, int b) { return src[a] < src[b]; });
+  HELM_HIP(hipEventRecord(e->ev_a, st));
+  HELM_HIP(hipStreamWaitEvent(e->copy, e->ev_a, 0));
+  int i = 0;
+  while (i < n) {
+    uint64_t s0 = src[idx[i]], d0 = dst[idx[i]], len = bytes[idx[i]];
+    int j = i + 1;
+    while (j < n && src[idx[j]] == s0 + len && dst[idx[j]] == d0 + len) {
+      len += bytes[idx[j]];
+      ++j;
+    }
+    if (len)
+      HELM_HIP(hipMemcpyAsync(reinterpret_cast<void*>(d0),
+                              reinterpret_cast<const void*>(s0), len, kind,
+                              e->copy));
+    i = j;
+  }
+  HELM_HIP(hipEventRecord(e->ev_b, e->copy));
+  if (sync) {
+    HELM_HIP(hipEventSynchronize(e->ev_b));
+  } else {
+    HELM_HIP(hipStreamWaitEvent(st, e->ev_b, 0));
+  }
+  return HELM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* helm_last_error_string(void) { return g_err.c_str(); }
+
+int helm_abi_version(void) { return HELM_AMD_ABI_VERSION; }
+
+int helm_engine_create(int device, size_t chunk_bytes, int ring_slots,
+                       helm_engine** out) {
+  if (!out) return fail(HELM_E_INVALID, "null engine out pointer");
+  *out = nullptr;
+  HELM_HIP(hipSetDevice(device));
+  helm_engine* e = new helm_engine();
+  e->device = device;
+  e->chunk_bytes = chunk_bytes ? chunk_bytes : (size_t)16 << 20;
+  e->ring_slots = ring_slots > 0 ? ring_slots : 4;
+  e->copy_done.resize(e->ring_slots);
+  e->slot_free.resize(e->ring_slots);
+  e->slot_used.assign(e->ring_slots, 0);
+  int rc = HELM_OK;
+  auto chk = [&](hipError_t err, const char* what) {
+    if (err != hipSuccess && rc == HELM_OK) rc = hip_fail(err, what);
+  };
+  chk(hipStreamCreateWithFlags(&e->copy, hipStreamNonBlocking),
+      "hipStreamCreateWithFlags");
+  for (int i = 0; i < e->ring_slots; ++i) {
+    chk(hipEventCreateWithFlags(&e->copy_done[i], hipEventDisableTiming),
+        "hipEventCreate");
+    chk(hipEventCreateWithFlags(&e->slot_free[i], hipEventDisableTiming),
+        "hipEventCreate");
+  }
+  for (int i = 0; i < helm_engine::kUp; ++i)
+    chk(hipEventCreateWithFlags(&e->up_done[i], hipEventDisableTiming),
+        "hipEventCreate");
+  chk(hipEventCreateWithFlags(&e->ev_a, hipEventDisableTiming),
+      "hipEventCreate");
+  chk(hipEventCreateWithFlags(&e->ev_b, hipEventDisableTiming),
+      "hipEventCreate");
+  if (rc != HELM_OK) {
+    helm_engine_destroy(e);
+    return rc;
+  }
+  *out = e;
+  return HELM_OK;
+}
+
+int helm_engine_destroy(helm_engine* e) {
+  if (!e) return HELM_OK;
+  // teardown: report nothing, release everything that was created
+  (void)hipSetDevice(e->device);
+  (void)hipDeviceSynchronize();
+  if (e->ws) (void)hipFree(e->ws);
+  if (e->ring) (void)hipFree(e->ring);
+  for (int i = 0; i < helm_engine::kUp; ++i) {
+    if (e->up_host[i]) (void)hipHostFree(e->up_host[i]);
+    if (e->up_dev[i]) (void)hipFree(e->up_dev[i]);
+    if (e->up_done[i]) (void)hipEventDestroy(e->up_done[i]);
+  }
+  for (auto ev : e->copy_done)
+    if (ev) (void)hipEventDestroy(ev);
+  for (auto ev : e->slot_free)
+    if (ev) (void)hipEventDestroy(ev);
+  if (e->ev_a) (void)hipEventDestroy(e->ev_a);
+  if (e->ev_b) (void)hipEventDestroy(e->ev_b);
+  if (e->copy) (void)hipStreamDestroy(e->copy);
+  delete e;
+  return HELM_OK;
+}
+
+void* helm_engine_copy_stream(helm_engine* e) {
+  return e ? reinterpret_cast<void*>(e->copy) : nullptr;
+}
+
+size_t helm_query_workspace_bytes(int B, int Hq, int Hkv, int q_len, int D,
+                                  int max_pages, int page_size,
+                                  int pages_per_split) {
+  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Hq % Hkv || q_len <= 0 || D <= 0 ||
+      page_size <= 0 || max_pages < 0)
+    return 0;
+  const int G = Hq / Hkv;
+  size_t best = 0;
+  for (int gm : {G <= 8 ? G : 4, 4}) {
+    Plan pl{};
+    pl.gm = gm;
+    pl.n_qtiles = (G * q_len + gm - 1) / gm;
+    pl.bpp = std::max(1, (page_size + kBlockTok - 1) / kBlockTok);
+    const int pps = pages_per_split > 0 ? std::min(pages_per_split, kMaxPps)
+                                        : min_pps(pl.bpp);
+    pl.max_splits = std::max(1, (max_pages + pps - 1) / pps);
+    size_plan(pl, B, Hkv, D);
+    best = std::max(best, pl.total());
+  }
+  return best;
+}
+
+int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
+                           const void* v_pool, int64_t slot_stride,
+                           int64_t head_stride, const int32_t* page_table,
+                           int table_stride, const int32_t* seq_lens, int B,
+                           int Hq, int Hkv, int q_len, int D, int page_size,
+                           int max_pages, int total_pages, float scale,
+                           float softcap, const float* mask,
+                           int64_t mask_bstride, int64_t mask_hstride,
+                           int64_t mask_qstride, int kv_dtype, int q_dtype,
+                           int pages_per_split, void* workspace,
+                           size_t ws_bytes, void* stream) {
+  if (!q || !out || !k_pool || !v_pool || !page_table || !seq_lens ||
+      !workspace)
+    return fail(HELM_E_INVALID, "null pointer argument");
+  if (page_size <= 0 || max_pages < 0 || table_stride < max_pages)
+    return fail(HELM_E_INVALID, "bad page_size / max_pages / table_stride");
+  const int eb = elem_bytes(kv_dtype);
+  const int qb = elem_bytes(q_dtype);
+  const bool al = aligned(q, 16) && aligned(out, 16) && aligned(k_pool, 16) &&
+                  aligned(v_pool, 16) && (slot_stride * eb) % 16 == 0 &&
+                  (head_stride * eb) % 16 == 0 && (D * qb) % 16 == 0;
+  const double avg = total_pages > 0 ? (double)total_pages / B : max_pages;
+  Plan pl{};
+  int rc = make_plan(pl, kv_dtype, q_dtype, B, Hq, Hkv, q_len, D, page_size,
+                     max_pages, avg, pages_per_split, al);
+  if (rc != HELM_OK) return rc;
+  if (ws_bytes < pl.total())
+    return fail(HELM_E_WORKSPACE,
+                "workspace too small: need " + std::to_string(pl.total()));
+  LaunchSpec s{};
+  fill_params(s.p, pl, q, out, B, Hq, Hkv, q_len, D, scale, softcap, mask,
+              mask_bstride, mask_hstride, mask_qstride, 0,
+              reinterpret_cast<char*>(workspace));
+  s.p.full_d = (al && D == 16 * pl.epl) ? 1 : 0;
+  s.mode = 0;
+  s.pool.k_pool = reinterpret_cast<const char*>(k_pool);
+  s.pool.v_pool = reinterpret_cast<const char*>(v_pool);
+  s.pool.slot_stride_b = slot_stride * eb;
+  s.pool.head_stride_b = head_stride * eb;
+  s.pool.table = page_table;
+  s.pool.table_stride = table_stride;
+  s.pool.seq_lens = seq_lens;
+  s.pool.page_size = page_size;
+  s.pool.max_pages = max_pages;
+  s.kv_dtype = kv_dtype;
+  s.q_dtype = q_dtype;
+  s.epl = pl.epl;
+  s.gm = pl.gm;
+  s.fast = pl.fast;
+  s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.n_qtiles, B);
+  hipError_t e = dispatch(s, reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "paged_attn launch");
+  return HELM_OK;
+}
+
+int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
+                     int Hq, int Hkv, int q_len, int D, const helm_page* pages,
+                     const int32_t* seq_off, float scale, float softcap,
+                     const float* mask, int64_t mask_bstride,
+                     int64_t mask_hstride, int64_t mask_qstride, int causal,
+                     int kv_dtype, int q_dtype, void* stream) {
+  if (!eng || !q || !out || !seq_off)
+    return fail(HELM_E_INVALID, "null pointer argument");
+  if (B <= 0) return fail(HELM_E_INVALID, "B must be positive");
+  if (Hkv <= 0 || D <= 0) return fail(HELM_E_INVALID, "bad Hkv / D");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int eb = elem_bytes(kv_dtype);
+  const int qb = elem_bytes(q_dtype);
+  if (!eb || !qb) return fail(HELM_E_INVALID, "unknown dtype");
+  const int n_all = seq_off[B];
+  if (seq_off[0] != 0 || n_all < 0)
+    return fail(HELM_E_INVALID, "seq_off must start at 0");
+  if (n_all > 0 && !pages) return fail(HELM_E_INVALID, "null pages");
+
+  // ---- validate -------------------------------------------------------------
+  int max_pages = 0, max_tok = 1, n_host = 0;
+  size_t max_region = 0;
+  for (int b = 0; b < B; ++b) {
+    const int n = seq_off[b + 1] - seq_off[b];
+    if (n < 0) return fail(HELM_E_INVALID, "seq_off not monotone");
+    max_pages = std::max(max_pages, n);
+  }
+  for (int i = 0; i < n_all; ++i) {
+    const helm_page& p = pages[i];
+    if (p.used <= 0 || !p.k || !p.v || p.head_stride < p.used * D)
+      return fail(HELM_E_INVALID, "bad page descriptor " + std::to_string(i));
+    max_tok = std::max(max_tok, p.used);
+    if (p.flags & HELM_PAGE_HOST) {
+      ++n_host;
+      max_region = std::max(max_region, 2 * page_extent(p, Hkv, D, eb));
+    }
+  }
+  if (n_host && B != 1)
+    return fail(HELM_E_UNSUPPORTED, "host-resident pages need B == 1");
+
+  // ---- descriptor order: device pages, then host pages chunk by chunk -------
+  std::vector<helm_page> desc;
+  desc.reserve(n_all);
+  std::vector<int32_t> off(B + 1, 0);
+  struct Launch { int lo, hi, chunk; };
+  struct Run { uint64_t src; size_t bytes; size_t dst_off; };
+  std::vector<Launch> launches;
+  std::vector<std::vector<Run>> chunk_runs;
+  std::vector<int> chunk_slot;
+
+  if (!n_host) {
+    desc.assign(pages, pages + n_all);
+    for (int b = 0; b <= B; ++b) off[b] = seq_off[b];
+  } else {
+    int rc = engine_ensure_ring(eng, max_region);
+    if (rc != HELM_OK) return rc;
+    for (int i = 0; i < n_all; ++i)
+      if (!(pages[i].flags & HELM_PAGE_HOST)) desc.push_back(pages[i]);
+    if (!desc.empty()) launches.push_back({0, (int)desc.size(), -1});
+    std::vector<int> hidx;
+    for (int i = 0; i < n_all; ++i)
+      if (pages[i].flags & HELM_PAGE_HOST) hidx.push_back(i);
+    std::sort(hidx.begin(), hidx.end(),
+              [&](int a, int b) { return pages[a].k < pages[b].k; });
+    size_t used_b = 0;
+    int chunk_lo = (int)desc.size();
+    chunk_runs.emplace_back();
+    // Staged position of a host region; regions adjacent in host memory stay
+    // adjacent in the chunk and share one copy.
+    auto add_region = [&](uint64_t src, size_t bytes) -> uint64_t {
+      std::vector<Run>& runs = chunk_runs.back();
+      const size_t dst = used_b;
+      if (!runs.empty() && runs.back().src + runs.back().bytes == src &&
+          runs.back().dst_off + runs.back().bytes == dst)
+        runs.back().bytes += bytes;
+      else
+        runs.push_back({src, bytes, dst});
+      used_b += bytes;
+      return dst;
+    };
+    for (int i : hidx) {
+      const helm_page& p = pages[i];
+      const size_t rb = page_extent(p, Hkv, D, eb);
+      if (used_b > 0 && used_b + 2 * rb > eng->chunk_bytes) {
+        launches.push_back(
+            {chunk_lo, (int)desc.size(), (int)chunk_runs.size() - 1});
+        chunk_lo = (int)desc.size();
+        chunk_runs.emplace_back();
+        used_b = 0;
+      }
+      helm_page d = p;
+      d.k = add_region(p.k, rb);  // chunk offsets, rebased below
+      d.v = add_region(p.v, rb);
+      desc.push_back(d);
+    }
+    launches.push_back(
+        {chunk_lo, (int)desc.size(), (int)chunk_runs.size() - 1});
+    off[1] = (int)desc.size();
+    chunk_slot.resize(chunk_runs.size());
+    for (size_t c = 0; c < chunk_runs.size(); ++c) {
+      chunk_slot[c] = eng->next_slot;
+      eng->next_slot = (eng->next_slot + 1) % eng->ring_slots;
+    }
+    for (const Launch& L : launches) {
+      if (L.chunk < 0) continue;
+      const uint64_t base = reinterpret_cast<uint64_t>(eng->ring) +
+                            (uint64_t)chunk_slot[L.chunk] * eng->chunk_bytes;
+      for (int i = L.lo; i < L.hi; ++i) {
+        desc[i].k += base;
+        desc[i].v += base;
+        desc[i].flags = 0;
+      }
+    }
+  }
+
+  // ---- kernel choice on the final addresses ---------------------------------
+  bool al = aligned(q, 16) && aligned(out, 16) && (D * qb) % 16 == 0;
+  for (const helm_page& p : desc)
+    al = al && (p.k % 16 == 0) && (p.v % 16 == 0) &&
+         ((int64_t)p.head_stride * eb) % 16 == 0;
+  Plan pl{};
+  int rc = make_plan(pl, kv_dtype, q_dtype, B, Hq, Hkv, q_len, D, max_tok,
+                     std::max(max_pages, 1), (double)n_all / B, 0, al);
+  if (rc != HELM_OK) return rc;
+  int total_splits = 0;
+  std::vector<int> split_base;
+  for (const Launch& L : launches) {
+    split_base.push_back(total_splits);
+    total_splits += (L.hi - L.lo + pl.pps - 1) / pl.pps;
+  }
+  pl.max_splits = n_host ? std::max(1, total_splits)
+                         : std::max(1, (max_pages + pl.pps - 1) / pl.pps);
+  size_plan(pl, B, Hkv, D);
+  rc = engine_ensure_ws(eng, pl.total(), st);
+  if (rc != HELM_OK) return rc;
+
+  // ---- upload descriptors + sequence offsets --------------------------------
+  const size_t dbytes = desc.size() * sizeof(helm_page);
+  std::vector<char> blob(align_up(dbytes, 16) + (B + 1) * sizeof(int32_t));
+  if (dbytes) std::memcpy(blob.data(), desc.data(), dbytes);
+  std::memcpy(blob.data() + align_up(dbytes, 16), off.data(),
+              (B + 1) * sizeof(int32_t));
+  char* dev_blob = nullptr;
+  rc = engine_upload(eng, blob.data(), blob.size(), st, &dev_blob);
+  if (rc != HELM_OK) return rc;
+
+  LaunchSpec s{};
+  fill_params(s.p, pl, q, out, B, Hq, Hkv, q_len, D, scale, softcap, mask,
+              mask_bstride, mask_hstride, mask_qstride, causal, eng->ws);
+  s.p.full_d = (al && D == 16 * pl.epl) ? 1 : 0;
+  s.mode = 1;
+  s.desc.pages = reinterpret_cast<const helm_page*>(dev_blob);
+  s.desc.seq_off =
+      reinterpret_cast<const int32_t*>(dev_blob + align_up(dbytes, 16));
+  s.desc.elem_bytes = eb;
+  s.kv_dtype = kv_dtype;
+  s.q_dtype = q_dtype;
+  s.epl = pl.epl;
+  s.gm = pl.gm;
+  s.fast = pl.fast;
+
+  if (!n_host) {
+    s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.n_qtiles, B);
+    hipError_t e = dispatch(s, st);
+    if (e != hipSuccess) return hip_fail(e, "stream_attn launch");
+    return engine_mark_upload_consumed(eng, st);
+  }
+
+  // ---- mixed residency (B == 1): device pages now, chunks as they land -----
+  s.p.total_splits = total_splits;
+  for (size_t li = 0; li < launches.size(); ++li) {
+    const Launch& L = launches[li];
+    if (L.chunk >= 0) {
+      const int slot = chunk_slot[L.chunk];
+      if (eng->slot_used[slot])
+        HELM_HIP(hipStreamWaitEvent(eng->copy, eng->slot_free[slot], 0));
+      char* dst = eng->ring + (size_t)slot * eng->chunk_bytes;
+      for (const Run& r : chunk_runs[L.chunk])
+        HELM_HIP(hipMemcpyAsync(dst + r.dst_off,
+                                reinterpret_cast<const void*>(r.src), r.bytes,
+                                hipMemcpyHostToDevice, eng->copy));
+      HELM_HIP(hipEventRecord(eng->copy_done[slot], eng->copy));
+      HELM_HIP(hipStreamWaitEvent(st, eng->copy_done[slot], 0));
+    }
+    s.p.lo = L.lo;
+    s.p.hi = L.hi;
+    s.p.split_base = split_base[li];
+    const int nsp = (L.hi - L.lo + pl.pps - 1) / pl.pps;
+    s.grid = dim3(std::max(1, nsp), Hkv * pl.n_qtiles, 1);
+    hipError_t e = dispatch(s, st);
+    if (e != hipSuccess) return hip_fail(e, "stream_attn chunk launch");
+    if (L.chunk >= 0) {
+      const int slot = chunk_slot[L.chunk];
+      HELM_HIP(hipEventRecord(eng->slot_free[slot], st));
+      eng->slot_used[slot] = 1;
+    }
+  }
+  return engine_mark_upload_consumed(eng, st);
+}
+
+int helm_page_append(const helm_append_seg* segs, int n_segs, int Hkv, int D,
+                     int dtype, void* stream) {
+  const int eb = elem_bytes(dtype);
+  if (!eb) return fail(HELM_E_INVALID, "unknown dtype");
+  if (n_segs < 0 || Hkv <= 0 || D <= 0)
+    return fail(HELM_E_INVALID, "bad append shape");
+  if (n_segs == 0) return HELM_OK;
+  if (!segs) return fail(HELM_E_INVALID, "null segments");
+  for (int i = 0; i < n_segs; ++i) {
+    const helm_append_seg& s = segs[i];
+    if (!s.dst_k || !s.dst_v || !s.src_k || !s.src_v || s.n_tok < 0 ||
+        s.dst_tok < 0 || s.dst_head_stride < (s.dst_tok + s.n_tok) * D)
+      return fail(HELM_E_INVALID, "bad append segment " + std::to_string(i));
+  }
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  for (int base = 0; base < n_segs; base += kAppendSegsPerLaunch) {
+    AppendArgs a{};
+    a.n_seg = std::min(kAppendSegsPerLaunch, n_segs - base);
+    a.D = D;
+    a.eb = eb;
+    for (int i = 0; i < a.n_seg; ++i) a.seg[i] = segs[base + i];
+    hipLaunchKernelGGL(page_append_kernel, dim3(a.n_seg, Hkv), dim3(256), 0,
+                       st, a);
+    HELM_HIP(hipGetLastError());
+  }
+  return HELM_OK;
+}
+
+int helm_evict_pages(helm_engine* eng, int n, const uint64_t* src_dev,
+                     const uint64_t* dst_host, const uint64_t* bytes, int sync,
+                     void* stream) {
+  if (!eng) return fail(HELM_E_INVALID, "null engine");
+  if (n > 0 && (!src_dev || !dst_host || !bytes))
+    return fail(HELM_E_INVALID, "null region arrays");
+  return engine_copies(eng, n, src_dev, dst_host, bytes,
+                       hipMemcpyDeviceToHost, sync,
+                       reinterpret_cast<hipStream_t>(stream));
+}
+
+int helm_prefetch_pages(helm_engine* eng, int n, const uint64_t* src_host,
+                        const uint64_t* dst_dev, const uint64_t* bytes,
+                        int sync, void* stream) {
+  if (!eng) return fail(HELM_E_INVALID, "null engine");
+  if (n > 0 && (!src_host || !dst_dev || !bytes))
+    return fail(HELM_E_INVALID, "null region arrays");
+  return engine_copies(eng, n, src_host, dst_dev, bytes,
+                       hipMemcpyHostToDevice, sync,
+                       reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

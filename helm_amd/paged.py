@@ -1,0 +1,88 @@
+"""Direct binding of the batched pool-layout decode attention
+(``helm_paged_decode_attn``): the vLLM-style entry point that the
+benchmark and any caller with its own page table use.
+
+The pool is the allocator's arena ``[n_slots, 2, Hkv, page, D]``;
+``k_pool = arena[:, 0]`` and ``v_pool = arena[:, 1]`` are passed as views, so
+the slot stride is ``2*Hkv*page*D`` elements and one page's head tile is
+``page*D`` contiguous elements.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from helm_amd import _native
+from helm_amd.runtime import engine as _engine
+
+_workspaces: Dict[int, torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A zero-initialised byte workspace of at least `nbytes` on `device`
+    (reused; the kernels leave its ticket region zero)."""
+    idx = _engine.device_index(device)
+    ws = _workspaces.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        torch.cuda.current_stream(device).synchronize()
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[idx] = ws
+    return ws
+
+
+def paged_decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                           page_table: torch.Tensor, seq_lens: torch.Tensor,
+                           max_pages: Optional[int] = None, total_pages: int = 0,
+                           scale: Optional[float] = None, softcap: Optional[float] = None,
+                           attention_mask: Optional[torch.Tensor] = None,
+                           out: Optional[torch.Tensor] = None,
+                           pages_per_split: int = 0) -> torch.Tensor:
+    """Decode attention of q [B,Hq,q_len,D] over pooled pages.
+
+    k_pool / v_pool: [n_slots, Hkv, page, D] (any slot stride, dense rows);
+    page_table: int32 [B, >=max_pages] slot ids; seq_lens: int32 [B] tokens
+    (device).  attention_mask: additive fp32-convertible [B|1, 1|Hq, q_len|1,
+    >=max tokens].  Returns out [B,Hq,q_len,D] in q's dtype."""
+    if q.device.type != "cuda":
+        raise RuntimeError("paged_decode_attention needs HIP tensors")
+    B, Hq, S, D = q.shape
+    n_slots, Hkv, P, Dk = k_pool.shape
+    if Dk != D or v_pool.shape != k_pool.shape:
+        raise ValueError("pool shapes do not match q")
+    if k_pool.stride()[1:] != v_pool.stride()[1:] or k_pool.stride(0) != v_pool.stride(0):
+        raise ValueError("k_pool and v_pool must share strides")
+    if k_pool.stride(3) != 1 or k_pool.stride(2) != D:
+        raise ValueError("pool pages need dense [page, D] rows")
+    if page_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
+        raise TypeError("page_table and seq_lens must be int32")
+    if max_pages is None:
+        max_pages = page_table.size(1)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    mask_ptr, mbs, mhs, mqs = None, 0, 0, 0
+    m = None
+    if attention_mask is not None:
+        m = attention_mask.to(device=q.device, dtype=torch.float32)
+        if m.stride(3) != 1:
+            m = m.contiguous()
+        mask_ptr = m.data_ptr()
+        mbs = m.stride(0) if m.size(0) > 1 else 0
+        mhs = m.stride(1) if m.size(1) > 1 else 0
+        mqs = m.stride(2) if m.size(2) > 1 else 0
+    kcode = _native.dtype_code(k_pool.dtype)
+    qcode = _native.dtype_code(q.dtype)
+    lib = _native.load()
+    need = lib.helm_query_workspace_bytes(B, Hq, Hkv, S, D, max_pages, P, pages_per_split)
+    ws = workspace(q.device, need)
+    _native.call("helm_paged_decode_attn", q.data_ptr(), out.data_ptr(), k_pool.data_ptr(),
+                 v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), page_table.data_ptr(),
+                 page_table.stride(0), seq_lens.data_ptr(), B, Hq, Hkv, S, D, P, max_pages,
+                 total_pages, float(scale), float(softcap) if softcap else 0.0, mask_ptr, mbs,
+                 mhs, mqs, kcode, qcode, pages_per_split, ws.data_ptr(), ws.numel(),
+                 _engine.stream_ptr(q.device))
+    return out

@@ -1,0 +1,622 @@
+"""Paged KV cache + streaming attention — drop-in for helm/runtime/kv_cache.py.
+
+Same public surface as HELM (helm/runtime/kv_cache.py:15-662): paging
+counters, ``KVPage``, ``LayerKVCache``, ``KVCacheManager`` (append, residency
+watermark, oldest-first eviction, contiguous fast path) and
+``perform_streaming_attention``.  What changes is where the work happens:
+
+* token appends are one ``helm_page_append`` kernel per call instead of two
+  ``copy_`` per page (kv_cache.py:135-136, :164-165);
+* eviction moves all selected pages with one batched, coalesced
+  ``helm_evict_pages`` copy into pinned host slots (kv_cache.py:179-222);
+* attention is ``helm_stream_attn``: split-K HIP kernels over the page list,
+  with host pages prefetched through a device staging ring on the engine's
+  copy stream while the device pages are being processed (kv_cache.py:405-662).
+
+There is no CPU compute path: a query that is not on a HIP device raises.
+"""
+from __future__ import annotations
+
+import math
+import os
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+
+from helm_amd import _native
+from helm_amd.runtime import engine as _engine
+from helm_amd.runtime.page import KVPage
+
+__all__ = [
+    "KVPagingStats", "reset_paging_stats", "get_paging_stats", "KVPage", "LayerKVCache",
+    "KVCacheManager", "perform_streaming_attention",
+]
+
+
+# ── paging counters (kv_cache.py:15-62) ─────────────────────────────────────────
+@dataclass
+class KVPagingStats:
+    evict_calls: int = 0
+    pages_evicted: int = 0
+    bytes_evicted: int = 0
+    prefetch_calls: int = 0
+    pages_prefetched: int = 0
+    bytes_prefetched: int = 0
+
+
+_PAGING_STATS = KVPagingStats()
+
+
+def reset_paging_stats() -> None:
+    """Zero the process-global paging counters."""
+    global _PAGING_STATS
+    _PAGING_STATS = KVPagingStats()
+
+
+def get_paging_stats() -> dict:
+    """The paging counters as a plain dict."""
+    s = _PAGING_STATS
+    return {
+        "evict_calls": s.evict_calls,
+        "pages_evicted": s.pages_evicted,
+        "bytes_evicted": s.bytes_evicted,
+        "prefetch_calls": s.prefetch_calls,
+        "pages_prefetched": s.pages_prefetched,
+        "bytes_prefetched": s.bytes_prefetched,
+    }
+
+
+def _record_eviction(n_pages: int, n_bytes: int) -> None:
+    """One eviction call that moved n_pages (n_bytes) GPU->CPU."""
+    if n_pages <= 0:
+        return
+    _PAGING_STATS.evict_calls += 1
+    _PAGING_STATS.pages_evicted += n_pages
+    _PAGING_STATS.bytes_evicted += n_bytes
+
+
+def _record_prefetch(n_pages: int, n_bytes: int) -> None:
+    """One attention call that streamed n_pages (n_bytes) CPU->GPU."""
+    if n_pages <= 0:
+        return
+    _PAGING_STATS.prefetch_calls += 1
+    _PAGING_STATS.pages_prefetched += n_pages
+    _PAGING_STATS.bytes_prefetched += n_bytes
+
+
+def _page_bytes(page: KVPage) -> int:
+    """K+V bytes of a whole page tensor (kv_cache.py:218, :232)."""
+    return page.k_tensor.numel() * page.k_tensor.element_size() * 2
+
+
+# ── layer cache (kv_cache.py:77-86) ───────────────────────────────────────────
+class LayerKVCache:
+    def __init__(self, layer_id: int):
+        self.layer_id = layer_id
+        self.pages: List[KVPage] = []
+        self.tail_page: Optional[KVPage] = None
+        self.total_tokens: int = 0
+
+    def append_page(self, page: KVPage):
+        self.pages.append(page)
+        self.tail_page = page
+
+
+# ── token writes ───────────────────────────────────────────────────────────────
+class _AppendQueue:
+    """Token writes into device pages, flushed as one helm_page_append launch."""
+
+    def __init__(self):
+        self.rows = []
+        self.keep = []          # source tensors alive until the launch is queued
+        self.device = None
+        self.dtype = None
+        self.hkv = 0
+        self.d = 0
+
+    def add(self, dst_k: torch.Tensor, dst_v: torch.Tensor, dst_tok: int, K: torch.Tensor,
+            V: torch.Tensor) -> None:
+        n = K.size(2)
+        if n == 0:
+            return
+        if K.dtype != dst_k.dtype:
+            K = K.to(dst_k.dtype)
+        if V.dtype != dst_v.dtype:
+            V = V.to(dst_v.dtype)
+        if K.stride(3) != 1 or V.stride(3) != 1 or K.stride()[1:] != V.stride()[1:]:
+            K, V = K.contiguous(), V.contiguous()
+        if dst_k.stride(1) != dst_v.stride(1) or dst_k.stride(2) != dst_k.size(3):
+            raise ValueError("destination page tensors must be [1, Hkv, P, D] with dense rows")
+        key = (K.device, dst_k.dtype, dst_k.size(1), dst_k.size(3))
+        if self.rows and key != (self.device, self.dtype, self.hkv, self.d):
+            self.flush()
+        self.device, self.dtype, self.hkv, self.d = key
+        self.rows.append((dst_k.data_ptr(), dst_v.data_ptr(), K.data_ptr(), V.data_ptr(),
+                          K.stride(1), K.stride(2), dst_k.stride(1), dst_tok, n, 0))
+        self.keep.append((K, V))
+
+    def flush(self) -> None:
+        if not self.rows:
+            return
+        segs = np.array(self.rows, dtype=_native.APPEND_DTYPE)
+        _native.call("helm_page_append", _native.ptr(segs), len(segs), self.hkv, self.d,
+                     _native.dtype_code(self.dtype), _engine.stream_ptr(self.device))
+        self.rows.clear()
+        self.keep.clear()
+
+
+def _write_tokens(queue: _AppendQueue, page: KVPage, dst_tok: int, K: torch.Tensor,
+                  V: torch.Tensor) -> None:
+    n = K.size(2)
+    if page.device.type == "cuda" and K.device.type == "cuda" and V.device.type == "cuda":
+        queue.add(page.k_tensor, page.v_tensor, dst_tok, K, V)
+    else:
+        queue.flush()
+        page.k_tensor[:, :, dst_tok:dst_tok + n, :].copy_(K)
+        page.v_tensor[:, :, dst_tok:dst_tok + n, :].copy_(V)
+
+
+def _evict_sync() -> bool:
+    return not bool(os.environ.get("HELM_AMD_ASYNC_EVICT"))
+
+
+# ── cache manager (kv_cache.py:88-376) ─────────────────────────────────────────
+class KVCacheManager:
+    """Owns every layer's pages: appends, residency watermark, eviction."""
+
+    def __init__(self, allocator, gpu_high_watermark_bytes: int = 512 * 1024 * 1024):
+        self.allocator = allocator
+        self.layers = {}
+        self.gpu_high_watermark_bytes = gpu_high_watermark_bytes
+        self.cont_K: dict = {}
+        self.cont_V: dict = {}
+        self.cont_capacity: int = 0
+        self.cont_num_layers: int = 0
+        self.cont_seq_len: int = 0
+        self.cont_prefill_len: int = 0
+        self.use_contiguous: bool = False
+        self._appends = _AppendQueue()
+
+    def initialize_layer_caches(self, num_layers: int):
+        for i in range(num_layers):
+            self.layers[i] = LayerKVCache(layer_id=i)
+
+    def _layer(self, layer_id: int) -> LayerKVCache:
+        layer = self.layers.get(layer_id)
+        if layer is None:
+            layer = self.layers[layer_id] = LayerKVCache(layer_id)
+        return layer
+
+    def append_prefill(self, layer_id: int, K_prefill: torch.Tensor, V_prefill: torch.Tensor):
+        """Split a [1,Hkv,S,D] chunk into page-sized blocks, each a new page
+        starting at the layer's running token count; the residency policy runs
+        after every page (kv_cache.py:113-143)."""
+        layer = self._layer(layer_id)
+        seq_len = K_prefill.size(2)
+        page_size = self.allocator.page_size
+        device = K_prefill.device
+        try:
+            for start_idx in range(0, seq_len, page_size):
+                chunk_len = min(page_size, seq_len - start_idx)
+                end_idx = start_idx + chunk_len
+                page = self.allocator.allocate(device)
+                page.layer_id = layer_id
+                page.start_token = layer.total_tokens
+                page.used_tokens = chunk_len
+                _write_tokens(self._appends, page, 0, K_prefill[:, :, start_idx:end_idx, :],
+                              V_prefill[:, :, start_idx:end_idx, :])
+                layer.append_page(page)
+                layer.total_tokens += chunk_len
+                self._enforce_residency_policy()
+        finally:
+            self._appends.flush()
+
+    def append_decode(self, layer_id: int, K_new: torch.Tensor, V_new: torch.Tensor,
+                      skip_residency: bool = False):
+        """Append one token; a new page when the tail is missing or full
+        (kv_cache.py:145-171)."""
+        self._append_decode_deferred(layer_id, K_new, V_new)
+        self._appends.flush()
+        if not skip_residency:
+            self._enforce_residency_policy()
+
+    def _append_decode_deferred(self, layer_id: int, K_new: torch.Tensor, V_new: torch.Tensor):
+        layer = self._layer(layer_id)
+        device = K_new.device
+        if layer.tail_page is None or layer.tail_page.used_tokens == layer.tail_page.capacity_tokens:
+            page = self.allocator.allocate(device)
+            page.layer_id = layer_id
+            page.start_token = layer.total_tokens
+            page.used_tokens = 0
+            layer.append_page(page)
+        page = layer.tail_page
+        _write_tokens(self._appends, page, page.used_tokens, K_new, V_new)
+        page.used_tokens += 1
+        layer.total_tokens += 1
+
+    def iterate_layer_pages(self, layer_id: int):
+        if layer_id not in self.layers:
+            return []
+        return list(self.layers[layer_id].pages)
+
+    def _evictable(self):
+        """(layer, page) pairs HELM may evict: GPU-resident, full, not a tail
+        (kv_cache.py:184-192), in layer then page order."""
+        out = []
+        for layer in self.layers.values():
+            tail = layer.tail_page
+            for page in layer.pages:
+                if (page.state == 'GPU' and page.device.type == 'cuda' and page is not tail
+                        and page.used_tokens == page.capacity_tokens):
+                    out.append((layer, page))
+        return out
+
+    def evict_pages(self, bytes_to_evict: int):
+        """Oldest-first (by start_token) eviction of at least `bytes_to_evict`
+        bytes of full, non-tail GPU pages to host (kv_cache.py:179-222)."""
+        if bytes_to_evict <= 0:
+            return
+        self._appends.flush()
+        gpu_pages = self._evictable()
+        gpu_pages.sort(key=lambda t: t[1].start_token)
+        chosen, evicted_bytes = [], 0
+        for layer, page in gpu_pages:
+            if evicted_bytes >= bytes_to_evict:
+                break
+            chosen.append((layer, page))
+            evicted_bytes += _page_bytes(page)
+        if not chosen:
+            _record_eviction(0, 0)
+            return
+        new_pages = self.allocator.move_pages([p for _, p in chosen], torch.device('cpu'),
+                                              sync=_evict_sync())
+        moved_bytes = 0
+        for (layer, page), new_page in zip(chosen, new_pages):
+            assert new_page.start_token == page.start_token, "Page invariant broken during migration"
+            idx = next(i for i, p in enumerate(layer.pages) if p is page)
+            layer.pages[idx] = new_page
+            if layer.tail_page is page:
+                layer.tail_page = new_page
+            moved_bytes += _page_bytes(new_page)
+        _record_eviction(len(new_pages), moved_bytes)
+
+    def _enforce_residency_policy(self):
+        """Evict the excess of evictable GPU bytes over the watermark
+        (kv_cache.py:224-235)."""
+        gpu_bytes = 0
+        for layer in self.layers.values():
+            tail = layer.tail_page
+            for page in layer.pages:
+                if (page.state == 'GPU' and page.device.type == 'cuda' and page is not tail
+                        and page.used_tokens == page.capacity_tokens):
+                    gpu_bytes += _page_bytes(page)
+        if gpu_bytes > self.gpu_high_watermark_bytes:
+            self.evict_pages(gpu_bytes - self.gpu_high_watermark_bytes)
+
+    def seq_len(self):
+        if 0 in self.layers:
+            return self.layers[0].total_tokens
+        return 0
+
+    def num_layers(self):
+        return len(self.layers)
+
+    def clear(self):
+        self._appends.flush()
+        for layer in self.layers.values():
+            for page in layer.pages:
+                if page.state != 'DEAD':
+                    self.allocator.free(page)
+            layer.pages.clear()
+            layer.tail_page = None
+            layer.total_tokens = 0
+        self.layers.clear()
+
+    def all_gpu_resident(self, layer_id: int) -> bool:
+        if layer_id not in self.layers:
+            return True
+        for page in self.layers[layer_id].pages:
+            if page.used_tokens > 0 and page.state != 'GPU':
+                return False
+        return True
+
+    # ── contiguous fast path (kv_cache.py:269-354) ──────────────────────────
+    def build_contiguous(self, num_layers: int, num_kv_heads: int, head_dim: int,
+                         capacity: int, device: torch.device, dtype: torch.dtype) -> bool:
+        cap = capacity
+        floor = max(1, min(capacity, 1024))
+        while cap >= floor:
+            try:
+                self.cont_K.clear()
+                self.cont_V.clear()
+                for lid in range(num_layers):
+                    self.cont_K[lid] = torch.zeros(1, num_kv_heads, cap, head_dim, device=device,
+                                                   dtype=dtype)
+                    self.cont_V[lid] = torch.zeros(1, num_kv_heads, cap, head_dim, device=device,
+                                                   dtype=dtype)
+                self.cont_capacity = cap
+                self.cont_num_layers = num_layers
+                self.use_contiguous = True
+                return True
+            except (torch.cuda.OutOfMemoryError, RuntimeError):
+                self.cont_K.clear()
+                self.cont_V.clear()
+                if device.type == 'cuda':
+                    torch.cuda.empty_cache()
+                cap //= 2
+        self.use_contiguous = False
+        return False
+
+    def prefill_contiguous(self, layer_id: int, K: torch.Tensor, V: torch.Tensor):
+        n = K.shape[2]
+        self._write_contiguous(layer_id, 0, K, V)
+        if layer_id == 0:
+            self.cont_prefill_len = n
+            self.cont_seq_len = n
+
+    def write_decode_contiguous(self, layer_id: int, K_new: torch.Tensor, V_new: torch.Tensor):
+        self._write_contiguous(layer_id, self.cont_seq_len, K_new, V_new)
+
+    def _write_contiguous(self, layer_id: int, at: int, K: torch.Tensor, V: torch.Tensor):
+        dk, dv = self.cont_K[layer_id], self.cont_V[layer_id]
+        if dk.device.type == "cuda" and K.device.type == "cuda":
+            self._appends.add(dk, dv, at, K, V)
+            self._appends.flush()
+        else:
+            n = K.shape[2]
+            dk[:, :, at:at + n, :].copy_(K)
+            dv[:, :, at:at + n, :].copy_(V)
+
+    def get_kv_contiguous(self, layer_id: int):
+        n = self.cont_seq_len + 1
+        return self.cont_K[layer_id][:, :, :n, :], self.cont_V[layer_id][:, :, :n, :]
+
+    def advance_contiguous(self):
+        self.cont_seq_len += 1
+
+    def migrate_contiguous_to_pages(self):
+        if not self.cont_K:
+            return
+        decode_start = self.cont_prefill_len
+        decode_end = self.cont_seq_len
+        if decode_end > decode_start:
+            for layer_id in range(self.cont_num_layers):
+                decode_K = self.cont_K[layer_id][:, :, decode_start:decode_end, :]
+                decode_V = self.cont_V[layer_id][:, :, decode_start:decode_end, :]
+                self.append_prefill(layer_id, decode_K, decode_V)
+        self.drop_contiguous()
+
+    def drop_contiguous(self):
+        self.cont_K.clear()
+        self.cont_V.clear()
+        self.use_contiguous = False
+
+    def reset_contiguous(self):
+        if self.cont_K:
+            self.use_contiguous = True
+            self.cont_seq_len = 0
+            self.cont_prefill_len = 0
+
+    def layers_keys(self):
+        return sorted(self.layers.keys())
+
+    def report_bytes_per_tier(self) -> dict:
+        gpu_bytes = 0
+        cpu_bytes = 0
+        for layer in self.layers.values():
+            for page in layer.pages:
+                if page.state == 'DEAD':
+                    continue
+                b = _page_bytes(page)
+                if page.state == 'GPU':
+                    gpu_bytes += b
+                elif page.state == 'CPU':
+                    cpu_bytes += b
+        return {"gpu_active_bytes": gpu_bytes, "cpu_active_bytes": cpu_bytes}
+
+
+# ── copy stream (kv_cache.py:383-396) ──────────────────────────────────────────
+def _get_kv_copy_stream(device: torch.device) -> torch.cuda.Stream:
+    """The per-device copy stream that evictions and prefetches run on."""
+    return _engine.copy_stream(device)
+
+
+def _async_kv_prefetch_enabled() -> bool:
+    """HELM_DISABLE_ASYNC_KV gates the overlapped prefetch (ablations)."""
+    return not bool(os.environ.get("HELM_DISABLE_ASYNC_KV"))
+
+
+# ── native attention ────────────────────────────────────────────────────────────
+class _Segment:
+    """A run of tokens of one sequence as the kernel sees it."""
+    __slots__ = ("k", "v", "used", "head_stride", "host", "keep")
+
+    def __init__(self, k, v, used, head_stride, host, keep=None):
+        self.k, self.v, self.used, self.head_stride, self.host, self.keep = (
+            k, v, used, head_stride, host, keep)
+
+
+def _page_segments(page: KVPage, b: int, B: int, Hkv: int, D: int, dtype) -> _Segment:
+    k, v = page.k_tensor, page.v_tensor
+    if k.dim() != 4 or v.shape != k.shape:
+        raise ValueError("page tensors must be [batch, Hkv, P, D] and K/V alike")
+    if k.size(1) != Hkv or k.size(3) != D:
+        raise ValueError(f"page shape {tuple(k.shape)} does not match Hkv={Hkv}, D={D}")
+    if k.dtype != dtype or v.dtype != dtype:
+        raise TypeError("all pages of one attention call must share one dtype")
+    if k.size(0) not in (1, B):
+        raise ValueError(f"page batch {k.size(0)} does not match query batch {B}")
+    if (k.stride(3) != 1 or k.stride(2) != D or v.stride(3) != 1 or v.stride(2) != D
+            or v.stride(1) != k.stride(1)):
+        k, v = k.contiguous(), v.contiguous()
+    bb = b if k.size(0) > 1 else 0
+    es = k.element_size()
+    return _Segment(k.data_ptr() + bb * k.stride(0) * es, v.data_ptr() + bb * v.stride(0) * es,
+                    page.used_tokens, k.stride(1), k.device.type != "cuda", (k, v))
+
+
+def _contiguous_segments(K: torch.Tensor, V: torch.Tensor, b: int, block: int = 16):
+    """[B,Hkv,n,D] contiguous-cache views as 16-token virtual pages."""
+    n = K.size(2)
+    es = K.element_size()
+    bb = b if K.size(0) > 1 else 0
+    kb = K.data_ptr() + bb * K.stride(0) * es
+    vb = V.data_ptr() + bb * V.stride(0) * es
+    segs = []
+    for t in range(0, n, block):
+        segs.append(_Segment(kb + t * K.stride(2) * es, vb + t * V.stride(2) * es,
+                             min(block, n - t), K.stride(1), False, None))
+    return segs
+
+
+def _attend(query: torch.Tensor, seqs: Sequence[Sequence[_Segment]], Hkv: int, kv_dtype,
+            scale: float, attention_mask: Optional[torch.Tensor], softcap: Optional[float],
+            causal: bool) -> torch.Tensor:
+    """One helm_stream_attn call: query [B,Hq,S,D], seqs[b] = ordered segments."""
+    device = query.device
+    B, Hq, S, D = query.shape
+    if Hq % Hkv != 0:
+        raise ValueError(f"num_q_heads {Hq} is not a multiple of num_kv_heads {Hkv}")
+    kcode = _native.dtype_code(kv_dtype)
+    q = query
+    if q.dtype != kv_dtype and q.dtype != torch.float32:
+        q = q.float()
+    q = q.contiguous()
+    qcode = _native.dtype_code(q.dtype)
+    out = torch.empty(q.shape, dtype=q.dtype, device=device)
+
+    n = sum(len(s) for s in seqs)
+    arr = np.zeros(n, dtype=_native.PAGE_DTYPE)
+    seq_off = np.zeros(B + 1, dtype=np.int32)
+    i = 0
+    t_max = 0
+    for b, segs in enumerate(seqs):
+        tok = 0
+        for sg in segs:
+            arr[i] = (sg.k, sg.v, sg.used, tok, sg.head_stride,
+                      _native.HELM_PAGE_HOST if sg.host else 0)
+            tok += sg.used
+            i += 1
+        seq_off[b + 1] = i
+        t_max = max(t_max, tok)
+
+    mask_ptr, mbs, mhs, mqs = None, 0, 0, 0
+    m = None
+    if attention_mask is not None:
+        m = attention_mask.to(device=device, dtype=torch.float32)
+        if m.dim() != 4:
+            raise ValueError("attention_mask must be 4-D [B, H, q_len, kv_len]")
+        Bm, Hm, Sm, Tm = m.shape
+        if Bm not in (1, B) or Hm not in (1, Hq) or Sm not in (1, S):
+            raise ValueError(f"attention_mask shape {tuple(m.shape)} does not broadcast to "
+                             f"[{B}, {Hq}, {S}, kv_len]")
+        if Tm < t_max:
+            if Tm != 1:
+                raise ValueError(f"attention_mask covers {Tm} keys, the pages hold {t_max}")
+            m = m.expand(Bm, Hm, Sm, t_max)
+        if m.stride(3) != 1:
+            m = m.contiguous()
+        mask_ptr = m.data_ptr()
+        mbs = m.stride(0) if Bm > 1 else 0
+        mhs = m.stride(1) if Hm > 1 else 0
+        mqs = m.stride(2) if Sm > 1 else 0
+
+    _native.call("helm_stream_attn", _engine.get_engine(device), q.data_ptr(), out.data_ptr(),
+                 B, Hq, Hkv, S, D, _native.ptr(arr) if n else None, _native.ptr(seq_off),
+                 float(scale), float(softcap) if softcap is not None else 0.0, mask_ptr,
+                 mbs, mhs, mqs, 1 if causal else 0, kcode, qcode, _engine.stream_ptr(device))
+    return out if out.dtype == query.dtype else out.to(query.dtype)
+
+
+def _stage_host_pages_sync(segs: List[_Segment], device: torch.device) -> List[_Segment]:
+    """HELM_DISABLE_ASYNC_KV: copy host pages to device synchronously first."""
+    out = []
+    for sg in segs:
+        if not sg.host:
+            out.append(sg)
+            continue
+        k, v = sg.keep
+        kd = k.to(device)
+        vd = v.to(device)
+        torch.cuda.current_stream(device).synchronize()
+        out.append(_Segment(kd.data_ptr() + (sg.k - k.data_ptr()),
+                            vd.data_ptr() + (sg.v - v.data_ptr()),
+                            sg.used, sg.head_stride, False, (kd, vd)))
+    return out
+
+
+def perform_streaming_attention(
+    query: torch.Tensor,
+    pages: List[KVPage],
+    scale: float = None,
+    attention_mask: Optional[torch.Tensor] = None,
+    softcap: Optional[float] = None,
+):
+    """Attention of `query` [B,Hq,q_len,D] over `pages`, HELM's helper
+    (kv_cache.py:405-662) with HIP kernels.
+
+    Path selection follows HELM: a mask or softcap attends every active page
+    in token order (online-softmax branch, :468-555); otherwise GPU-only pages
+    use top-left causal masking when q_len > 1 (Path 1, :562-568) and mixed
+    residency attends all pages unmasked (Path 3, :584-662).  Host pages are
+    prefetched through the engine's staging ring, overlapped with the device
+    pages.  The output has the query's shape and dtype.
+    """
+    device = query.device
+    if scale is None:
+        scale = 1.0 / math.sqrt(query.size(-1))
+    active_pages = [p for p in pages if p.used_tokens > 0 and p.state != 'DEAD']
+    if not active_pages:
+        return torch.zeros_like(query)
+
+    gpu_pages = [p for p in active_pages if p.state == 'GPU' and p.device.type == "cuda"]
+    cpu_pages = [p for p in active_pages if p.state == 'CPU' and p.device.type != "cuda"]
+
+    if device.type == "cuda" and cpu_pages:
+        _cpu_bytes = sum(p.k_tensor[:, :, :p.used_tokens, :].numel() * p.k_tensor.element_size() * 2
+                         for p in cpu_pages)
+        _record_prefetch(len(cpu_pages), _cpu_bytes)
+
+    if device.type != "cuda":
+        raise RuntimeError(
+            "perform_streaming_attention: the query must be on a HIP device; this library "
+            "implements the GPU attention path only (CPU-stage attention stays HELM's own)")
+
+    masked = attention_mask is not None or softcap is not None
+    if masked:
+        seq_pages, causal = active_pages, False
+    elif not cpu_pages:
+        seq_pages, causal = gpu_pages, query.size(2) > 1
+    else:
+        seq_pages, causal = gpu_pages + cpu_pages, False
+    if not seq_pages:
+        return torch.zeros_like(query)
+
+    first = seq_pages[0].k_tensor
+    Hkv, D, kv_dtype = first.size(1), query.size(-1), first.dtype
+    B = query.size(0)
+    seqs = []
+    for b in range(B):
+        segs = [_page_segments(p, b, B, Hkv, D, kv_dtype) for p in seq_pages]
+        if not _async_kv_prefetch_enabled():
+            segs = _stage_host_pages_sync(segs, device)
+        if B > 1 and any(sg.host for sg in segs):
+            # host pages are streamed per sequence
+            return torch.cat([
+                perform_streaming_attention(
+                    query[i:i + 1], [_batch_view(p, i) for p in pages], scale,
+                    attention_mask[i:i + 1] if attention_mask is not None and
+                    attention_mask.size(0) > 1 else attention_mask, softcap)
+                for i in range(B)], dim=0)
+        seqs.append(segs)
+    return _attend(query, seqs, Hkv, kv_dtype, scale, attention_mask, softcap, causal)
+
+
+def _batch_view(page: KVPage, i: int) -> KVPage:
+    if page.k_tensor.dim() == 4 and page.k_tensor.size(0) > 1:
+        return KVPage(page.page_id, page.layer_id, page.start_token, page.used_tokens,
+                      page.capacity_tokens, page.k_tensor[i:i + 1], page.v_tensor[i:i + 1],
+                      page.device, page.state)
+    return page

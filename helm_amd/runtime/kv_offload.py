@@ -1,0 +1,405 @@
+"""KV offload integration — drop-in for helm/runtime/kv_offload.py.
+
+Installs paged-KV attention forwards on a Hugging Face model's attention
+modules and routes every attention through the HIP paged-attention library:
+
+* decode (q_len == 1) appends the token to each batch item's paged cache and
+  runs one batched native attention call when every item is GPU-resident,
+  otherwise per-item streaming attention with host-page prefetch
+  (``_decode_batched``, kv_offload.py:86-186);
+* prefill appends the chunk to the pages; the first chunk attends over its
+  own K/V, later chunks stream over every cached page (kv_offload.py:197-227).
+
+The per-architecture differences of HELM's forwards (kv_offload.py:291-651) —
+where q/k norms apply, Gemma-2's scaling, soft-cap and sliding window — are
+captured by one traits table and a single forward builder.
+"""
+from __future__ import annotations
+
+import importlib
+import math
+from dataclasses import dataclass
+from types import MethodType
+from typing import Optional
+
+import torch
+
+from helm_amd.runtime.kv_allocator import KVAllocator
+from helm_amd.runtime.kv_cache import (KVCacheManager, _attend, _contiguous_segments,
+                                       _page_segments, perform_streaming_attention)
+
+
+# ── config (kv_offload.py:33-79) ───────────────────────────────────────────────
+@dataclass
+class KVOffloadConfig:
+    num_layers: int
+    num_kv_heads: int
+    head_dim: int
+    page_size: int = 64
+    dtype: torch.dtype = torch.float16
+    # GPU KV bytes kept hot before older pages go to host; default ~512 tokens
+    # per layer.
+    gpu_watermark_bytes: Optional[int] = None
+    # tokens of the optional pre-allocated contiguous all-GPU cache (0 = off)
+    cont_capacity: int = 0
+
+    def __post_init__(self):
+        if self.gpu_watermark_bytes is None:
+            elem = torch.tensor([], dtype=self.dtype).element_size()
+            per_token_bytes = 2 * self.num_kv_heads * self.head_dim * elem
+            self.gpu_watermark_bytes = 512 * per_token_bytes * self.num_layers
+
+    @staticmethod
+    def from_model(model, page_size: int = 64, gpu_watermark_bytes: Optional[int] = None,
+                   cont_capacity: Optional[int] = None) -> "KVOffloadConfig":
+        cfg = model.config
+        num_kv_heads = getattr(cfg, "num_key_value_heads", cfg.num_attention_heads)
+        head_dim = getattr(cfg, "head_dim", None) or (cfg.hidden_size // cfg.num_attention_heads)
+        return KVOffloadConfig(
+            num_layers=cfg.num_hidden_layers,
+            num_kv_heads=num_kv_heads,
+            head_dim=head_dim,
+            page_size=page_size,
+            dtype=next(model.parameters()).dtype,
+            gpu_watermark_bytes=gpu_watermark_bytes,
+            cont_capacity=0 if cont_capacity is None else cont_capacity,
+        )
+
+
+def _require_hip(t: torch.Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{what}: tensors must be on a HIP device (no CPU attention path)")
+
+
+# ── decode (kv_offload.py:86-186) ──────────────────────────────────────────────
+def _decode_batched(kvcms, q, k, v, layer_idx: int, scale: float,
+                    attention_mask: Optional[torch.Tensor] = None):
+    """One decode step of attention for a batch; returns [bsz, Hq, 1, D].
+
+    Contiguous-cache path when enabled and within capacity; otherwise the
+    token goes into every item's pages (residency enforced), then a single
+    batched kernel call if all items are GPU-resident (ragged lengths are
+    fine), else per-item streaming attention with host prefetch.
+    `attention_mask` is the caller's additive key mask, [bsz, *, 1, kv_len].
+    """
+    bsz = q.shape[0]
+    Hkv, D = k.shape[1], q.shape[-1]
+
+    if kvcms[0].use_contiguous:
+        if kvcms[0].cont_seq_len < kvcms[0].cont_capacity:
+            _require_hip(q, "_decode_batched")
+            for i in range(bsz):
+                kvcms[i].write_decode_contiguous(layer_idx, k[i:i + 1], v[i:i + 1])
+            views = [kvcms[i].get_kv_contiguous(layer_idx) for i in range(bsz)]
+            if layer_idx == kvcms[0].cont_num_layers - 1:
+                for kvcm in kvcms:
+                    kvcm.advance_contiguous()
+            seqs = [_contiguous_segments(K, V, 0) for K, V in views]
+            return _attend(q, seqs, Hkv, views[0][0].dtype, scale, attention_mask, None, False)
+        for kvcm in kvcms:
+            kvcm.migrate_contiguous_to_pages()
+
+    all_pages = []
+    for i in range(bsz):
+        kvcms[i].append_decode(layer_idx, k[i:i + 1], v[i:i + 1], skip_residency=False)
+        all_pages.append(kvcms[i].iterate_layer_pages(layer_idx))
+
+    if all(kvcms[i].all_gpu_resident(layer_idx) for i in range(bsz)):
+        lists = [[p for p in pages if p.used_tokens > 0] for pages in all_pages]
+        if all(lists):
+            _require_hip(q, "_decode_batched")
+            dtype = lists[0][0].k_tensor.dtype
+            seqs = [[_page_segments(p, 0, 1, Hkv, D, dtype) for p in lst] for lst in lists]
+            return _attend(q, seqs, Hkv, dtype, scale, attention_mask, None, False)
+
+    outs = [
+        perform_streaming_attention(
+            q[i:i + 1], all_pages[i], scale=scale,
+            attention_mask=attention_mask[i:i + 1] if attention_mask is not None else None)
+        for i in range(bsz)
+    ]
+    return torch.cat(outs, dim=0)
+
+
+def _cached_tokens(kvcm, layer_idx: int) -> int:
+    return sum(page.used_tokens for page in kvcm.iterate_layer_pages(layer_idx)
+               if page.used_tokens > 0 and getattr(page, "state", None) != "DEAD")
+
+
+def _append_prefill_batched(kvcms, k, v, layer_idx: int) -> list:
+    """Append a prefill chunk per item; returns each item's past length."""
+    past_lengths = []
+    for i in range(k.shape[0]):
+        past_lengths.append(_cached_tokens(kvcms[i], layer_idx))
+        kvcms[i].append_prefill(layer_idx, k[i:i + 1], v[i:i + 1])
+        if getattr(kvcms[i], "use_contiguous", False):
+            kvcms[i].prefill_contiguous(layer_idx, k[i:i + 1], v[i:i + 1])
+    return past_lengths
+
+
+def _stream_prefill_batched(kvcms, q, layer_idx: int, scale: float,
+                            attention_mask: Optional[torch.Tensor] = None,
+                            softcap: Optional[float] = None):
+    """A later prefill chunk attends over every cached page, per item."""
+    outs = []
+    for i in range(q.shape[0]):
+        item_mask = attention_mask[i:i + 1] if attention_mask is not None else None
+        outs.append(perform_streaming_attention(q[i:i + 1], kvcms[i].iterate_layer_pages(layer_idx),
+                                                scale=scale, attention_mask=item_mask,
+                                                softcap=softcap))
+    return torch.cat(outs, dim=0)
+
+
+def _local_attention(q, k, v, scale, attention_mask, softcap=None):
+    """First prefill chunk: attention over the chunk's own K/V (no pages yet),
+    the SDPA / eager call of kv_offload.py:330-338, :605-613."""
+    _require_hip(q, "prefill attention")
+    if attention_mask is not None and attention_mask.dtype == torch.bool:
+        attention_mask = torch.zeros(attention_mask.shape, dtype=torch.float32,
+                                     device=attention_mask.device).masked_fill_(
+            ~attention_mask, torch.finfo(torch.float32).min)
+    if k.stride(3) != 1 or k.stride(2) != k.size(3) or v.stride() != k.stride():
+        k, v = k.contiguous(), v.contiguous()
+    seqs = [_contiguous_segments(k, v, b) for b in range(q.shape[0])]
+    return _attend(q, seqs, k.shape[1], k.dtype, scale, attention_mask, softcap, False)
+
+
+def _apply_softcap(attn_weights: torch.Tensor, softcap: Optional[float]) -> torch.Tensor:
+    if softcap is None:
+        return attn_weights
+    return torch.tanh(attn_weights / softcap) * softcap
+
+
+def _gemma2_sliding_window_mask(attn_self, attention_mask, cache_position, key_length: int, *,
+                                device: torch.device, dtype: torch.dtype):
+    """Caller mask plus Gemma-2's per-layer sliding window
+    (kv_offload.py:240-288): key j is visible to query position i iff
+    i - window < j <= i."""
+    if attention_mask is not None:
+        query_length = attention_mask.shape[-2]
+        attention_mask = attention_mask[:, :, :query_length, :key_length]
+    elif cache_position is not None:
+        query_length = int(cache_position.numel())
+    else:
+        query_length = key_length
+
+    window = getattr(attn_self, "sliding_window", None)
+    if window is None:
+        return attention_mask
+
+    if cache_position is None:
+        qpos = torch.arange(query_length, device=device, dtype=torch.long)
+    else:
+        qpos = cache_position.to(device=device, dtype=torch.long).reshape(-1)
+        if qpos.numel() != query_length:
+            raise ValueError(
+                "Gemma2 sliding-window mask requires cache_position to match "
+                f"query length ({query_length}), got {qpos.numel()}.")
+    kpos = torch.arange(key_length, device=device, dtype=torch.long)
+    visible = (kpos[None, :] <= qpos[:, None]) & (kpos[None, :] > qpos[:, None] - window)
+    sliding = torch.full((query_length, key_length), torch.finfo(dtype).min, device=device,
+                         dtype=dtype).masked_fill_(visible, 0)[None, None]
+    return sliding if attention_mask is None else attention_mask + sliding
+
+
+# ── per-architecture forwards (kv_offload.py:291-651) ─────────────────────────
+@dataclass(frozen=True)
+class _Arch:
+    module: str        # transformers module holding the attention class
+    cls: str           # attention class name
+    rope_module: str   # module whose apply_rotary_pos_emb the forward uses
+    qk_norm: str       # "none" | "head" (norm per head, Qwen3) | "proj" (OLMo-2)
+    gemma: bool = False
+
+
+_TM = "transformers.models."
+_ARCHS = {
+    "qwen2": _Arch(_TM + "qwen2.modeling_qwen2", "Qwen2Attention", _TM + "qwen2.modeling_qwen2", "none"),
+    "qwen3": _Arch(_TM + "qwen3.modeling_qwen3", "Qwen3Attention", _TM + "qwen3.modeling_qwen3", "head"),
+    "llama": _Arch(_TM + "llama.modeling_llama", "LlamaAttention", _TM + "llama.modeling_llama", "none"),
+    "mistral": _Arch(_TM + "mistral.modeling_mistral", "MistralAttention",
+                     _TM + "llama.modeling_llama", "none"),
+    "ministral": _Arch(_TM + "ministral.modeling_ministral", "MinistralAttention",
+                       _TM + "llama.modeling_llama", "none"),
+    "olmo2": _Arch(_TM + "olmo2.modeling_olmo2", "Olmo2Attention", _TM + "olmo2.modeling_olmo2", "proj"),
+    "gemma2": _Arch(_TM + "gemma2.modeling_gemma2", "Gemma2Attention",
+                    _TM + "gemma2.modeling_gemma2", "none", gemma=True),
+}
+# name-substring resolution order of kv_offload.py:766-795 ("ministral" is
+# checked before "mistral"; "qwen3" before "qwen2")
+_RESOLVE_ORDER = ("qwen3", "qwen2", "gemma2", "ministral", "olmo2", "mistral", "llama")
+
+
+def _make_forward(kvcms, arch: _Arch):
+    """Attention forward for `arch` bound to the per-item caches `kvcms`."""
+
+    def forward(attn_self, hidden_states, position_embeddings, attention_mask=None,
+                past_key_values=None, cache_position=None, **kwargs):
+        rope = importlib.import_module(arch.rope_module).apply_rotary_pos_emb
+        bsz, q_len, _ = hidden_states.shape
+        shape = (bsz, q_len, -1, attn_self.head_dim)
+
+        q = attn_self.q_proj(hidden_states)
+        k = attn_self.k_proj(hidden_states)
+        v = attn_self.v_proj(hidden_states)
+        if arch.qk_norm == "proj":
+            q, k = attn_self.q_norm(q), attn_self.k_norm(k)
+        q, k, v = q.view(shape), k.view(shape), v.view(shape)
+        if arch.qk_norm == "head":
+            q, k = attn_self.q_norm(q), attn_self.k_norm(k)
+        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        cos, sin = position_embeddings
+        q, k = rope(q, k, cos, sin)
+
+        if arch.gemma:
+            scale = getattr(attn_self, "scaling", 1.0 / math.sqrt(attn_self.head_dim))
+            softcap = getattr(attn_self, "attn_logit_softcapping", None)
+        else:
+            scale = 1.0 / math.sqrt(attn_self.head_dim)
+            softcap = None
+        layer = attn_self.layer_idx
+
+        if q_len > 1:
+            past_lengths = _append_prefill_batched(kvcms, k, v, layer)
+            if any(past > 0 for past in past_lengths):
+                mask = attention_mask
+                if arch.gemma:
+                    key_length = max(_cached_tokens(c, layer) for c in kvcms)
+                    mask = _gemma2_sliding_window_mask(attn_self, attention_mask, cache_position,
+                                                       key_length, device=q.device, dtype=q.dtype)
+                out = _stream_prefill_batched(kvcms, q, layer, scale, mask, softcap)
+            else:
+                mask = attention_mask
+                if arch.gemma:
+                    mask = _gemma2_sliding_window_mask(attn_self, attention_mask, cache_position,
+                                                       k.shape[-2], device=q.device, dtype=q.dtype)
+                out = _local_attention(q, k, v, scale, mask, softcap)
+        elif arch.gemma:
+            outs = []
+            for i in range(bsz):
+                kvcms[i].append_decode(layer, k[i:i + 1], v[i:i + 1])
+                pages = kvcms[i].iterate_layer_pages(layer)
+                key_length = sum(p.used_tokens for p in pages
+                                 if p.used_tokens > 0 and p.state != "DEAD")
+                item_mask = (_gemma2_sliding_window_mask(
+                    attn_self, attention_mask[i:i + 1] if attention_mask is not None else None,
+                    cache_position, key_length, device=q.device, dtype=q.dtype)
+                    if key_length > 0 else None)
+                outs.append(perform_streaming_attention(q[i:i + 1], pages, scale=scale,
+                                                        attention_mask=item_mask,
+                                                        softcap=softcap))
+            out = torch.cat(outs, dim=0)
+        else:
+            out = _decode_batched(kvcms, q, k, v, layer, scale, attention_mask)
+
+        out = out.transpose(1, 2).contiguous().reshape(bsz, q_len, -1)
+        return attn_self.o_proj(out), None
+
+    return forward
+
+
+def _make_qwen2_forward(kvcms):
+    return _make_forward(kvcms, _ARCHS["qwen2"])
+
+
+def _make_qwen3_forward(kvcms):
+    return _make_forward(kvcms, _ARCHS["qwen3"])
+
+
+def _make_olmo2_forward(kvcms):
+    return _make_forward(kvcms, _ARCHS["olmo2"])
+
+
+def _make_llama_forward(kvcms):
+    return _make_forward(kvcms, _ARCHS["llama"])
+
+
+def _make_gemma2_forward(kvcms):
+    return _make_forward(kvcms, _ARCHS["gemma2"])
+
+
+# ── manager (kv_offload.py:658-831) ────────────────────────────────────────────
+class KVOffloadManager:
+    """Installs paged-KV attention forwards on one model's attention modules
+    and owns one KVCacheManager per batch item over a shared KVAllocator."""
+
+    def __init__(self, model, config: KVOffloadConfig, batch_size: int = 1):
+        self.config = config
+        self.batch_size = batch_size
+        self.allocator = KVAllocator(num_layers=config.num_layers,
+                                     num_kv_heads=config.num_kv_heads,
+                                     head_dim=config.head_dim, page_size=config.page_size,
+                                     dtype=config.dtype)
+        watermark_per_item = max(config.gpu_watermark_bytes // batch_size, 1)
+        self.kvcms = [KVCacheManager(self.allocator, gpu_high_watermark_bytes=watermark_per_item)
+                      for _ in range(batch_size)]
+        self._patched: dict = {}
+        self._patched_instance_forwards: dict = {}
+        self._apply_patches(model)
+        self.patch_module_roots(model)
+
+        if config.cont_capacity > 0:
+            device = next(model.parameters()).device
+            if device.type == "cuda":
+                built = [kvcm.build_contiguous(num_layers=config.num_layers,
+                                               num_kv_heads=config.num_kv_heads,
+                                               head_dim=config.head_dim,
+                                               capacity=config.cont_capacity, device=device,
+                                               dtype=config.dtype)
+                         for kvcm in self.kvcms]
+                if not all(built):
+                    for kvcm in self.kvcms:
+                        kvcm.drop_contiguous()
+
+    def reset(self):
+        """Clear every paged cache and re-arm the contiguous path."""
+        for kvcm in self.kvcms:
+            kvcm.clear()
+            kvcm.reset_contiguous()
+
+    def restore(self):
+        """Put the original attention forwards back."""
+        for module, had_instance_forward, original in self._patched_instance_forwards.values():
+            if had_instance_forward:
+                module.forward = original
+            else:
+                module.__dict__.pop("forward", None)
+        self._patched_instance_forwards.clear()
+        self._patched.clear()
+
+    def report(self) -> dict:
+        return self.allocator.report_usage()
+
+    def patch_module_roots(self, *roots):
+        """Bind the patched forward on every matching module instance under
+        `roots` (instances only: the class and other models stay untouched)."""
+        for root in roots:
+            if root is None:
+                continue
+            for cls, patched_forward in self._patched.values():
+                for module in root.modules():
+                    if not isinstance(module, cls):
+                        continue
+                    key = id(module)
+                    if key in self._patched_instance_forwards:
+                        continue
+                    had = "forward" in module.__dict__
+                    original = module.__dict__.get("forward")
+                    module.forward = MethodType(patched_forward, module)
+                    self._patched_instance_forwards[key] = (module, had, original)
+
+    def _apply_patches(self, model):
+        name = model.__class__.__name__.lower()
+        for arch in _RESOLVE_ORDER:
+            if arch in name:
+                self._patch(arch)
+                return
+        raise NotImplementedError(
+            f"KVOffloadManager: no attention patch for {model.__class__.__name__}")
+
+    def _patch(self, arch: str):
+        spec = _ARCHS.get(arch)
+        if spec is None:
+            raise ValueError(arch)
+        cls = getattr(importlib.import_module(spec.module), spec.cls)
+        self._patched[arch] = (cls, _make_forward(self.kvcms, spec))

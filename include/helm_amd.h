@@ -1,0 +1,185 @@
+/*
+ * helm_amd.h — C-ABI of the MI355X (gfx950) paged-KV decode-attention and
+ * cold-page offload library (libhelm_amd.so).
+ *
+ * Every entry point takes plain pointers, integers and a hipStream_t passed as
+ * `void*`.  No torch types cross this boundary.  The caller owns every buffer
+ * it passes in; the library never frees caller memory.  The only memory the
+ * library owns is held by a `helm_engine` (workspace, staging ring, pinned
+ * descriptor-upload buffers, one copy stream) and is released by
+ * helm_engine_destroy().
+ *
+ * Status convention: 0 = success; a positive value is the hipError_t that
+ * failed; a negative value is an argument/contract error (HELM_E_*).  On any
+ * non-zero status helm_last_error_string() returns a thread-local message.
+ *
+ * Element types: HELM_F16 (IEEE binary16), HELM_BF16, HELM_F32.
+ *
+ * Layouts (all row-major, innermost dimension last and contiguous):
+ *   query / out      [B, Hq, q_len, D]  (dense)
+ *   one page's K, V  [Hkv, page_tokens, D] — the [1,Hkv,page,D] tensors that
+ *                    HELM's KVPage.k_tensor / v_tensor hold.  head_stride is the
+ *                    element distance between consecutive KV heads of a page
+ *                    (= page capacity * D for a dense page).
+ *   mask             additive fp32, element (b, h, s, t) at
+ *                    mask + b*mask_bstride + h*mask_hstride + s*mask_qstride + t
+ *                    where t is the position of the key among the sequence's
+ *                    active tokens (HELM's token_cursor).
+ *
+ * GQA: query head h reads KV head h / (Hq / Hkv) (HELM repeat_interleave).
+ */
+#ifndef HELM_AMD_H
+#define HELM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HELM_AMD_ABI_VERSION 1
+
+enum helm_dtype { HELM_F16 = 0, HELM_BF16 = 1, HELM_F32 = 2 };
+
+enum helm_status {
+  HELM_OK = 0,
+  HELM_E_INVALID = -1,     /* bad argument (shape, pointer, size)          */
+  HELM_E_UNSUPPORTED = -2, /* valid request this build does not implement  */
+  HELM_E_WORKSPACE = -3,   /* caller workspace smaller than required        */
+};
+
+/* One KV page as the streaming entry point sees it.  `k`/`v` point at the
+ * page's head-0, token-0 element (device memory, or pinned host memory when
+ * HELM_PAGE_HOST is set).  `tok_off` is the position of the page's first token
+ * among the sequence's active tokens.  32 bytes. */
+typedef struct helm_page {
+  uint64_t k;
+  uint64_t v;
+  int32_t used;        /* tokens in the page (> 0)                          */
+  int32_t tok_off;     /* HELM token_cursor of the page's first token       */
+  int32_t head_stride; /* elements between KV heads inside the page         */
+  int32_t flags;       /* HELM_PAGE_HOST: page lives in pinned host memory  */
+} helm_page;
+
+#define HELM_PAGE_HOST 1
+
+/* One run of tokens appended into one page (helm_page_append).  The source
+ * holds `n_tok` tokens for every KV head: element (h, s, d) of the source K at
+ * src_k + h*src_head_stride + s*src_tok_stride + d; the destination token s
+ * lands at page row dst_tok + s. */
+typedef struct helm_append_seg {
+  uint64_t dst_k;
+  uint64_t dst_v;
+  uint64_t src_k;
+  uint64_t src_v;
+  int64_t src_head_stride; /* elements */
+  int64_t src_tok_stride;  /* elements */
+  int32_t dst_head_stride; /* elements */
+  int32_t dst_tok;
+  int32_t n_tok;
+  int32_t pad;
+} helm_append_seg;
+
+typedef struct helm_engine helm_engine;
+
+/* ---- library ------------------------------------------------------------ */
+
+/* Thread-local message for the last non-zero status on this thread. */
+const char* helm_last_error_string(void);
+int helm_abi_version(void);
+
+/* ---- engine: per-device state (copy stream, workspace, staging ring) ----- */
+
+/* Creates the per-device engine.  chunk_bytes / ring_slots size the device
+ * staging ring that cold pages are prefetched through (0 = defaults:
+ * 16 MiB x 4).  Replaces the per-device copy stream of
+ * helm/runtime/kv_cache.py:383-391 (_get_kv_copy_stream). */
+int helm_engine_create(int device, size_t chunk_bytes, int ring_slots,
+                       helm_engine** out);
+int helm_engine_destroy(helm_engine* eng);
+/* The engine's copy stream (hipStream_t). */
+void* helm_engine_copy_stream(helm_engine* eng);
+
+/* ---- attention ------------------------------------------------------------ */
+
+/* Workspace (bytes) helm_paged_decode_attn needs for this shape.  The first
+ * helm_ticket_bytes(...) bytes of the workspace are merge tickets: they must
+ * be zero before the first call and every completed call leaves them zero. */
+size_t helm_query_workspace_bytes(int B, int Hq, int Hkv, int q_len, int D,
+                                  int max_pages, int page_size,
+                                  int pages_per_split);
+
+/* Batched paged decode attention over a slot pool with an int32 page table.
+ * Replaces perform_streaming_attention (helm/runtime/kv_cache.py:405-662) and
+ * the batched all-GPU branch of _decode_batched (helm/runtime/kv_offload.py:
+ * 152-174) for the vLLM-style layout: slot s of the K pool starts at
+ * k_pool + s*slot_stride elements, the page of sequence b at position p is
+ * slot page_table[b*table_stride + p], sequence b holds seq_lens[b] tokens
+ * (device array), every page but the last is full (page_size tokens).
+ * pages_per_split <= 0 picks the split automatically; total_pages is an
+ * optional hint (sum over b of pages, 0 = unknown) for that choice.
+ * softcap <= 0 disables the tanh soft-cap; mask may be NULL. */
+int helm_paged_decode_attn(const void* q, void* out,
+                           const void* k_pool, const void* v_pool,
+                           int64_t slot_stride, int64_t head_stride,
+                           const int32_t* page_table, int table_stride,
+                           const int32_t* seq_lens,
+                           int B, int Hq, int Hkv, int q_len, int D,
+                           int page_size, int max_pages, int total_pages,
+                           float scale, float softcap,
+                           const float* mask, int64_t mask_bstride,
+                           int64_t mask_hstride, int64_t mask_qstride,
+                           int kv_dtype, int q_dtype, int pages_per_split,
+                           void* workspace, size_t ws_bytes, void* stream);
+
+/* Streaming attention over explicit page lists with mixed residency — the
+ * drop-in for perform_streaming_attention (helm/runtime/kv_cache.py:405-662),
+ * all four paths.  `pages` (host array) holds the active pages of every
+ * sequence, sequence b owning pages[seq_off[b] .. seq_off[b+1]) (host array of
+ * B+1).  Pages flagged HELM_PAGE_HOST are copied into the engine's device
+ * staging ring on the engine's copy stream with hipMemcpyAsync (runs of
+ * adjacent host pages become one copy) while attention over the device pages
+ * runs on `stream`; each staged chunk is consumed as soon as its copy event
+ * fires.  causal != 0 applies a top-left causal mask (key t visible to query
+ * row s iff t <= s), HELM's is_causal=q_len>1 of Path 1.  A sequence with no
+ * pages yields zeros.  Host pages require B == 1. */
+int helm_stream_attn(helm_engine* eng, const void* q, void* out,
+                     int B, int Hq, int Hkv, int q_len, int D,
+                     const helm_page* pages, const int32_t* seq_off,
+                     float scale, float softcap,
+                     const float* mask, int64_t mask_bstride,
+                     int64_t mask_hstride, int64_t mask_qstride, int causal,
+                     int kv_dtype, int q_dtype, void* stream);
+
+/* ---- page movement -------------------------------------------------------- */
+
+/* Writes K/V tokens into pages (device memory), one kernel launch for all
+ * segments.  Replaces the per-token / per-chunk copy_ of
+ * KVCacheManager.append_decode and append_prefill
+ * (helm/runtime/kv_cache.py:135-136, :164-165).  Bit-exact copy. */
+int helm_page_append(const helm_append_seg* segs, int n_segs, int Hkv, int D,
+                     int dtype, void* stream);
+
+/* Eviction copies: n regions of bytes[i] from device src[i] to pinned host
+ * dst[i], issued on the engine's copy stream after everything already queued
+ * on `stream`; regions adjacent on both sides are merged into one copy.  With
+ * sync != 0 the call returns after the copies completed (HELM's synchronous
+ * move_page, helm/runtime/kv_allocator.py:104-116); otherwise `stream` is made
+ * to wait for them.  Replaces KVAllocator.move_page GPU->CPU. */
+int helm_evict_pages(helm_engine* eng, int n, const uint64_t* src_dev,
+                     const uint64_t* dst_host, const uint64_t* bytes,
+                     int sync, void* stream);
+
+/* Prefetch copies: the host->device mirror of helm_evict_pages (pinned host
+ * src -> device dst).  Replaces KVAllocator.move_page CPU->GPU
+ * (helm/runtime/kv_allocator.py:95-121). */
+int helm_prefetch_pages(helm_engine* eng, int n, const uint64_t* src_host,
+                        const uint64_t* dst_dev, const uint64_t* bytes,
+                        int sync, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HELM_AMD_H */

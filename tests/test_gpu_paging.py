@@ -1,0 +1,337 @@
+"""Page append / evict / prefetch on the GPU: bit-exact data movement, HELM's
+residency semantics (checked against oracle/paging.py), and attention over
+mixed-residency pages (device + pinned host, staged through the copy ring)."""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helm_amd import _native
+from helm_amd import workloads as W
+from helm_amd.runtime import kv_cache as KC
+from helm_amd.runtime.kv_allocator import KVAllocator
+from helm_amd.runtime.kv_cache import KVCacheManager, perform_streaming_attention
+from helm_amd.runtime.kv_offload import KVOffloadConfig, KVOffloadManager, _decode_batched
+from oracle import attention as A
+from oracle.paging import AllocatorModel, CacheModel
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+CPU = torch.device("cpu")
+
+
+def _positional_kv(n, start, H=2, D=8, dtype=torch.float32, device=DEV):
+    """K[h, t, d] = (start + t) * 1000 + h * 10 + d / 16 — every element names
+    its token, head and dim exactly (bit-exact gather checks)."""
+    t = torch.arange(start, start + n, dtype=torch.float64).view(1, 1, n, 1)
+    h = torch.arange(H, dtype=torch.float64).view(1, H, 1, 1)
+    d = torch.arange(D, dtype=torch.float64).view(1, 1, 1, D)
+    k = (t * 1000 + h * 10 + d / 16).to(dtype)
+    return k.to(device), (-k).to(device)
+
+
+def _gather(mgr, lid):
+    pages = [p for p in mgr.layers[lid].pages if p.used_tokens > 0 and p.state != "DEAD"]
+    k = torch.cat([p.k_tensor[:, :, :p.used_tokens].to(CPU) for p in pages], 2)
+    v = torch.cat([p.v_tensor[:, :, :p.used_tokens].to(CPU) for p in pages], 2)
+    return k, v
+
+
+def test_append_prefill_decode_bit_exact():
+    a = KVAllocator(2, 8, 128, page_size=16, dtype=torch.bfloat16)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    g = torch.Generator(device=DEV).manual_seed(0)
+    # non-contiguous source like the projection output (transpose of [1,S,H,D])
+    src = torch.randn(1, 37, 8, 128, generator=g, device=DEV).bfloat16()
+    kp, vp = src.transpose(1, 2), (src * 2).transpose(1, 2)
+    mgr.append_prefill(0, kp, vp)
+    toks_k, toks_v = [kp.cpu()], [vp.cpu()]
+    for i in range(20):
+        kd = torch.randn(1, 8, 1, 128, generator=g, device=DEV).bfloat16()
+        vd = torch.randn(1, 8, 1, 128, generator=g, device=DEV).bfloat16()
+        mgr.append_decode(0, kd, vd)
+        toks_k.append(kd.cpu())
+        toks_v.append(vd.cpu())
+    torch.cuda.synchronize()
+    k, v = _gather(mgr, 0)
+    assert torch.equal(k, torch.cat(toks_k, 2)) and torch.equal(v, torch.cat(toks_v, 2))
+    L = mgr.layers[0]
+    assert [p.start_token for p in L.pages] == [0, 16, 32, 48]
+    # 37 prefill tokens -> pages of 16, 16, 5; 20 decode tokens fill the tail
+    # page to 16 and open a fourth page holding 9
+    assert [p.used_tokens for p in L.pages] == [16, 16, 16, 9]
+    assert L.total_tokens == 57
+
+
+def test_evict_round_trip_bit_exact_and_tail_protected():
+    """test_kv_cache.py:260-311 on pooled pages."""
+    a = KVAllocator(num_layers=2, num_kv_heads=2, head_dim=8, page_size=4, dtype=torch.float32)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    mgr.initialize_layer_caches(2)
+    k, v = _positional_kv(10, 0)
+    mgr.append_prefill(0, k, v)
+    tail = mgr.layers[0].tail_page
+    KC.reset_paging_stats()
+    mgr.evict_pages(999999)
+    s = KC.get_paging_stats()
+    assert s["evict_calls"] == 1 and s["pages_evicted"] == 2
+    assert s["bytes_evicted"] == 2 * 2 * 2 * 4 * 8 * 4
+    assert tail is mgr.layers[0].tail_page and tail.state == "GPU"
+    assert [p.state for p in mgr.layers[0].pages] == ["CPU", "CPU", "GPU"]
+    assert all(p.k_tensor.is_pinned() for p in mgr.layers[0].pages[:2])
+    gk, gv = _gather(mgr, 0)
+    assert torch.equal(gk, k.cpu()) and torch.equal(gv, v.cpu())
+
+
+def test_move_page_cpu_to_gpu_and_back():
+    """test_kv_allocator.py:175-220 KATs (7.0 / 8.0) plus the DEAD transition."""
+    a = KVAllocator(num_layers=2, num_kv_heads=2, head_dim=8, page_size=4, dtype=torch.float32)
+    page = a.allocate(CPU)
+    page.layer_id, page.start_token, page.used_tokens = 2, 8, 3
+    page.k_tensor[:, :, :3, :] = 7.0
+    page.v_tensor[:, :, :3, :] = 8.0
+    free_before = len(a.cpu_free_pool)
+    new = a.move_page(page, DEV)
+    assert len(a.cpu_free_pool) == free_before + 1
+    assert new.device.type == "cuda" and (new.layer_id, new.start_token, new.used_tokens) == (2, 8, 3)
+    assert torch.all(new.k_tensor[:, :, :3].cpu() == 7.0) and torch.all(new.v_tensor[:, :, :3].cpu() == 8.0)
+    gpu_before = a.gpu_total_pages
+    back = a.move_page(new, CPU)
+    assert new.state == "DEAD" and new.k_tensor.numel() == 0 and a.gpu_total_pages == gpu_before - 1
+    assert torch.all(back.k_tensor[:, :, :3] == 7.0)
+    empty = a.allocate(CPU)
+    moved = a.move_page(empty, DEV)
+    assert moved.used_tokens == 0 and moved.device.type == "cuda"
+
+
+def test_copy_stream_memoized():
+    s1 = KC._get_kv_copy_stream(DEV)
+    s2 = KC._get_kv_copy_stream(DEV)
+    assert s1 is s2 and s1.device == DEV
+
+
+@pytest.mark.parametrize("watermark_pages", [0, 1, 3])
+def test_residency_matches_paging_model(watermark_pages):
+    """A mixed prefill/decode run over 3 layers with a small watermark:
+    page ids, start tokens, fill, states, eviction counters and every byte
+    of every page agree with the paging model."""
+    H, D, P = 2, 8, 4
+    page_bytes = 2 * H * P * D * 4
+    wm = watermark_pages * page_bytes
+    a = KVAllocator(3, H, D, page_size=P, dtype=torch.float32)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=wm)
+    model = CacheModel(AllocatorModel(P, page_bytes), wm)
+    KC.reset_paging_stats()
+    rng = np.random.default_rng(watermark_pages)
+    totals = [0, 0, 0]
+    for step in range(40):
+        lid = int(rng.integers(0, 3))
+        if rng.random() < 0.25:
+            n = int(rng.integers(1, 11))
+            mgr.append_prefill(lid, *_positional_kv(n, totals[lid], H, D))
+            model.append_prefill(lid, n)
+            totals[lid] += n
+        else:
+            mgr.append_decode(lid, *_positional_kv(1, totals[lid], H, D))
+            model.append_decode(lid)
+            totals[lid] += 1
+    torch.cuda.synchronize()
+    for lid in range(3):
+        if lid not in model.layers:
+            continue
+        got = [(p.page_id, p.start_token, p.used_tokens, p.state) for p in mgr.layers[lid].pages]
+        ref = [(p.page_id, p.start_token, p.used_tokens, p.state) for p in model.layers[lid].pages]
+        assert got == ref
+        k, v = _gather(mgr, lid)
+        pos = torch.from_numpy(model.gathered(lid))
+        ek, ev = _positional_kv(len(pos), 0, H, D, device=CPU)
+        assert torch.equal(k, ek[:, :, pos]) and torch.equal(v, ev[:, :, pos])
+    s = KC.get_paging_stats()
+    assert (s["evict_calls"], s["pages_evicted"], s["bytes_evicted"]) == (
+        model.stats["evict_calls"], model.stats["pages_evicted"], model.stats["bytes_evicted"])
+    assert a.report_usage() == model.alloc.report_usage()
+
+
+@pytest.mark.parametrize("dtype,H,kvh", [(torch.bfloat16, 32, 8), (torch.float16, 40, 40),
+                                        (torch.float32, 4, 2)])
+def test_mixed_residency_attention(dtype, H, kvh):
+    """Attention after evicting the oldest pages equals the fp64 oracle over
+    the same tokens; the prefetch counters record the host pages."""
+    D, P, T = 128, 16, 700
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=dtype)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    g = torch.Generator(device=DEV).manual_seed(1)
+    k = torch.randn(1, kvh, T, D, generator=g, device=DEV).to(dtype)
+    v = torch.randn(1, kvh, T, D, generator=g, device=DEV).to(dtype)
+    mgr.append_prefill(0, k, v)
+    q = torch.randn(1, H, 1, D, generator=g, device=DEV).to(dtype)
+    full = perform_streaming_attention(q, mgr.iterate_layer_pages(0))
+    page_bytes = 2 * kvh * P * D * k.element_size()
+    mgr.evict_pages(20 * page_bytes)
+    pages = mgr.iterate_layer_pages(0)
+    n_cpu = sum(p.state == "CPU" for p in pages)
+    assert n_cpu == 20
+    KC.reset_paging_stats()
+    mask = torch.zeros(1, 1, 1, T, device=DEV)
+    mixed = perform_streaming_attention(q, pages, attention_mask=mask)
+    unmasked = perform_streaming_attention(q, pages)
+    s = KC.get_paging_stats()
+    assert s["prefetch_calls"] == 2 and s["pages_prefetched"] == 40
+    per_call = 20 * kvh * P * D * k.element_size() * 2      # K + V of 20 full pages
+    assert s["bytes_prefetched"] == 2 * per_call
+    ref = A.attention_fp64_batched(q[0].cpu(), k[0].cpu(), v[0].cpu())
+    tol = {torch.bfloat16: 1e-2, torch.float16: 2e-3, torch.float32: 1e-5}[dtype]
+    for out in (full, mixed, unmasked):
+        assert (out[0].double().cpu() - ref).abs().max().item() <= tol
+
+
+def _ring_engine(chunk, slots):
+    lib = _native.load()
+    h = ctypes.c_void_p()
+    _native.call("helm_engine_create", 0, chunk, slots, ctypes.byref(h))
+    return lib, h
+
+
+def test_staging_ring_reuse_many_chunks():
+    """More staged chunks than ring slots: every slot is reused several times
+    in one call and across calls; results stay exact to the oracle."""
+    w = W.Workload("t", 1, 32, 8, 128, torch.bfloat16, T=4096)
+    n_pages = 256
+    pool_h = torch.randn(n_pages, 2, 8, 16, 128, generator=torch.Generator().manual_seed(2)
+                         ).bfloat16().pin_memory()
+    dev_pool = torch.randn(64, 2, 8, 16, 128, device=DEV).bfloat16()
+    q = torch.randn(1, 32, 1, 128, device=DEV).bfloat16()
+    es = 2
+    slot_b = 2 * 8 * 16 * 128 * es
+    pages = np.zeros(n_pages + 64, dtype=_native.PAGE_DTYPE)
+    order = np.random.default_rng(0).permutation(n_pages + 64)  # token order mixes tiers
+    for j, idx in enumerate(order):
+        if idx < n_pages:
+            base = pool_h.data_ptr() + int(idx) * slot_b
+            pages[j] = (base, base + slot_b // 2, 16, 16 * j, 16 * 128, _native.HELM_PAGE_HOST)
+        else:
+            base = dev_pool.data_ptr() + int(idx - n_pages) * slot_b
+            pages[j] = (base, base + slot_b // 2, 16, 16 * j, 16 * 128, 0)
+    seq_off = np.array([0, len(pages)], dtype=np.int32)
+    lib, eng = _ring_engine(1 << 20, 2)          # 1 MiB chunks (16 pages), 2 slots
+    try:
+        outs = []
+        for _ in range(3):
+            out = torch.empty_like(q)
+            _native.call("helm_stream_attn", eng, q.data_ptr(), out.data_ptr(), 1, 32, 8, 1, 128,
+                         _native.ptr(pages), _native.ptr(seq_off), 1 / math.sqrt(128), 0.0, None,
+                         0, 0, 0, 0, _native.HELM_BF16, _native.HELM_BF16,
+                         torch.cuda.current_stream().cuda_stream)
+            outs.append(out)
+        torch.cuda.synchronize()
+    finally:
+        lib.helm_engine_destroy(eng)
+    K = torch.empty(8, 16 * len(pages), 128)
+    V = torch.empty(8, 16 * len(pages), 128)
+    for j, idx in enumerate(order):
+        src = pool_h[idx] if idx < n_pages else dev_pool[idx - n_pages].cpu()
+        K[:, 16 * j:16 * j + 16] = src[0].float()
+        V[:, 16 * j:16 * j + 16] = src[1].float()
+    ref = A.attention_fp64_batched(q[0].cpu(), K, V)
+    for out in outs:
+        assert (out[0].double().cpu() - ref).abs().max().item() <= 1e-2
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+
+
+def test_decode_batched_poison_pad_on_gpu():
+    """test_kv_offload.py:168-245 on the GPU path."""
+    torch.manual_seed(0)
+    q = torch.randn(1, 1, 1, 4)
+    real_k, real_v = torch.randn(1, 1, 3, 4), torch.randn(1, 1, 3, 4)
+    pad_k = q.expand(1, 1, 2, 4) * 50.0
+    pad_v = torch.full((1, 1, 2, 4), 1000.0)
+    k_dec, v_dec = torch.randn(1, 1, 1, 4), torch.randn(1, 1, 1, 4)
+    a = KVAllocator(1, 1, 4, page_size=8, dtype=torch.float32)
+    for masked in (True, False):
+        kvcm = KVCacheManager(a, gpu_high_watermark_bytes=0)
+        kvcm.append_prefill(0, torch.cat([real_k, pad_k], 2).to(DEV),
+                            torch.cat([real_v, pad_v], 2).to(DEV))
+        mask = torch.zeros(1, 1, 1, 6)
+        mask[..., 3:5] = float("-inf")
+        out = _decode_batched([kvcm], q.to(DEV), k_dec.to(DEV), v_dec.to(DEV), 0, 1.0,
+                              attention_mask=mask.to(DEV) if masked else None)
+        exp = torch.nn.functional.scaled_dot_product_attention(
+            q, torch.cat([real_k, k_dec], 2), torch.cat([real_v, v_dec], 2), scale=1.0)
+        close = torch.allclose(out.cpu(), exp, atol=1e-4)
+        assert close if masked else not close
+        kvcm.clear()
+
+
+def test_decode_batched_ragged_batch_and_offload():
+    """Batched decode over per-item managers with ragged lengths (one kernel
+    call) and with evicted pages (per-item streaming) agree with the oracle."""
+    H, kvh, D = 8, 2, 64
+    a = KVAllocator(1, kvh, D, page_size=16, dtype=torch.float16)
+    g = torch.Generator().manual_seed(3)
+    lens = [40, 75, 16]
+    for evict in (False, True):
+        kvcms = [KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12) for _ in lens]
+        ks, vs = [], []
+        for m, n in zip(kvcms, lens):
+            k = torch.randn(1, kvh, n, D, generator=g).half()
+            v = torch.randn(1, kvh, n, D, generator=g).half()
+            m.append_prefill(0, k.to(DEV), v.to(DEV))
+            ks.append(k)
+            vs.append(v)
+            if evict:
+                m.evict_pages(10 ** 9)
+        q = torch.randn(3, H, 1, D, generator=g).half()
+        kd = torch.randn(3, kvh, 1, D, generator=g).half()
+        vd = torch.randn(3, kvh, 1, D, generator=g).half()
+        out = _decode_batched(kvcms, q.to(DEV), kd.to(DEV), vd.to(DEV), 0, 1 / math.sqrt(D))
+        for i in range(3):
+            K = torch.cat([ks[i], kd[i:i + 1]], 2)[0].float()
+            V = torch.cat([vs[i], vd[i:i + 1]], 2)[0].float()
+            ref = A.attention_fp64_batched(q[i].float(), K, V)
+            assert (out[i].double().cpu() - ref).abs().max().item() <= 2e-3
+        for m in kvcms:
+            m.clear()
+
+
+def test_tiny_llama_greedy_matches_hf_with_eviction():
+    """test_kv_eviction_e2e.py:10-66 pattern: a tiny random Llama generates the
+    same greedy tokens through the paged, evicting cache as HF's own
+    full-recompute forward."""
+    from transformers.models.llama import LlamaConfig, LlamaForCausalLM
+    torch.manual_seed(0)
+    cfg = LlamaConfig(vocab_size=97, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=256)
+    cfg._attn_implementation = "eager"
+    ref_model = LlamaForCausalLM(cfg).eval().to(DEV)
+    model = LlamaForCausalLM(cfg).eval().to(DEV)
+    model.load_state_dict(ref_model.state_dict())
+    conf = KVOffloadConfig.from_model(model, page_size=16, gpu_watermark_bytes=1024)
+    mgr = KVOffloadManager(model, conf, batch_size=1)
+    prompt = torch.randint(0, 97, (1, 12), generator=torch.Generator().manual_seed(1)).to(DEV)
+    steps = 40
+    with torch.no_grad():
+        ids = prompt.clone()
+        for _ in range(steps):
+            nxt = ref_model(ids, use_cache=False).logits[:, -1].argmax(-1, keepdim=True)
+            ids = torch.cat([ids, nxt], 1)
+        ref_tokens = ids[0, prompt.shape[1]:].tolist()
+
+        KC.reset_paging_stats()
+        S = prompt.shape[1]
+        logits = model(prompt, position_ids=torch.arange(S, device=DEV)[None],
+                       use_cache=False).logits
+        out_tokens = []
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        for t in range(steps):
+            out_tokens.append(int(tok))
+            pos = S + t
+            mask = torch.zeros(1, 1, 1, pos + 1, device=DEV)
+            logits = model(tok, position_ids=torch.tensor([[pos]], device=DEV),
+                           attention_mask=None, use_cache=False,
+                           cache_position=torch.tensor([pos], device=DEV)).logits
+            tok = logits[:, -1].argmax(-1, keepdim=True)
+    mgr.restore()
+    assert out_tokens == ref_tokens
+    assert KC.get_paging_stats()["pages_evicted"] > 0

@@ -1,0 +1,247 @@
+"""Host bookkeeping of helm_amd.runtime with host (CPU) pages — no GPU work.
+
+Mirrors the CPU tests HELM holds for these classes
+(tests/unit/runtime/test_kv_allocator.py, test_kv_cache.py,
+test_batch_kv_offload.py) and cross-checks page metadata against the paging
+model in oracle/paging.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+from helm_amd.runtime import kv_cache as KC
+from helm_amd.runtime.kv_allocator import KVAllocator
+from helm_amd.runtime.kv_cache import KVCacheManager, LayerKVCache
+from helm_amd.runtime.kv_offload import KVOffloadConfig
+from oracle.paging import AllocatorModel, CacheModel
+
+CPU = torch.device("cpu")
+NUM_HEADS, HEAD_DIM, PAGE_SIZE, NUM_LAYERS = 2, 8, 4, 4
+
+
+@pytest.fixture()
+def allocator():
+    return KVAllocator(num_layers=NUM_LAYERS, num_kv_heads=NUM_HEADS, head_dim=HEAD_DIM,
+                       page_size=PAGE_SIZE, dtype=torch.float32)
+
+
+@pytest.fixture()
+def cache(allocator):
+    mgr = KVCacheManager(allocator, gpu_high_watermark_bytes=0)
+    mgr.initialize_layer_caches(num_layers=NUM_LAYERS)
+    return mgr
+
+
+def _kv(n, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(1, NUM_HEADS, n, HEAD_DIM, generator=g),
+            torch.randn(1, NUM_HEADS, n, HEAD_DIM, generator=g))
+
+
+# ── allocator (test_kv_allocator.py) ──────────────────────────────────────────
+def test_allocate_state_and_reserve(allocator):
+    page = allocator.allocate(CPU)
+    assert page.state == "CPU" and page.device.type == "cpu"
+    assert allocator.cpu_total_pages == 16 and len(allocator.cpu_free_pool) == 15
+
+
+def test_allocate_resets_metadata_and_lifo(allocator):
+    p = allocator.allocate(CPU)
+    p.layer_id, p.start_token, p.used_tokens = 99, 500, 3
+    allocator.free(p)
+    assert p.state == "FREE"
+    p2 = allocator.allocate(CPU)
+    assert p2 is p
+    assert (p2.layer_id, p2.start_token, p2.used_tokens) == (-1, 0, 0)
+
+
+def test_page_shape_dtype_and_ids():
+    a = KVAllocator(num_layers=2, num_kv_heads=3, head_dim=16, page_size=8, dtype=torch.float16)
+    p0, p1 = a.allocate(CPU), a.allocate(CPU)
+    assert p0.k_tensor.shape == (1, 3, 8, 16) and p0.v_tensor.shape == (1, 3, 8, 16)
+    assert p0.k_tensor.dtype == torch.float16
+    assert p0.page_id != p1.page_id
+    # K and V of a page are adjacent halves of one arena slot
+    es = p0.k_tensor.element_size()
+    assert p0.v_tensor.data_ptr() - p0.k_tensor.data_ptr() == 3 * 8 * 16 * es
+
+
+def test_reserve_batch_accumulates(allocator):
+    allocator.reserve_batch(3, CPU)
+    allocator.reserve_batch(4, CPU)
+    assert allocator.cpu_total_pages == 7 and len(allocator.cpu_free_pool) == 7
+
+
+def test_move_page_same_device_and_data(allocator):
+    page = allocator.allocate(CPU)
+    page.used_tokens = 2
+    page.k_tensor[:, :, :2, :] = 42.0
+    page.v_tensor[:, :, :2, :] = 99.0
+    res = allocator.move_page(page, CPU)
+    assert res is page
+    assert torch.all(res.k_tensor[:, :, :2, :] == 42.0)
+    assert torch.all(res.v_tensor[:, :, :2, :] == 99.0)
+
+
+def test_report_usage_matches_model(allocator):
+    model = AllocatorModel(PAGE_SIZE, 2 * NUM_HEADS * PAGE_SIZE * HEAD_DIM * 4)
+    for _ in range(5):
+        allocator.allocate(CPU)
+        model.allocate("cpu")
+    assert allocator.report_usage() == model.report_usage()
+
+
+# ── cache manager (test_kv_cache.py CPU part) ─────────────────────────────────
+def test_layer_cache_tail(allocator):
+    layer = LayerKVCache(0)
+    p1, p2 = allocator.allocate(CPU), allocator.allocate(CPU)
+    layer.append_page(p1)
+    layer.append_page(p2)
+    assert layer.tail_page is p2 and len(layer.pages) == 2
+
+
+@pytest.mark.parametrize("n,pages", [(3, 1), (4, 1), (9, 3), (8, 2)])
+def test_prefill_pages_and_start_tokens(cache, n, pages):
+    k, v = _kv(n)
+    cache.append_prefill(0, k, v)
+    L = cache.layers[0]
+    assert len(L.pages) == pages and L.total_tokens == n
+    assert [p.start_token for p in L.pages] == list(range(0, n, PAGE_SIZE))
+    got_k = torch.cat([p.k_tensor[:, :, :p.used_tokens] for p in L.pages], 2)
+    got_v = torch.cat([p.v_tensor[:, :, :p.used_tokens] for p in L.pages], 2)
+    assert torch.equal(got_k, k) and torch.equal(got_v, v)
+
+
+def test_decode_tail_growth(cache):
+    k, v = _kv(PAGE_SIZE)
+    cache.append_prefill(0, k, v)
+    kd, vd = _kv(1, seed=1)
+    cache.append_decode(0, kd, vd)
+    assert len(cache.layers[0].pages) == 2 and cache.layers[0].tail_page.used_tokens == 1
+    assert torch.equal(cache.layers[0].tail_page.k_tensor[:, :, :1], kd)
+    for i in range(PAGE_SIZE + 2):
+        cache.append_decode(1, *_kv(1, seed=10 + i))
+    assert len(cache.layers[1].pages) == 2 and cache.layers[1].total_tokens == PAGE_SIZE + 2
+    assert cache.seq_len() == PAGE_SIZE + 1
+
+
+def test_auto_create_layer_and_iterate(cache):
+    del cache.layers[3]
+    cache.append_prefill(3, *_kv(2))
+    assert 3 in cache.layers
+    assert isinstance(cache.iterate_layer_pages(3), list)
+    assert cache.iterate_layer_pages(99) == []
+
+
+def test_clear_returns_pages(cache):
+    alloc = cache.allocator
+    cache.append_prefill(0, *_kv(PAGE_SIZE))
+    before = len(alloc.cpu_free_pool)
+    cache.clear()
+    assert len(alloc.cpu_free_pool) > before
+    assert cache.num_layers() == 0 and cache.seq_len() == 0
+
+
+def test_report_bytes_and_cpu_eviction_noop(cache):
+    cache.append_prefill(0, *_kv(8))
+    cache.evict_pages(99999)       # no GPU pages -> nothing moves
+    r = cache.report_bytes_per_tier()
+    assert r["gpu_active_bytes"] == 0
+    assert r["cpu_active_bytes"] == 2 * 2 * NUM_HEADS * PAGE_SIZE * HEAD_DIM * 4
+
+
+def test_metadata_matches_paging_model(allocator):
+    mgr = KVCacheManager(allocator, gpu_high_watermark_bytes=0)
+    model = CacheModel(AllocatorModel(PAGE_SIZE, 2 * NUM_HEADS * PAGE_SIZE * HEAD_DIM * 4), 0)
+    ops = [("p", 0, 9), ("d", 0), ("d", 0), ("p", 1, 3), ("d", 1), ("d", 0), ("d", 0), ("d", 0)]
+    for op in ops:
+        if op[0] == "p":
+            mgr.append_prefill(op[1], *_kv(op[2]))
+            model.append_prefill(op[1], op[2], device="cpu")
+        else:
+            mgr.append_decode(op[1], *_kv(1))
+            model.append_decode(op[1], device="cpu")
+    for lid in (0, 1):
+        got = [(p.page_id, p.start_token, p.used_tokens, p.state) for p in mgr.layers[lid].pages]
+        ref = [(p.page_id, p.start_token, p.used_tokens, p.state) for p in model.layers[lid].pages]
+        assert got == ref
+
+
+def test_build_contiguous_small_capacities():
+    for cap in (64, 640, 768, 2048):
+        a = KVAllocator(num_layers=2, num_kv_heads=2, head_dim=8, page_size=4, dtype=torch.float32)
+        m = KVCacheManager(a, gpu_high_watermark_bytes=0)
+        assert m.build_contiguous(2, 2, 8, cap, CPU, torch.float32)
+        assert m.use_contiguous and m.cont_capacity == cap
+        assert m.cont_K[0].shape == (1, 2, cap, 8)
+
+
+def test_build_contiguous_halves_on_oom(monkeypatch):
+    # kv_cache.py:277-299: on allocation failure the capacity halves down to
+    # a floor of min(capacity, 1024)
+    real = torch.zeros
+    tried = []
+
+    def flaky(*shape, **kw):
+        tried.append(shape[2])
+        if shape[2] > 1024:
+            raise RuntimeError("out of memory")
+        return real(*shape, **kw)
+
+    a = KVAllocator(num_layers=1, num_kv_heads=2, head_dim=8, page_size=4, dtype=torch.float32)
+    m = KVCacheManager(a)
+    monkeypatch.setattr(torch, "zeros", flaky)
+    assert m.build_contiguous(1, 2, 8, 4096, CPU, torch.float32)
+    assert m.cont_capacity == 1024 and tried[0] == 4096 and 2048 in tried
+    monkeypatch.setattr(torch, "zeros", lambda *s, **k: (_ for _ in ()).throw(RuntimeError("oom")))
+    assert not m.build_contiguous(1, 2, 8, 4096, CPU, torch.float32)
+    assert not m.use_contiguous
+
+
+# ── counters (test_kv_cache.py:321-361) ───────────────────────────────────────
+ZERO = {"evict_calls": 0, "pages_evicted": 0, "bytes_evicted": 0,
+        "prefetch_calls": 0, "pages_prefetched": 0, "bytes_prefetched": 0}
+
+
+def test_paging_counters():
+    KC.reset_paging_stats()
+    assert KC.get_paging_stats() == ZERO
+    KC._record_eviction(2, 1000)
+    KC._record_eviction(3, 1500)
+    KC._record_prefetch(4, 4096)
+    KC._record_eviction(0, 0)
+    KC._record_prefetch(0, 0)
+    s = KC.get_paging_stats()
+    assert (s["evict_calls"], s["pages_evicted"], s["bytes_evicted"]) == (2, 5, 2500)
+    assert (s["prefetch_calls"], s["pages_prefetched"], s["bytes_prefetched"]) == (1, 4, 4096)
+
+
+def test_cpu_query_has_no_fallback():
+    q = torch.randn(1, 2, 1, 8)
+    page = KC.KVPage(0, 0, 0, 4, 4, torch.randn(1, 2, 4, 8), torch.randn(1, 2, 4, 8), CPU, "CPU")
+    with pytest.raises(RuntimeError, match="HIP device"):
+        KC.perform_streaming_attention(q, [page])
+    # no active pages -> zeros, as HELM
+    assert torch.all(KC.perform_streaming_attention(q, []) == 0)
+
+
+# ── batch managers (test_batch_kv_offload.py) ─────────────────────────────────
+def test_batch_managers_independent(allocator):
+    kvcms = [KVCacheManager(allocator, gpu_high_watermark_bytes=0) for _ in range(3)]
+    kvcms[0].append_prefill(0, *_kv(4))
+    kvcms[1].append_prefill(0, *_kv(8))
+    assert 0 not in kvcms[2].layers
+    assert kvcms[0].layers[0].total_tokens == 4 and kvcms[1].layers[0].total_tokens == 8
+    kvcms[1].append_decode(0, *_kv(1))
+    assert kvcms[1].layers[0].total_tokens == 9
+    used = allocator.report_usage()["active_cpu_pages"]
+    assert used > 0
+    for m in kvcms:
+        m.clear()
+    assert allocator.report_usage()["active_cpu_pages"] == 0
+
+
+def test_offload_config_defaults():
+    cfg = KVOffloadConfig(num_layers=36, num_kv_heads=8, head_dim=128, dtype=torch.bfloat16)
+    assert cfg.page_size == 64 and cfg.cont_capacity == 0
+    assert cfg.gpu_watermark_bytes == 512 * 2 * 8 * 128 * 2 * 36
