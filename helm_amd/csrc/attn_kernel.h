@@ -38,6 +38,9 @@ constexpr int kWaves = 4;
 constexpr int kRowLanes = 16;   // lanes per token row (one DPP row)
 constexpr int kBlockTok = 16;   // tokens per wave block (4 rows x 4 j)
 constexpr int kMaxPps = 256;    // pages per split held in LDS
+constexpr int kMaxSplits = 256; // splits per (sequence, head, tile) merged
+constexpr int kMergeBatch = 16; // independent partial loads in flight per thread
+constexpr float kRescaleSlack = 8.f;  // lazy online-softmax rescale threshold
 
 // ---- element types ----------------------------------------------------------
 struct f16_t { uint16_t x; };
@@ -118,6 +121,76 @@ __device__ __forceinline__ Raw<EPL * ElemBytes<T>::v> load_elems(
   return r;
 }
 
+// ---- buffer loads (SGPR resource + VGPR offset) ----------------------------
+// Raw (untyped) buffer resource word 3 for CDNA: 32-bit data format.
+constexpr int kBufFlags = 0x00020000;
+
+__device__ __forceinline__ uint64_t uniform64(uint64_t x) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(x >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// clamp(x, lo, hi) on the scalar ALU.  Written out so the compiler cannot
+// fold it into a VALU med3 whose VGPR temporary may alias the destination of
+// a load still in flight (which would force a full vmcnt(0) wait).
+__device__ __forceinline__ int sclamp(int x, int lo, int hi) {
+  int r;
+  asm volatile("s_max_i32 %0, %1, %2\n\ts_min_i32 %0, %0, %3"
+               : "=&s"(r)
+               : "s"(x), "s"(lo), "s"(hi)
+               : "scc");
+  return r;
+}
+
+// Resource over [base, base + bytes); loads past `bytes` return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes,
+                                           kBufFlags);
+}
+
+template <int NB>
+__device__ __forceinline__ Raw<NB> buf_load(__amdgpu_buffer_rsrc_t r, int off) {
+  Raw<NB> out;
+  if constexpr (NB % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < NB / 16; ++i) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
+      out.w[4 * i + 0] = v[0]; out.w[4 * i + 1] = v[1];
+      out.w[4 * i + 2] = v[2]; out.w[4 * i + 3] = v[3];
+    }
+  } else if constexpr (NB == 8) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    out.w[0] = v[0]; out.w[1] = v[1];
+  } else if constexpr (NB == 4) {
+    out.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  } else {
+    static_assert(NB == 2, "unsupported raw width");
+    out.w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
+  return out;
+}
+
+// Element-wise buffer loads of the first n_valid elements (any D).
+template <typename T, int EPL>
+__device__ __forceinline__ Raw<EPL * ElemBytes<T>::v> buf_load_elems(
+    __amdgpu_buffer_rsrc_t r, int off, int n_valid) {
+  constexpr int EB = ElemBytes<T>::v;
+  Raw<EPL * EB> out = zero_raw<EPL * EB>();
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    if (e < n_valid) {
+      if constexpr (EB == 4) {
+        out.w[e] = __builtin_amdgcn_raw_buffer_load_b32(r, off + 4 * e, 0, 0);
+      } else {
+        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(r, off + 2 * e, 0, 0);
+        out.w[e >> 1] |= (e & 1) ? (h << 16) : h;
+      }
+    }
+  }
+  return out;
+}
+
 template <typename T>
 __device__ __forceinline__ void store_elem(char* p, float v);
 template <>
@@ -165,10 +238,12 @@ __device__ __forceinline__ float dot2<f16_t>(uint32_t a, uint32_t b,
 // ---- DPP row (16-lane) sum -------------------------------------------------
 // quad_perm[1,0,3,2], quad_perm[2,3,0,1], row_half_mirror, row_mirror: after
 // the four steps every lane of the row holds the same (commutative) sum.
+// update_dpp with old = 0 and bound_ctrl lets the compiler fold the move
+// into the following add (v_add_f32_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {
   return __int_as_float(
-      __builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xf, 0xf, false));
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, true));
 }
 __device__ __forceinline__ float row_sum16(float x) {
   x += dpp_mov<0xB1>(x);
@@ -178,8 +253,50 @@ __device__ __forceinline__ float row_sum16(float x) {
   return x;
 }
 
+// ---- agent-scope (cross-XCD coherent) partial-result accesses -------------
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent_ml(float* p, float m, float l) {
+  const unsigned long long u = (unsigned long long)__float_as_uint(m) |
+                               ((unsigned long long)__float_as_uint(l) << 32);
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), u,
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 ld_agent_ml(const float2* p) {
+  const unsigned long long u =
+      __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p),
+                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((unsigned)u),
+                     __uint_as_float((unsigned)(u >> 32)));
+}
+__device__ __forceinline__ float4 ld_agent4(const float* p) {
+  const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
+  const unsigned long long a =
+      __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b =
+      __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float4(__uint_as_float((unsigned)a), __uint_as_float((unsigned)(a >> 32)),
+                     __uint_as_float((unsigned)b), __uint_as_float((unsigned)(b >> 32)));
+}
+
 // exp(x) for x <= 0 or -inf (returns 0 for -inf).
 __device__ __forceinline__ float fexp(float x) { return __expf(x); }
+
+// Load through the constant address space: a wave-uniform address becomes a
+// scalar (SMEM) load whose wait never involves the vector loads in flight.
+template <typename T>
+__device__ __forceinline__ T sload(const T* p) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef const __attribute__((address_space(4))) T ConstT;
+  return *(ConstT*)(reinterpret_cast<uintptr_t>(p));
+#else
+  return *p;  // host pass only parses device code
+#endif
+}
 
 // ---- page sources -----------------------------------------------------------
 struct PageView {
@@ -203,12 +320,12 @@ struct PoolSrc {
   int max_pages;  // table columns the caller declared; bounds every walk
 
   __device__ __forceinline__ int n_pages(int b) const {
-    const int T = seq_lens[b];
+    const int T = sload(seq_lens + b);
     return T > 0 ? min((T + page_size - 1) / page_size, max_pages) : 0;
   }
   __device__ __forceinline__ PageView page(int b, int p, int hk) const {
-    const int slot = table[(int64_t)b * table_stride + p];
-    const int T = seq_lens[b];
+    const int slot = sload(table + (int64_t)b * table_stride + p);
+    const int T = sload(seq_lens + b);
     PageView pv;
     const int64_t off = (int64_t)slot * slot_stride_b + hk * head_stride_b;
     pv.k = k_pool + off;
@@ -228,10 +345,10 @@ struct DescSrc {
   int elem_bytes;
 
   __device__ __forceinline__ int n_pages(int b) const {
-    return seq_off[b + 1] - seq_off[b];
+    return sload(seq_off + b + 1) - sload(seq_off + b);
   }
   __device__ __forceinline__ PageView page(int b, int p, int hk) const {
-    const helm_page d = pages[seq_off[b] + p];
+    const helm_page d = sload(pages + sload(seq_off + b) + p);
     PageView pv;
     const int64_t off = (int64_t)hk * d.head_stride * elem_bytes;
     pv.k = reinterpret_cast<const char*>(d.k) + off;
@@ -270,13 +387,12 @@ struct AttnParams {
 // Per-workgroup LDS.
 template <int GM, int DMAX>
 struct Smem {
-  const char* pk[kMaxPps];
-  const char* pv[kMaxPps];
-  int used[kMaxPps];
-  int tok_off[kMaxPps];
   float o[kWaves][GM][DMAX];
   float m[kWaves][GM];
   float l[kWaves][GM];
+  // final merge: per-thread partial results of the split subsets
+  float4 red[kThreads];
+  float2 redml[kThreads];
   int last;
 };
 
@@ -292,7 +408,8 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
   __shared__ Smem<GM, DMAX> sm;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  // wave index made scalar so block indices / page bases live in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int row = lane >> 4;
   const int col = lane & 15;
@@ -335,15 +452,6 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
   const int pg0 = lo + split_local * p.pps;
   const int pg1 = min(pg0 + p.pps, hi);
   const int npg = pg1 - pg0;
-
-  // ---- page addresses of the split into LDS --------------------------------
-  for (int i = tid; i < npg; i += kThreads) {
-    PageView pv = src.page(b, pg0 + i, hk);
-    sm.pk[i] = pv.k;
-    sm.pv[i] = pv.v;
-    sm.used[i] = pv.used;
-    sm.tok_off[i] = pv.tok_off;
-  }
 
   // ---- query rows into registers -------------------------------------------
   const int d0 = col * EPL;
@@ -392,37 +500,71 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
   const int64_t row_bytes = (int64_t)D * EB;
   const int nblk = npg * p.bpp;
 
-  auto load_block = [&](int bi, Raw<NB> (&kr)[4], Raw<NB> (&vr)[4]) {
-    const int pi = bi / p.bpp;
-    const int sub = bi - pi * p.bpp;
-    const int used = sm.used[pi];
-    const char* kb = sm.pk[pi];
-    const char* vb = sm.pv[pi];
+  // A block's registers: 4 token rows of K and V for this lane, and the
+  // shared decode-mask value of each of those rows.
+  struct Blk {
+    Raw<NB> k[4];
+    Raw<NB> v[4];
+    float mk[4];
+    int used;      // tokens in the block's page (0: past the end)
+    int tok_base;  // HELM token cursor of the page's first token
+    int tok0;      // first token of the block inside its page
+  };
+  // the mask row is shared by every query row of the tile (decode mask)
+  const bool mask_shared = has_mask && p.mask_hstride == 0 && S == 1;
+  // fast kernels always have full 128-dim rows in 16-byte-aligned pages
+  const bool full = DOT2 || p.full_d;
+
+  // Issues the loads of block bi.  Blocks past the end get a zero-byte
+  // resource: the loads return 0 without touching memory, so every
+  // iteration issues the same loads and waits stay exact.
+  auto load_block = [&](int bi, Blk& B) {
+    const bool valid = bi < nblk;
+    const int pi = valid ? bi / p.bpp : 0;
+    const int sub = valid ? bi - pi * p.bpp : 0;
+    const PageView pv = src.page(b, pg0 + pi, hk);
+    const int used = valid ? pv.used : 0;
+    const int tok0 = sub * kBlockTok;
+    B.used = used;
+    B.tok_base = pv.tok_off;
+    B.tok0 = tok0;
+    const int ntok = sclamp(used - tok0, 0, kBlockTok);
+    const char* kb = pv.k;
+    const char* vb = pv.v;
+    const int nbytes = ntok * (int)row_bytes;
+    const auto rk = make_rsrc(kb + tok0 * row_bytes, nbytes);
+    const auto rv = make_rsrc(vb + tok0 * row_bytes, nbytes);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int t = sub * kBlockTok + 4 * j + row;
-      if (t < used) {
-        const int64_t off = (int64_t)t * row_bytes + (int64_t)d0 * EB;
-        if (p.full_d) {
-          kr[j] = load_raw<NB>(kb + off);
-          vr[j] = load_raw<NB>(vb + off);
-        } else {
-          kr[j] = load_elems<TKV, EPL>(kb + off, dvalid);
-          vr[j] = load_elems<TKV, EPL>(vb + off, dvalid);
-        }
+      const int off = (4 * j + row) * (int)row_bytes + d0 * EB;
+      if constexpr (DOT2) {
+        B.k[j] = buf_load<NB>(rk, off);
+        B.v[j] = buf_load<NB>(rv, off);
       } else {
-        kr[j] = zero_raw<NB>();
-        vr[j] = zero_raw<NB>();
+        if (full) {
+          B.k[j] = buf_load<NB>(rk, off);
+          B.v[j] = buf_load<NB>(rv, off);
+        } else {
+          B.k[j] = buf_load_elems<TKV, EPL>(rk, off, dvalid);
+          B.v[j] = buf_load_elems<TKV, EPL>(rv, off, dvalid);
+        }
       }
+    }
+    if (mask_shared) {
+      const float* mb = reinterpret_cast<const float*>(uniform64(
+          reinterpret_cast<uint64_t>(p.mask + mrow[0] + pv.tok_off + tok0)));
+      const auto rm = make_rsrc(mb, ntok * 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        B.mk[j] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(rm, (4 * j + row) * 4, 0, 0));
     }
   };
 
-  auto compute_block = [&](int bi, const Raw<NB> (&kr)[4],
-                           const Raw<NB> (&vr)[4]) {
-    const int pi = bi / p.bpp;
-    const int sub = bi - pi * p.bpp;
-    const int used = sm.used[pi];
-    const int tok_base = sm.tok_off[pi];
+  auto compute_block = [&](const Blk& B) {
+    const int used = B.used;
+    const int tok_base = B.tok_base;
+    // q . k of this lane's 4 token rows, reduced across the 16-lane row
     float sc[GM][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -432,13 +574,13 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
           float acc = 0.f;
 #pragma unroll
           for (int w = 0; w < NB / 4; ++w)
-            acc = dot2<TKV>(kr[j].w[w], qraw[g].w[w], acc);
+            acc = dot2<TKV>(B.k[j].w[w], qraw[g].w[w], acc);
           sc[g][j] = acc;
         }
       } else {
         float kf[EPL];
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) kf[e] = elem_f32<TKV>(kr[j], e);
+        for (int e = 0; e < EPL; ++e) kf[e] = elem_f32<TKV>(B.k[j], e);
 #pragma unroll
         for (int g = 0; g < GM; ++g) {
           float acc = 0.f;
@@ -453,66 +595,109 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
 #pragma unroll
       for (int j = 0; j < 4; ++j) sc[g][j] = row_sum16(sc[g][j]);
 
-    float vf[4][EPL];
+    // logits: scale, then the optional features, each one uniform branch per
+    // block rather than per (row, token)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int g = 0; g < GM; ++g)
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) vf[j][e] = elem_f32<TKV>(vr[j], e);
-
+      for (int j = 0; j < 4; ++j) sc[g][j] *= scale;
+    if (has_cap) {
+#pragma unroll
+      for (int g = 0; g < GM; ++g)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[g][j] = tanhf(sc[g][j] * inv_cap) * cap;
+    }
+    if (mask_shared) {
+#pragma unroll
+      for (int g = 0; g < GM; ++g)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[g][j] += B.mk[j];
+    } else if (has_mask) {
+      // per-row mask rows (prefill chunks, per-head masks); the clamp keeps
+      // the read inside the page's tokens
+#pragma unroll
+      for (int g = 0; g < GM; ++g)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          sc[g][j] += p.mask[mrow[g] + tok_base +
+                             min(B.tok0 + 4 * j + row, used - 1)];
+    }
+    if (p.causal) {
+#pragma unroll
+      for (int g = 0; g < GM; ++g)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (tok_base + B.tok0 + 4 * j + row > srow[g]) sc[g][j] = -INFINITY;
+    }
+    // online-softmax update; sc becomes the probabilities.  The reference
+    // max m is refreshed only when a block max exceeds it by more than
+    // kRescaleSlack (checked across the wave, so the branch is uniform);
+    // otherwise p = exp(s - m) <= e^kRescaleSlack and O, L stay exact
+    // relative to the stale m.
+    float bm[GM];
+    bool need = false;
 #pragma unroll
     for (int g = 0; g < GM; ++g) {
-      float s4[4];
-      float bm = -INFINITY;
+      bm[g] = -INFINITY;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int t = sub * kBlockTok + 4 * j + row;
-        float s = sc[g][j] * scale;
-        if (has_cap) s = tanhf(s * inv_cap) * cap;
-        // clamp keeps the mask read inside the page's tokens
-        const int tpos = tok_base + min(t, used - 1);
-        if (has_mask) s += p.mask[mrow[g] + tpos];
-        if (p.causal && tpos > srow[g]) s = -INFINITY;
-        if (t >= used) s = -INFINITY;
-        s4[j] = s;
-        bm = fmaxf(bm, s);
+        if (B.tok0 + 4 * j + row >= used) sc[g][j] = -INFINITY;
+        bm[g] = fmaxf(bm[g], sc[g][j]);
       }
-      const float mn = fmaxf(m[g], bm);
-      const float base = (mn == -INFINITY) ? 0.f : mn;
-      const float alpha = fexp(m[g] - base);
+      need = need || (bm[g] > m[g] + kRescaleSlack);
+    }
+    if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+      for (int g = 0; g < GM; ++g) {
+        const float mn = fmaxf(m[g], bm[g]);
+        const float base = (mn == -INFINITY) ? 0.f : mn;
+        const float a = fexp(m[g] - base);
+        l[g] *= a;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[g][e] *= a;
+        m[g] = mn;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+      const float base = (m[g] == -INFINITY) ? 0.f : m[g];
       float ps = 0.f;
-      float pj[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        pj[j] = fexp(s4[j] - base);
-        ps += pj[j];
+        sc[g][j] = fexp(sc[g][j] - base);
+        ps += sc[g][j];
       }
-      l[g] = l[g] * alpha + ps;
+      l[g] += ps;
+    }
+    // P . V, one token row of V widened at a time
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        float acc = o[g][e] * alpha;
+    for (int j = 0; j < 4; ++j) {
+      float vf[EPL];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc = fmaf(pj[j], vf[j][e], acc);
-        o[g][e] = acc;
-      }
-      m[g] = mn;
+      for (int e = 0; e < EPL; ++e) vf[e] = elem_f32<TKV>(B.v[j], e);
+#pragma unroll
+      for (int g = 0; g < GM; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[g][e] = fmaf(sc[g][j], vf[e], o[g][e]);
     }
   };
 
-  // ---- main loop: two register buffers, next block's loads in flight ------
+  // ---- main loop: three register buffers, two blocks' loads in flight ------
   {
-    Raw<NB> ka[4], va[4], kb2[4], vb2[4];
-    int bi = wave;
-    if (bi < nblk) load_block(bi, ka, va);
-    while (bi < nblk) {
-      const int bn = bi + kWaves;
-      if (bn < nblk) load_block(bn, kb2, vb2);
-      compute_block(bi, ka, va);
-      bi = bn;
-      if (bi >= nblk) break;
-      const int bn2 = bi + kWaves;
-      if (bn2 < nblk) load_block(bn2, ka, va);
-      compute_block(bi, kb2, vb2);
-      bi = bn2;
+    constexpr int W = kWaves;
+    const int nmine = nblk > wave ? (nblk - wave + W - 1) / W : 0;
+    Blk ba, bb, bc;
+    load_block(wave, ba);
+    load_block(wave + W, bb);
+    for (int k = 0; k < nmine; k += 3) {
+      load_block(wave + (k + 2) * W, bc);
+      compute_block(ba);
+      if (k + 1 >= nmine) break;
+      load_block(wave + (k + 3) * W, ba);
+      compute_block(bb);
+      if (k + 2 >= nmine) break;
+      load_block(wave + (k + 4) * W, bb);
+      compute_block(bc);
     }
   }
 
@@ -565,15 +750,17 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
       L += a * sm.l[w][g];
       O += a * sm.o[w][g][d];
     }
-    p.ws_o[(part + g) * D + d] = O;
-    if (d == 0) {
-      p.ws_ml[(part + g) * 2 + 0] = M;
-      p.ws_ml[(part + g) * 2 + 1] = L;
-    }
+    st_agent(&p.ws_o[(part + g) * D + d], O);
+    if (d == 0) st_agent_ml(&p.ws_ml[(part + g) * 2], M, L);
   }
 
   // ---- ticket: the last split of the tile merges -----------------------------
-  __threadfence();
+  // Partials are written with agent-scope stores, which complete only once
+  // they are coherent across XCDs; the barrier waits (vmcnt(0)) for every
+  // wave's stores before the agent-scope ticket increment.  The merging
+  // workgroup reads the partials back with agent-scope loads, so no L2
+  // writeback / invalidate (an agent-scope release/acquire fence, which
+  // serialises per XCD) is needed.
   __syncthreads();
   if (tid == 0) {
     const uint32_t prev = atomicAdd(&p.tickets[tile], 1u);
@@ -581,32 +768,110 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
   }
   __syncthreads();
   if (!sm.last) return;
-  __threadfence();
 
+  // ---- final merge: one batch of independent loads per thread -------------
+  // Thread (sub, c) owns output column c (cw consecutive dims of one row) and
+  // the splits s = sub, sub + nsub, ...; it loads (m_s, l_s) and o_s[c] of
+  // all of them at once, merges them online, and the nsub partial results
+  // of a column are combined through LDS.
   const int64_t part0 = (int64_t)tile * p.max_splits * GM;
-  for (int idx = tid; idx < nrows * D; idx += kThreads) {
-    const int g = idx / D;
-    const int d = idx - g * D;
-    float M = -INFINITY;
-    for (int sp = 0; sp < total; ++sp)
-      M = fmaxf(M, p.ws_ml[(part0 + (int64_t)sp * GM + g) * 2]);
-    const float base = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f, O = 0.f;
-    for (int sp = 0; sp < total; ++sp) {
-      const int64_t pi = part0 + (int64_t)sp * GM + g;
-      const float ms = p.ws_ml[pi * 2];
-      const float ls = p.ws_ml[pi * 2 + 1];
-      const float os = p.ws_o[pi * D + d];
-      const float a = fexp(ms - base);
-      L += a * ls;
-      O += a * os;
+  const int cw = (D % 4 == 0) ? 4 : 1;
+  const int ncol = nrows * D / cw;
+  const int nsub = ncol >= kThreads ? 1 : kThreads / ncol;
+  const int cstep = ncol >= kThreads ? kThreads : ncol * nsub;
+  const int sub = ncol >= kThreads ? 0 : tid / ncol;
+  const float2* mlp = reinterpret_cast<const float2*>(p.ws_ml) + part0;
+  for (int c = (ncol >= kThreads ? tid : tid % ncol); c < ncol && sub < nsub;
+       c += cstep) {
+    const int e0 = c * cw;  // element index inside [nrows][D]
+    const int g = e0 / D;
+    float M = -INFINITY, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = sub; s0 < total; s0 += nsub * kMergeBatch) {
+      float2 ml[kMergeBatch];
+      float4 v[kMergeBatch];
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        const int sp = s0 + k * nsub;
+        if (sp < total) {
+          const int64_t pi = (int64_t)sp * GM + g;
+          ml[k] = ld_agent_ml(mlp + pi);
+          const float* src = p.ws_o + (part0 + pi) * D + (e0 - g * D);
+          v[k] = (cw == 4) ? ld_agent4(src)
+                           : make_float4(ld_agent(src), 0.f, 0.f, 0.f);
+        } else {
+          ml[k] = make_float2(-INFINITY, 0.f);
+          v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+      float mb = M;
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) mb = fmaxf(mb, ml[k].x);
+      const float base = (mb == -INFINITY) ? 0.f : mb;
+      const float a0 = fexp(M - base);
+      L *= a0;
+      acc.x *= a0; acc.y *= a0; acc.z *= a0; acc.w *= a0;
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        const float wgt = fexp(ml[k].x - base);
+        L = fmaf(wgt, ml[k].y, L);
+        acc.x = fmaf(wgt, v[k].x, acc.x);
+        acc.y = fmaf(wgt, v[k].y, acc.y);
+        acc.z = fmaf(wgt, v[k].z, acc.z);
+        acc.w = fmaf(wgt, v[k].w, acc.w);
+      }
+      M = mb;
     }
-    const int rr = r0 + g;
-    const int gg = rr / S, s = rr % S;
-    const int h = hk * G + gg;
-    const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * D + d;
-    store_elem<TQ>(reinterpret_cast<char*>(p.out) + o_off * QB,
-                   O / fmaxf(L, 1e-12f));
+    if (nsub > 1) {
+      sm.red[tid] = acc;
+      sm.redml[tid] = make_float2(M, L);
+    } else {
+      const float inv = 1.f / fmaxf(L, 1e-12f);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j >= cw) break;
+        const float aj = j == 0 ? acc.x : j == 1 ? acc.y : j == 2 ? acc.z : acc.w;
+        const int e = e0 + j;
+        const int gg_r = r0 + e / D;
+        const int gg = gg_r / S, s = gg_r % S;
+        const int h = hk * G + gg;
+        const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * D + e % D;
+        store_elem<TQ>(reinterpret_cast<char*>(p.out) + o_off * QB, aj * inv);
+      }
+    }
+  }
+  if (nsub > 1) {
+    __syncthreads();
+    if (tid < ncol) {
+      float M = -INFINITY;
+      for (int j = 0; j < nsub; ++j) M = fmaxf(M, sm.redml[tid + j * ncol].x);
+      const float base = (M == -INFINITY) ? 0.f : M;
+      float L = 0.f;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int j = 0; j < nsub; ++j) {
+        const float2 ml = sm.redml[tid + j * ncol];
+        const float4 t = sm.red[tid + j * ncol];
+        const float wgt = fexp(ml.x - base);
+        L = fmaf(wgt, ml.y, L);
+        acc.x = fmaf(wgt, t.x, acc.x);
+        acc.y = fmaf(wgt, t.y, acc.y);
+        acc.z = fmaf(wgt, t.z, acc.z);
+        acc.w = fmaf(wgt, t.w, acc.w);
+      }
+      const int e0 = tid * cw;
+      const float inv = 1.f / fmaxf(L, 1e-12f);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (j >= cw) break;
+        const float aj = j == 0 ? acc.x : j == 1 ? acc.y : j == 2 ? acc.z : acc.w;
+        const int e = e0 + j;
+        const int gg_r = r0 + e / D;
+        const int gg = gg_r / S, s = gg_r % S;
+        const int h = hk * G + gg;
+        const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * D + e % D;
+        store_elem<TQ>(reinterpret_cast<char*>(p.out) + o_off * QB, aj * inv);
+      }
+    }
   }
   if (tid == 0) p.tickets[tile] = 0u;
 }

@@ -123,10 +123,21 @@ int make_plan(Plan& pl, int kv_dtype, int q_dtype, int B, int Hq, int Hkv,
     pps = (int)std::ceil(std::max(1.0, avg_pages) / splits);
     pps = std::max(pps, min_pps(pl.bpp));
   }
-  pl.pps = std::min(std::max(pps, 1), kMaxPps);
+  pps = std::max(pps, (max_pages + kMaxSplits - 1) / kMaxSplits);
+  if (pps > kMaxPps)
+    return fail(HELM_E_UNSUPPORTED,
+                "context longer than kMaxSplits * kMaxPps pages per sequence");
+  pl.pps = std::max(pps, 1);
   pl.max_splits = std::max(1, (max_pages + pl.pps - 1) / pl.pps);
   size_plan(pl, B, Hkv, D);
   return HELM_OK;
+}
+
+// Splits of a chained (mixed residency) call: one run of splits per launch.
+int chained_splits(const std::vector<std::pair<int, int>>& ranges, int pps) {
+  int total = 0;
+  for (const auto& r : ranges) total += (r.second - r.first + pps - 1) / pps;
+  return total;
 }
 
 // Bytes from a page's head-0 token-0 element to the end of its last used
@@ -459,8 +470,9 @@ size_t helm_query_workspace_bytes(int B, int Hq, int Hkv, int q_len, int D,
     pl.gm = gm;
     pl.n_qtiles = (G * q_len + gm - 1) / gm;
     pl.bpp = std::max(1, (page_size + kBlockTok - 1) / kBlockTok);
-    const int pps = pages_per_split > 0 ? std::min(pages_per_split, kMaxPps)
-                                        : min_pps(pl.bpp);
+    int pps = pages_per_split > 0 ? std::min(pages_per_split, kMaxPps)
+                                  : min_pps(pl.bpp);
+    pps = std::max(pps, (max_pages + kMaxSplits - 1) / kMaxSplits);
     pl.max_splits = std::max(1, (max_pages + pps - 1) / pps);
     size_plan(pl, B, Hkv, D);
     best = std::max(best, pl.total());
@@ -647,6 +659,18 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   int rc = make_plan(pl, kv_dtype, q_dtype, B, Hq, Hkv, q_len, D, max_tok,
                      std::max(max_pages, 1), (double)n_all / B, 0, al);
   if (rc != HELM_OK) return rc;
+  if (n_host) {
+    // every launch owns whole splits; keep the call within kMaxSplits
+    std::vector<std::pair<int, int>> ranges;
+    for (const Launch& L : launches) ranges.push_back({L.lo, L.hi});
+    while (chained_splits(ranges, pl.pps) > kMaxSplits) {
+      if (pl.pps >= kMaxPps)
+        return fail(HELM_E_UNSUPPORTED, "too many staged chunks for one call");
+      pl.pps = std::min(kMaxPps, pl.pps * 2);
+    }
+    if ((int)launches.size() > kMaxSplits)
+      return fail(HELM_E_UNSUPPORTED, "too many staged chunks for one call");
+  }
   int total_splits = 0;
   std::vector<int> split_base;
   for (const Launch& L : launches) {

@@ -51,8 +51,10 @@ def test_workspace_sizing_host_only():
     # Qwen3-8B shape, 2048 pages of 16 tokens
     n = lib.helm_query_workspace_bytes(1, 32, 8, 1, 128, 2048, 16, 0)
     assert n > 0
-    # grows with pages, invalid shapes give 0
-    assert lib.helm_query_workspace_bytes(1, 32, 8, 1, 128, 4096, 16, 0) > n
+    # grows with pages up to the per-tile split cap (256 splits), then flat;
+    # invalid shapes give 0
+    assert lib.helm_query_workspace_bytes(1, 32, 8, 1, 128, 1024, 16, 0) < n
+    assert lib.helm_query_workspace_bytes(1, 32, 8, 1, 128, 65536, 16, 0) == n
     assert lib.helm_query_workspace_bytes(1, 30, 8, 1, 128, 2048, 16, 0) == 0
 
 
