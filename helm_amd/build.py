@@ -35,6 +35,9 @@ HIPCC_FLAGS = [
     f"-I{CSRC}",
     # no packed-fp32 instructions in device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: the decode kernel rescales them
+    # with vector ALU ops, which cannot address AGPRs
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "attn_kernel.h"
+#include "attn_mfma.h"
 
 namespace helm {
 namespace {
@@ -34,6 +35,39 @@ hipError_t launch_generic(const LaunchSpec& s, hipStream_t st) {
 }
 
 #if HELM_TKV_IS_16BIT
+// Matrix-core kernels: D = 128, q and KV of the same 16-bit type.
+template <typename T, class Src, int FEAT>
+hipError_t launch_mfma_feat(const LaunchSpec& s, const Src& src, hipStream_t st) {
+  if (s.nw == 8)
+    hipLaunchKernelGGL((decode_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), 0, st, s.p,
+                       src);
+  else
+    hipLaunchKernelGGL((decode_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), 0, st, s.p,
+                       src);
+  return hipGetLastError();
+}
+
+template <typename T, class Src>
+hipError_t launch_mfma_src(const LaunchSpec& s, const Src& src, hipStream_t st) {
+  switch (s.feat) {
+    case 0: return launch_mfma_feat<T, Src, 0>(s, src, st);
+    case 1: return launch_mfma_feat<T, Src, 1>(s, src, st);
+    case 2: return launch_mfma_feat<T, Src, 2>(s, src, st);
+    case 3: return launch_mfma_feat<T, Src, 3>(s, src, st);
+    case 4: return launch_mfma_feat<T, Src, 4>(s, src, st);
+    case 5: return launch_mfma_feat<T, Src, 5>(s, src, st);
+    case 6: return launch_mfma_feat<T, Src, 6>(s, src, st);
+    case 7: return launch_mfma_feat<T, Src, 7>(s, src, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <typename T>
+hipError_t launch_mfma(const LaunchSpec& s, hipStream_t st) {
+  if (s.mode == 0) return launch_mfma_src<T, PoolSrc>(s, s.pool, st);
+  return launch_mfma_src<T, DescSrc>(s, s.desc, st);
+}
+
 // Fast kernels: D = 128, q and KV of the same 16-bit type, exact G rows.
 template <typename T>
 hipError_t launch_fast(const LaunchSpec& s, hipStream_t st) {
@@ -55,6 +89,7 @@ hipError_t launch_fast(const LaunchSpec& s, hipStream_t st) {
 
 hipError_t HELM_LAUNCH_NAME(const LaunchSpec& s, hipStream_t st) {
 #if HELM_TKV_IS_16BIT
+  if (s.mfma) return launch_mfma<HELM_TKV>(s, st);
   if (s.fast) return launch_fast<HELM_TKV>(s, st);
 #endif
   if (s.q_dtype == HELM_F32) return launch_generic<HELM_TKV, float>(s, st);

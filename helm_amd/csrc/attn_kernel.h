@@ -19,11 +19,10 @@
 //   keeps an online-softmax state (m, l, o[EPL]) over the tokens of its row
 //   with no cross-row traffic in the loop.  All query heads of the GQA group
 //   reuse every K/V tile from registers.
-//   At the end the 16 row states are merged (shuffles, then LDS), each
-//   workgroup writes one partial (m, l, o[D]) per row to the workspace, and
-//   the last workgroup of a (sequence, head, tile) to arrive — found with an
-//   agent-scope atomic ticket — merges all splits and writes the output.  The
-//   ticket is reset by that workgroup, so the workspace needs zeroing once.
+//   At the end the 16 row states are merged (shuffles, then LDS) and each
+//   workgroup writes one partial (m, l, o[D]) per row to the workspace;
+//   merge_splits_kernel, launched after the split kernels, combines the
+//   partials of every (sequence, head, tile) and writes the output.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -39,7 +38,6 @@ constexpr int kRowLanes = 16;   // lanes per token row (one DPP row)
 constexpr int kBlockTok = 16;   // tokens per wave block (4 rows x 4 j)
 constexpr int kMaxPps = 256;    // pages per split held in LDS
 constexpr int kMaxSplits = 256; // splits per (sequence, head, tile) merged
-constexpr int kMergeBatch = 16; // independent partial loads in flight per thread
 constexpr float kRescaleSlack = 8.f;  // lazy online-softmax rescale threshold
 
 // ---- element types ----------------------------------------------------------
@@ -379,22 +377,297 @@ struct AttnParams {
   int total_splits;   // > 0: splits of the whole call (chained launches)
   int max_splits;     // stride of the partial buffers
   int full_d;         // D == 16*EPL and 16-byte friendly addresses
-  float* ws_o;        // [tiles][max_splits][GM][D]
-  float* ws_ml;       // [tiles][max_splits][GM][2]
-  uint32_t* tickets;  // [tiles]
+  float* ws_o;        // [tiles][max_splits][rows_per_tile][D]
+  float* ws_ml;       // [tiles][max_splits][rows_per_tile][2]
+  int* counts;        // [tiles] splits of each tile (merge-kernel mode)
+  uint32_t* tickets;  // [tiles] arrivals (fused mode; zero between calls)
+  int fused;          // 1: the last split of a tile merges in-kernel
 };
 
-// Per-workgroup LDS.
-template <int GM, int DMAX>
+// Per-workgroup LDS: per-wave online-softmax states of the tile's rows, and
+// the cross-thread reduction of the in-kernel split merge.
+template <int NW, int GM, int DMAX>
 struct Smem {
-  float o[kWaves][GM][DMAX];
-  float m[kWaves][GM];
-  float l[kWaves][GM];
-  // final merge: per-thread partial results of the split subsets
-  float4 red[kThreads];
-  float2 redml[kThreads];
+  float o[NW][GM][DMAX];
+  float m[NW][GM];
+  float l[NW][GM];
+  float4 red[64 * NW];
+  float2 redml[64 * NW];
   int last;
 };
+
+// Agent-coherent 16-byte accesses (sc1: coherent across XCDs) to the split
+// partials of the in-kernel merge, through one resource over the partial
+// buffer (uniform base, per-lane byte offsets).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partials_rsrc(const AttnParams& p) {
+  return make_rsrc(p.ws_o, 0x7ffffff0);
+}
+__device__ __forceinline__ void st_coherent16(__amdgpu_buffer_rsrc_t r, int64_t elem, float4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(
+      __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, v), r,
+      static_cast<int>(elem * 4), 0, 16);
+}
+__device__ __forceinline__ float4 ld_coherent16(__amdgpu_buffer_rsrc_t r, int64_t elem) {
+  return __builtin_bit_cast(float4,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(elem * 4), 0, 16));
+}
+
+// Shared end of a split for every decode kernel (NW waves per workgroup).
+// On entry sm.o / sm.m / sm.l hold the per-wave online-softmax states of the
+// tile's `nrows` rows (a barrier has been passed).  Merges the waves and
+// writes the split's partial (m, l, o[D]) per row.  In fused mode the
+// partials are written agent-coherently, an atomic ticket counts the tile's
+// arrivals and the last split to arrive merges all of them and writes the
+// output; otherwise merge_splits_kernel does that after the kernel.
+template <typename TQ, int NW, int GM, int DMAX>
+__device__ __forceinline__ void split_epilogue(Smem<NW, GM, DMAX>& sm, const AttnParams& p,
+                                               int tid, int tile, int split, int total,
+                                               int nrows, int r0, int b, int hk) {
+  constexpr int NT = 64 * NW;
+  constexpr int QB = ElemBytes<TQ>::v;
+  const int D = p.D;
+  const int RS = p.rows_per_tile;  // workspace rows per (tile, split)
+  const int64_t part = ((int64_t)tile * p.max_splits + split) * RS;
+  const int cw = (D % 4 == 0) ? 4 : 1;
+  const int ncol_all = nrows * (D / cw);
+  const auto pr = partials_rsrc(p);
+  for (int idx = tid; idx < ncol_all; idx += NT) {
+    const int g = idx / (D / cw);
+    const int d0 = (idx - g * (D / cw)) * cw;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm.m[w][g]);
+    const float base = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f;
+    float O[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float a = fexp(sm.m[w][g] - base);
+      L += a * sm.l[w][g];
+      for (int j = 0; j < cw; ++j) O[j] += a * sm.o[w][g][d0 + j];
+    }
+    float* dst = &p.ws_o[(part + g) * D + d0];
+    if (p.fused) {
+      if (cw == 4) st_coherent16(pr, (part + g) * D + d0, make_float4(O[0], O[1], O[2], O[3]));
+      else st_agent(dst, O[0]);
+      if (d0 == 0) st_agent_ml(&p.ws_ml[(part + g) * 2], M, L);
+    } else {
+      for (int j = 0; j < cw; ++j) dst[j] = O[j];
+      if (d0 == 0) *reinterpret_cast<float2*>(&p.ws_ml[(part + g) * 2]) = make_float2(M, L);
+    }
+  }
+  if (!p.fused) return;
+
+  // ---- ticket: the last split of the tile merges -----------------------------
+  // The barrier waits (vmcnt(0)) for every wave's coherent stores before the
+  // agent-scope ticket increment; the merging workgroup reads the partials
+  // with coherent loads issued after it has seen the ticket.
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev = atomicAdd(&p.tickets[tile], 1u);
+    sm.last = (prev == static_cast<uint32_t>(total - 1)) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!sm.last) return;
+
+  // Thread (sub, c) owns column chunk c of the tile's rows and the splits
+  // sub, sub + nsub, ...: every load of a batch is in flight at once.
+  constexpr int kBatch = 16;
+  const int64_t part0 = (int64_t)tile * p.max_splits * RS;
+  const int ncol = ncol_all;
+  const int nsub = ncol >= NT ? 1 : NT / ncol;
+  const int sub = ncol >= NT ? 0 : tid / ncol;
+  const int cstep = ncol >= NT ? NT : ncol * nsub;
+  const int S = p.S, G = p.G;
+  for (int c = (ncol >= NT ? tid : tid % ncol); c < ncol && sub < nsub; c += cstep) {
+    const int g = c / (D / cw);
+    const int d0 = (c - g * (D / cw)) * cw;
+    float M = -INFINITY, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = sub; s0 < total; s0 += nsub * kBatch) {
+      float2 ml[kBatch];
+      float4 v[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int sp = s0 + k * nsub;
+        if (sp < total) {
+          const int64_t pi = part0 + (int64_t)sp * RS + g;
+          ml[k] = ld_agent_ml(reinterpret_cast<const float2*>(p.ws_ml) + pi);
+          v[k] = (cw == 4) ? ld_coherent16(pr, pi * D + d0)
+                           : make_float4(ld_agent(p.ws_o + pi * D + d0), 0.f, 0.f, 0.f);
+        } else {
+          ml[k] = make_float2(-INFINITY, 0.f);
+          v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+      float mb = M;
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) mb = fmaxf(mb, ml[k].x);
+      const float base = (mb == -INFINITY) ? 0.f : mb;
+      const float a0 = fexp(M - base);
+      L *= a0;
+      acc.x *= a0; acc.y *= a0; acc.z *= a0; acc.w *= a0;
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const float wgt = fexp(ml[k].x - base);
+        L = fmaf(wgt, ml[k].y, L);
+        acc.x = fmaf(wgt, v[k].x, acc.x);
+        acc.y = fmaf(wgt, v[k].y, acc.y);
+        acc.z = fmaf(wgt, v[k].z, acc.z);
+        acc.w = fmaf(wgt, v[k].w, acc.w);
+      }
+      M = mb;
+    }
+    if (nsub > 1) {
+      sm.red[tid] = acc;
+      sm.redml[tid] = make_float2(M, L);
+    } else {
+      const int rr = r0 + g;
+      const int h = hk * G + rr / S, s = rr % S;
+      char* orow = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * S + s) * D * QB;
+      const float inv = 1.f / fmaxf(L, 1e-12f);
+      const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+      for (int j = 0; j < cw; ++j) store_elem<TQ>(orow + (d0 + j) * QB, a[j] * inv);
+    }
+  }
+  if (nsub > 1) {
+    __syncthreads();
+    if (tid < ncol) {
+      float M = -INFINITY;
+      for (int j = 0; j < nsub; ++j) M = fmaxf(M, sm.redml[tid + j * ncol].x);
+      const float base = (M == -INFINITY) ? 0.f : M;
+      float L = 0.f;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int j = 0; j < nsub; ++j) {
+        const float2 ml = sm.redml[tid + j * ncol];
+        const float4 t = sm.red[tid + j * ncol];
+        const float wgt = fexp(ml.x - base);
+        L = fmaf(wgt, ml.y, L);
+        acc.x = fmaf(wgt, t.x, acc.x);
+        acc.y = fmaf(wgt, t.y, acc.y);
+        acc.z = fmaf(wgt, t.z, acc.z);
+        acc.w = fmaf(wgt, t.w, acc.w);
+      }
+      const int g = tid / (D / cw);
+      const int d0 = (tid - g * (D / cw)) * cw;
+      const int rr = r0 + g;
+      const int h = hk * G + rr / S, s = rr % S;
+      char* orow = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * S + s) * D * QB;
+      const float inv = 1.f / fmaxf(L, 1e-12f);
+      const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+      for (int j = 0; j < cw; ++j) store_elem<TQ>(orow + (d0 + j) * QB, a[j] * inv);
+    }
+  }
+  if (tid == 0) p.tickets[tile] = 0u;
+}
+
+// Combines the split partials of one (tile, row) and writes the output row:
+// out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, M = max_s m_s — the
+// final normalisation of HELM's loop, out / clamp(sum, 1e-12)
+// (helm/runtime/kv_cache.py:554-555).  grid = (tiles, rows_per_tile); a tile
+// whose sequence has no pages (split count 0) gets zeros
+// (kv_cache.py:441-442).  Thread (sub, c) owns output column chunk c and the
+// splits sub, sub + nsub, ...; all of its loads of a batch are in flight at
+// once, and the nsub partial results of a column meet in LDS.
+constexpr int kMergeBatch = 8;
+
+template <typename TQ>
+__global__ __launch_bounds__(kThreads) void merge_splits_kernel(AttnParams p) {
+  constexpr int QB = ElemBytes<TQ>::v;
+  __shared__ float4 red[kThreads];
+  __shared__ float2 redml[kThreads];
+  const int tile = blockIdx.x;
+  const int row = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int D = p.D, S = p.S, G = p.G;
+  const int RS = p.rows_per_tile;
+  const int qt = tile % p.n_qtiles;
+  const int hk = (tile / p.n_qtiles) % p.Hkv;
+  const int b = tile / (p.n_qtiles * p.Hkv);
+  const int r0 = qt * RS;
+  if (r0 + row >= G * S) return;
+  const int rr = r0 + row;
+  const int h = hk * G + rr / S, s = rr % S;
+  char* out_row = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * S + s) * D * QB;
+  const int total = p.counts[tile];
+
+  const int cw = (D % 4 == 0) ? 4 : 1;
+  const int ncol = D / cw;
+  const int nsub = ncol >= kThreads ? 1 : kThreads / ncol;
+  const int sub = tid / ncol;
+  const int c0 = tid % ncol;
+  const int64_t base_part = (int64_t)tile * p.max_splits * RS + row;
+  for (int c = c0; c < ncol && sub < nsub; c += kThreads) {
+    float M = -INFINITY, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = sub; s0 < total; s0 += nsub * kMergeBatch) {
+      float2 ml[kMergeBatch];
+      float4 v[kMergeBatch];
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        const int sp = s0 + k * nsub;
+        if (sp < total) {
+          const int64_t pi = base_part + (int64_t)sp * RS;
+          ml[k] = *reinterpret_cast<const float2*>(p.ws_ml + pi * 2);
+          const float* src = p.ws_o + pi * D + c * cw;
+          v[k] = (cw == 4) ? *reinterpret_cast<const float4*>(src)
+                           : make_float4(*src, 0.f, 0.f, 0.f);
+        } else {
+          ml[k] = make_float2(-INFINITY, 0.f);
+          v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+      float mb = M;
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) mb = fmaxf(mb, ml[k].x);
+      const float base = (mb == -INFINITY) ? 0.f : mb;
+      const float a0 = fexp(M - base);
+      L *= a0;
+      acc.x *= a0; acc.y *= a0; acc.z *= a0; acc.w *= a0;
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        const float wgt = fexp(ml[k].x - base);
+        L = fmaf(wgt, ml[k].y, L);
+        acc.x = fmaf(wgt, v[k].x, acc.x);
+        acc.y = fmaf(wgt, v[k].y, acc.y);
+        acc.z = fmaf(wgt, v[k].z, acc.z);
+        acc.w = fmaf(wgt, v[k].w, acc.w);
+      }
+      M = mb;
+    }
+    if (nsub > 1) {
+      red[tid] = acc;
+      redml[tid] = make_float2(M, L);
+    } else {
+      const float inv = 1.f / fmaxf(L, 1e-12f);
+      const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+      for (int j = 0; j < cw; ++j) store_elem<TQ>(out_row + (c * cw + j) * QB, a[j] * inv);
+    }
+  }
+  if (nsub > 1) {
+    __syncthreads();
+    if (tid < ncol) {
+      float M = -INFINITY;
+      for (int j = 0; j < nsub; ++j) M = fmaxf(M, redml[tid + j * ncol].x);
+      const float base = (M == -INFINITY) ? 0.f : M;
+      float L = 0.f;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int j = 0; j < nsub; ++j) {
+        const float2 ml = redml[tid + j * ncol];
+        const float4 t = red[tid + j * ncol];
+        const float wgt = fexp(ml.x - base);
+        L = fmaf(wgt, ml.y, L);
+        acc.x = fmaf(wgt, t.x, acc.x);
+        acc.y = fmaf(wgt, t.y, acc.y);
+        acc.z = fmaf(wgt, t.z, acc.z);
+        acc.w = fmaf(wgt, t.w, acc.w);
+      }
+      const float inv = 1.f / fmaxf(L, 1e-12f);
+      const float a[4] = {acc.x, acc.y, acc.z, acc.w};
+      for (int j = 0; j < cw; ++j) store_elem<TQ>(out_row + (tid * cw + j) * QB, a[j] * inv);
+    }
+  }
+}
 
 template <typename TKV, typename TQ, int EPL, int GM, bool DOT2, class Src>
 __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
@@ -405,7 +678,7 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
   constexpr int DMAX = kRowLanes * EPL;
   static_assert(!DOT2 || (EB == 2 && QB == 2), "dot2 needs 16-bit q and kv");
 
-  __shared__ Smem<GM, DMAX> sm;
+  __shared__ Smem<kWaves, GM, DMAX> sm;
 
   const int tid = threadIdx.x;
   // wave index made scalar so block indices / page bases live in SGPRs
@@ -434,13 +707,15 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
   const int nsplit_launch = (hi - lo + p.pps - 1) / p.pps;
   const int total = p.total_splits > 0 ? p.total_splits : nsplit_launch;
 
+  // split 0 publishes the tile's split count; a tile without pages gets
+  // zeros (HELM kv_cache.py:441-442), from split 0 in fused mode and from
+  // merge_splits_kernel otherwise
+  if (split_local == 0 && tid == 0) p.counts[tile] = total;
   if (total == 0) {
-    // Sequence without active tokens: zeros (HELM kv_cache.py:441-442).
-    if (split_local == 0) {
+    if (p.fused && split_local == 0) {
       for (int idx = tid; idx < nrows * D; idx += kThreads) {
         const int rr = r0 + idx / D;
-        const int g = rr / S, s = rr % S;
-        const int h = hk * G + g;
+        const int h = hk * G + rr / S, s = rr % S;
         const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * D + idx % D;
         store_elem<TQ>(reinterpret_cast<char*>(p.out) + o_off * QB, 0.f);
       }
@@ -734,146 +1009,7 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
   }
   __syncthreads();
 
-  // ---- merge the 4 waves, write this split's partial ------------------------
-  const int64_t part = ((int64_t)tile * p.max_splits + split) * GM;
-  for (int idx = tid; idx < nrows * D; idx += kThreads) {
-    const int g = idx / D;
-    const int d = idx - g * D;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm.m[w][g]);
-    const float base = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f, O = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float a = fexp(sm.m[w][g] - base);
-      L += a * sm.l[w][g];
-      O += a * sm.o[w][g][d];
-    }
-    st_agent(&p.ws_o[(part + g) * D + d], O);
-    if (d == 0) st_agent_ml(&p.ws_ml[(part + g) * 2], M, L);
-  }
-
-  // ---- ticket: the last split of the tile merges -----------------------------
-  // Partials are written with agent-scope stores, which complete only once
-  // they are coherent across XCDs; the barrier waits (vmcnt(0)) for every
-  // wave's stores before the agent-scope ticket increment.  The merging
-  // workgroup reads the partials back with agent-scope loads, so no L2
-  // writeback / invalidate (an agent-scope release/acquire fence, which
-  // serialises per XCD) is needed.
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = atomicAdd(&p.tickets[tile], 1u);
-    sm.last = (prev == static_cast<uint32_t>(total - 1)) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!sm.last) return;
-
-  // ---- final merge: one batch of independent loads per thread -------------
-  // Thread (sub, c) owns output column c (cw consecutive dims of one row) and
-  // the splits s = sub, sub + nsub, ...; it loads (m_s, l_s) and o_s[c] of
-  // all of them at once, merges them online, and the nsub partial results
-  // of a column are combined through LDS.
-  const int64_t part0 = (int64_t)tile * p.max_splits * GM;
-  const int cw = (D % 4 == 0) ? 4 : 1;
-  const int ncol = nrows * D / cw;
-  const int nsub = ncol >= kThreads ? 1 : kThreads / ncol;
-  const int cstep = ncol >= kThreads ? kThreads : ncol * nsub;
-  const int sub = ncol >= kThreads ? 0 : tid / ncol;
-  const float2* mlp = reinterpret_cast<const float2*>(p.ws_ml) + part0;
-  for (int c = (ncol >= kThreads ? tid : tid % ncol); c < ncol && sub < nsub;
-       c += cstep) {
-    const int e0 = c * cw;  // element index inside [nrows][D]
-    const int g = e0 / D;
-    float M = -INFINITY, L = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = sub; s0 < total; s0 += nsub * kMergeBatch) {
-      float2 ml[kMergeBatch];
-      float4 v[kMergeBatch];
-#pragma unroll
-      for (int k = 0; k < kMergeBatch; ++k) {
-        const int sp = s0 + k * nsub;
-        if (sp < total) {
-          const int64_t pi = (int64_t)sp * GM + g;
-          ml[k] = ld_agent_ml(mlp + pi);
-          const float* src = p.ws_o + (part0 + pi) * D + (e0 - g * D);
-          v[k] = (cw == 4) ? ld_agent4(src)
-                           : make_float4(ld_agent(src), 0.f, 0.f, 0.f);
-        } else {
-          ml[k] = make_float2(-INFINITY, 0.f);
-          v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
-      float mb = M;
-#pragma unroll
-      for (int k = 0; k < kMergeBatch; ++k) mb = fmaxf(mb, ml[k].x);
-      const float base = (mb == -INFINITY) ? 0.f : mb;
-      const float a0 = fexp(M - base);
-      L *= a0;
-      acc.x *= a0; acc.y *= a0; acc.z *= a0; acc.w *= a0;
-#pragma unroll
-      for (int k = 0; k < kMergeBatch; ++k) {
-        const float wgt = fexp(ml[k].x - base);
-        L = fmaf(wgt, ml[k].y, L);
-        acc.x = fmaf(wgt, v[k].x, acc.x);
-        acc.y = fmaf(wgt, v[k].y, acc.y);
-        acc.z = fmaf(wgt, v[k].z, acc.z);
-        acc.w = fmaf(wgt, v[k].w, acc.w);
-      }
-      M = mb;
-    }
-    if (nsub > 1) {
-      sm.red[tid] = acc;
-      sm.redml[tid] = make_float2(M, L);
-    } else {
-      const float inv = 1.f / fmaxf(L, 1e-12f);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j >= cw) break;
-        const float aj = j == 0 ? acc.x : j == 1 ? acc.y : j == 2 ? acc.z : acc.w;
-        const int e = e0 + j;
-        const int gg_r = r0 + e / D;
-        const int gg = gg_r / S, s = gg_r % S;
-        const int h = hk * G + gg;
-        const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * D + e % D;
-        store_elem<TQ>(reinterpret_cast<char*>(p.out) + o_off * QB, aj * inv);
-      }
-    }
-  }
-  if (nsub > 1) {
-    __syncthreads();
-    if (tid < ncol) {
-      float M = -INFINITY;
-      for (int j = 0; j < nsub; ++j) M = fmaxf(M, sm.redml[tid + j * ncol].x);
-      const float base = (M == -INFINITY) ? 0.f : M;
-      float L = 0.f;
-      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int j = 0; j < nsub; ++j) {
-        const float2 ml = sm.redml[tid + j * ncol];
-        const float4 t = sm.red[tid + j * ncol];
-        const float wgt = fexp(ml.x - base);
-        L = fmaf(wgt, ml.y, L);
-        acc.x = fmaf(wgt, t.x, acc.x);
-        acc.y = fmaf(wgt, t.y, acc.y);
-        acc.z = fmaf(wgt, t.z, acc.z);
-        acc.w = fmaf(wgt, t.w, acc.w);
-      }
-      const int e0 = tid * cw;
-      const float inv = 1.f / fmaxf(L, 1e-12f);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (j >= cw) break;
-        const float aj = j == 0 ? acc.x : j == 1 ? acc.y : j == 2 ? acc.z : acc.w;
-        const int e = e0 + j;
-        const int gg_r = r0 + e / D;
-        const int gg = gg_r / S, s = gg_r % S;
-        const int h = hk * G + gg;
-        const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * D + e % D;
-        store_elem<TQ>(reinterpret_cast<char*>(p.out) + o_off * QB, aj * inv);
-      }
-    }
-  }
-  if (tid == 0) p.tickets[tile] = 0u;
+  split_epilogue<TQ, kWaves, GM, DMAX>(sm, p, tid, tile, split, total, nrows, r0, b, hk);
 }
 
 // ---- host-side launch description -------------------------------------------
@@ -886,6 +1022,9 @@ struct LaunchSpec {
   int epl;            // elements per lane (D <= 16*epl)
   int gm;             // rows per tile
   int fast;           // exact-G dot2 kernel
+  int mfma;           // matrix-core kernel (attn_mfma.h)
+  int feat;           // its feature bits (MfmaFeat)
+  int nw;             // its waves per workgroup (4 or 8)
   dim3 grid;
 };
 

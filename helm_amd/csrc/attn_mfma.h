@@ -1,0 +1,383 @@
+// Split-K paged decode attention on the matrix cores (gfx950 MFMA), for
+// 16-bit K/V pages with head_dim 128 — the hot configuration of HELM's
+// perform_streaming_attention (helm/runtime/kv_cache.py:468-555 masked
+// online-softmax loop, :562-568 Path 1, :584-662 Path 3) and of the batched
+// decode of _decode_batched (helm/runtime/kv_offload.py:152-174).
+//
+// Decode attention is bound by HBM: every K/V byte is read once.  The matrix
+// cores are used here only to take the arithmetic off the vector ALU, so that
+// the ALU work per 16-token block stays far below the time its 8 KiB take to
+// arrive, at any GQA group size up to 16 query rows per KV head.
+//
+// Work decomposition: grid.x = split (<= kMfmaMaxPps pages), grid.y = KV head
+// + Hkv * row tile, grid.z = sequence; NW waves per workgroup, wave w takes
+// the 16-token blocks w, w+NW, ... of the split.  Per block, with q4 = lane/16 and
+// n = lane%16:
+//   * scores: S^T = K . Q^T with four 16x16x32 MFMAs (k = head dims).  Lane l
+//     loads K of token tau(n) = 4*(n%4) + n/4 at dims chunk 4i + q4 (16 B, i =
+//     0..3); Q^T's operand holds query row n at the same chunks.  The result
+//     gives lane l the scores of query row n for tokens 4r + q4 (r = 0..3).
+//   * online softmax per row on those four scores, in natural-log units as
+//     HELM's loop; the running max is refreshed (wave-uniformly) only when a
+//     score exceeds it by more than kMfmaSlack, otherwise the stale max keeps
+//     every weight <= e^kMfmaSlack and O, L exact relative to it.
+//   * O += P . V with eight 16x16x32 MFMAs (one per dim e of each lane's
+//     8-dim column group): P's operand is {hi(p_r), lo(p_r)} — each weight
+//     split into two 16-bit values whose sum carries 16 mantissa bits — and
+//     V's operand the same four tokens 4j + q4 twice, so one MFMA adds
+//     (hi + lo) . v.  Lane (q4, n) loads V rows 4j + q4 at dims 8n..8n+7: a
+//     wave load is 1 KiB contiguous.  Products are exact and accumulate in
+//     fp32.
+// No data moves between lanes in the loop; the split's per-wave states meet in
+// LDS; the shared split epilogue (attn_kernel.h) merges the waves and then
+// the splits.
+#pragma once
+
+#include "attn_kernel.h"
+
+namespace helm {
+
+constexpr int kMfmaRows = 16;     // query rows per tile (MFMA M dimension)
+constexpr int kMfmaMaxPps = 64;   // pages per split: page records live one per lane
+constexpr int kMfmaMaxSplits = 4096;
+constexpr float kMfmaSlack = 8.f;
+
+enum MfmaFeat { kFeatMask = 1, kFeatCap = 2, kFeatCausal = 4 };
+
+typedef __bf16 mf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mf_f16x8 __attribute__((ext_vector_type(8)));
+typedef float mf_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t mf_u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct MfmaOps;
+
+template <> struct MfmaOps<bf16_t> {
+  __device__ static __forceinline__ mf_f32x4 mma(mf_u32x4 a, mf_u32x4 b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mf_bf16x8, a),
+                                                   __builtin_bit_cast(mf_bf16x8, b), c, 0, 0, 0);
+  }
+  // round to nearest even (finite, non-negative inputs: softmax weights)
+  __device__ static __forceinline__ uint32_t to16(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  }
+  __device__ static __forceinline__ float from16(uint32_t h) { return __uint_as_float(h << 16); }
+};
+
+template <> struct MfmaOps<f16_t> {
+  __device__ static __forceinline__ mf_f32x4 mma(mf_u32x4 a, mf_u32x4 b, mf_f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf_f16x8, a),
+                                                  __builtin_bit_cast(mf_f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t to16(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+  }
+  __device__ static __forceinline__ float from16(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+  }
+};
+
+// 16-byte buffer load with the non-temporal hint: K/V are read exactly once.
+__device__ __forceinline__ mf_u32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, int off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
+  return mf_u32x4{v[0], v[1], v[2], v[3]};
+}
+
+// Low / high 16-bit halves of two words packed into one: (a.lo, b.lo), (a.hi, b.hi).
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// ---- page records held one per lane ------------------------------------------
+// Lane i holds the record of page pg0 + i of the split; a block reads its
+// page's record with v_readlane (a uniform lane index), so no memory access
+// sits between a block's turn and the issue of its loads.
+struct PoolLanes {
+  int slot;
+};
+struct DescLanes {
+  uint32_t klo, khi, vlo, vhi;
+  int used, tok_off, head_stride;
+};
+
+__device__ __forceinline__ PoolLanes lane_pages(const PoolSrc& s, int b, int pg0, int npg,
+                                                int lane) {
+  PoolLanes L;
+  L.slot = s.table[(int64_t)b * s.table_stride + pg0 + min(lane, npg - 1)];
+  return L;
+}
+__device__ __forceinline__ DescLanes lane_pages(const DescSrc& s, int b, int pg0, int npg,
+                                                int lane) {
+  const int base = sload(s.seq_off + b);
+  const helm_page d = s.pages[base + pg0 + min(lane, npg - 1)];
+  DescLanes L;
+  L.klo = static_cast<uint32_t>(d.k);
+  L.khi = static_cast<uint32_t>(d.k >> 32);
+  L.vlo = static_cast<uint32_t>(d.v);
+  L.vhi = static_cast<uint32_t>(d.v >> 32);
+  L.used = d.used;
+  L.tok_off = d.tok_off;
+  L.head_stride = d.head_stride;
+  return L;
+}
+
+// Page i of the split (uniform): head-hk K / V bases, used tokens, token offset.
+__device__ __forceinline__ PageView lane_page_view(const PoolSrc& s, const PoolLanes& L, int b,
+                                                   int pg, int i, int hk) {
+  const int slot = __builtin_amdgcn_readlane(L.slot, i);
+  const int T = sload(s.seq_lens + b);
+  PageView pv;
+  const int64_t off = (int64_t)slot * s.slot_stride_b + hk * s.head_stride_b;
+  pv.k = s.k_pool + off;
+  pv.v = s.v_pool + off;
+  pv.tok_off = pg * s.page_size;
+  pv.used = min(s.page_size, T - pv.tok_off);
+  pv.head_stride_b = 0;
+  return pv;
+}
+__device__ __forceinline__ PageView lane_page_view(const DescSrc& s, const DescLanes& L, int,
+                                                   int, int i, int hk) {
+  const uint64_t k = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(L.khi, i) << 32) |
+                     (uint32_t)__builtin_amdgcn_readlane(L.klo, i);
+  const uint64_t v = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(L.vhi, i) << 32) |
+                     (uint32_t)__builtin_amdgcn_readlane(L.vlo, i);
+  const int hs = __builtin_amdgcn_readlane(L.head_stride, i);
+  const int64_t off = (int64_t)hk * hs * s.elem_bytes;
+  PageView pv;
+  pv.k = reinterpret_cast<const char*>(k) + off;
+  pv.v = reinterpret_cast<const char*>(v) + off;
+  pv.used = __builtin_amdgcn_readlane(L.used, i);
+  pv.tok_off = __builtin_amdgcn_readlane(L.tok_off, i);
+  pv.head_stride_b = 0;
+  return pv;
+}
+
+template <class Src> struct LanesOf;
+template <> struct LanesOf<PoolSrc> { using type = PoolLanes; };
+template <> struct LanesOf<DescSrc> { using type = DescLanes; };
+
+template <typename T, class Src, int FEAT, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src src) {
+  using Ops = MfmaOps<T>;
+  constexpr int NT = 64 * NW;
+  constexpr int kRow = 256;  // bytes per token row (128 dims x 2 B)
+  constexpr bool kMask = (FEAT & kFeatMask) != 0;
+  constexpr bool kCap = (FEAT & kFeatCap) != 0;
+  constexpr bool kCausal = (FEAT & kFeatCausal) != 0;
+
+  __shared__ Smem<NW, kMfmaRows, 128> sm;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int q4 = lane >> 4;
+  const int n = lane & 15;
+
+  const int split_local = blockIdx.x;
+  const int hk = blockIdx.y % p.Hkv;
+  const int qt = blockIdx.y / p.Hkv;
+  const int b = blockIdx.z;
+  const int tile = (b * p.Hkv + hk) * p.n_qtiles + qt;
+  const int S = p.S;
+  const int G = p.G;
+  const int r0 = qt * kMfmaRows;
+  const int nrows = min(kMfmaRows, G * S - r0);
+
+  // ---- this workgroup's page range -------------------------------------------
+  const int np = src.n_pages(b);
+  const int lo = min(p.lo, np);
+  const int hi = min(p.hi, np);
+  const int nsplit_launch = (hi - lo + p.pps - 1) / p.pps;
+  const int total = p.total_splits > 0 ? p.total_splits : nsplit_launch;
+  // split 0 publishes the tile's split count; a tile without pages gets
+  // zeros (HELM kv_cache.py:441-442), from split 0 in fused mode and from
+  // merge_splits_kernel otherwise
+  if (split_local == 0 && tid == 0) p.counts[tile] = total;
+  if (total == 0) {
+    if (p.fused && split_local == 0) {
+      for (int idx = tid; idx < nrows * 128; idx += NT) {
+        const int rr = r0 + idx / 128;
+        const int h = hk * G + rr / S, s = rr % S;
+        const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * 128 + idx % 128;
+        store_elem<T>(reinterpret_cast<char*>(p.out) + o_off * 2, 0.f);
+      }
+    }
+    return;
+  }
+  if (split_local >= nsplit_launch) return;
+  const int split = p.split_base + split_local;
+  const int pg0 = lo + split_local * p.pps;
+  const int npg = min(pg0 + p.pps, hi) - pg0;  // 1..kMfmaMaxPps
+
+  // page records first: their latency overlaps the query load
+  const typename LanesOf<Src>::type lanes = lane_pages(src, b, pg0, npg, lane);
+
+  // ---- query operand: row n of the tile at dim chunks 4i + q4 ---------------
+  const bool row_ok = n < nrows;
+  const int rr = r0 + (row_ok ? n : 0);
+  const int g_row = rr / S;
+  const int s_row = rr % S;
+  mf_u32x4 qop[4];
+  {
+    const int h = hk * G + g_row;
+    const char* qp = reinterpret_cast<const char*>(p.q) +
+                     ((int64_t)(b * p.Hq + h) * S + s_row) * kRow;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qp + 16 * (4 * i + q4));
+      qop[i] = row_ok ? mf_u32x4{v.x, v.y, v.z, v.w} : mf_u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  const float* mrow = nullptr;
+  if constexpr (kMask)
+    mrow = p.mask + (int64_t)b * p.mask_bstride + (int64_t)(hk * G + g_row) * p.mask_hstride +
+           (int64_t)s_row * p.mask_qstride;
+
+  const float scale = p.scale;
+  const float cap = p.softcap;
+  const float inv_cap = kCap ? 1.f / cap : 0.f;
+
+  float m = -INFINITY;  // running max of row n (same in the 4 lanes of the row)
+  float lsum = 0.f;     // this lane's share of row n's weight sum
+  mf_f32x4 o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int bpp = p.bpp;
+  const int nblk = npg * bpp;
+  // lane offsets inside a block: K token tau(n) at chunk q4 (+64 B per i),
+  // V token q4 at dims 8n (+1 KiB per j)
+  const int voff_k = (4 * (n & 3) + (n >> 2)) * kRow + 16 * q4;
+  const int voff_v = q4 * kRow + 16 * n;
+
+  struct Blk {
+    mf_u32x4 k[4];
+    mf_u32x4 v[4];
+    float mk[4];
+    int ntok;   // valid tokens of the block (0: past the end)
+    int tok0;   // HELM token cursor of the block's first token
+  };
+
+  auto load_block = [&](int bi, Blk& B) {
+    const bool valid = bi < nblk;
+    const int pi = valid ? bi / bpp : 0;
+    const int sub = valid ? bi - pi * bpp : 0;
+    const PageView pv = lane_page_view(src, lanes, b, pg0 + pi, pi, hk);
+    const int tok_in = sub * kBlockTok;
+    const int ntok = valid ? sclamp(pv.used - tok_in, 0, kBlockTok) : 0;
+    B.ntok = ntok;
+    B.tok0 = pv.tok_off + tok_in;
+    const auto rk = make_rsrc(pv.k + tok_in * kRow, ntok * kRow);
+    const auto rv = make_rsrc(pv.v + tok_in * kRow, ntok * kRow);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) B.k[i] = buf_load16_nt(rk, voff_k + 64 * i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) B.v[j] = buf_load16_nt(rv, voff_v + 1024 * j);
+    if constexpr (kMask) {
+      // token 4r + q4 of the block for row n; clamped inside the page's tokens
+      const int last = max(ntok - 1, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        B.mk[r] = mrow[B.tok0 + min(4 * r + q4, last)];
+    }
+  };
+
+  auto compute_block = [&](const Blk& B) {
+    // scores of row n for tokens 4r + q4
+    mf_f32x4 sc = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc = Ops::mma(B.k[i], qop[i], sc);
+    float x[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = sc[r] * scale;
+      if constexpr (kCap) v = tanhf(v * inv_cap) * cap;
+      if constexpr (kMask) v += B.mk[r];
+      if constexpr (kCausal)
+        if (B.tok0 + 4 * r + q4 > s_row) v = -INFINITY;
+      x[r] = v;
+    }
+    if (B.ntok < kBlockTok) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (4 * r + q4 >= B.ntok) x[r] = -INFINITY;
+    }
+    const float bm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    if (__builtin_amdgcn_ballot_w64(bm > m + kMfmaSlack)) {
+      // refresh the row max (uniform across the row's four lanes)
+      float rm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+      rm = fmaxf(rm, __shfl_xor(rm, 32, 64));
+      const float mn = fmaxf(m, rm);
+      const float a = fexp(m - ((mn == -INFINITY) ? 0.f : mn));
+      lsum *= a;
+      m = mn;
+      // O rows of this lane are 4*q4 + r: fetch their factors
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float ar = __shfl(a, 4 * q4 + r, 64);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e][r] *= ar;
+      }
+    }
+    const float base = (m == -INFINITY) ? 0.f : m;
+    uint32_t h16[4], l16[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float w = fexp(x[r] - base);
+      lsum += w;
+      h16[r] = Ops::to16(w);
+      l16[r] = Ops::to16(w - Ops::from16(h16[r]));
+    }
+    const mf_u32x4 pop = mf_u32x4{h16[0] | (h16[1] << 16), h16[2] | (h16[3] << 16),
+                                  l16[0] | (l16[1] << 16), l16[2] | (l16[3] << 16)};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t a01 = pack_lo(B.v[0][w], B.v[1][w]);
+      const uint32_t a23 = pack_lo(B.v[2][w], B.v[3][w]);
+      const uint32_t b01 = pack_hi(B.v[0][w], B.v[1][w]);
+      const uint32_t b23 = pack_hi(B.v[2][w], B.v[3][w]);
+      o[2 * w] = Ops::mma(pop, mf_u32x4{a01, a23, a01, a23}, o[2 * w]);
+      o[2 * w + 1] = Ops::mma(pop, mf_u32x4{b01, b23, b01, b23}, o[2 * w + 1]);
+    }
+  };
+
+  // ---- main loop: three register buffers, two blocks' loads in flight ------
+  {
+    constexpr int W = NW;
+    const int nmine = nblk > wave ? (nblk - wave + W - 1) / W : 0;
+    Blk ba, bb, bc;
+    load_block(wave, ba);
+    load_block(wave + W, bb);
+    for (int k = 0; k < nmine; k += 3) {
+      load_block(wave + (k + 2) * W, bc);
+      compute_block(ba);
+      if (k + 1 >= nmine) break;
+      load_block(wave + (k + 3) * W, ba);
+      compute_block(bb);
+      if (k + 2 >= nmine) break;
+      load_block(wave + (k + 4) * W, bb);
+      compute_block(bc);
+    }
+  }
+
+  // ---- per-wave state to LDS ---------------------------------------------------
+  float lrow = lsum + __shfl_xor(lsum, 16, 64);
+  lrow += __shfl_xor(lrow, 32, 64);
+  if (q4 == 0) {
+    sm.m[wave][n] = m;
+    sm.l[wave][n] = lrow;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float* dst = &sm.o[wave][4 * q4 + r][8 * n];
+    *reinterpret_cast<float4*>(dst) = make_float4(o[0][r], o[1][r], o[2][r], o[3][r]);
+    *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4][r], o[5][r], o[6][r], o[7][r]);
+  }
+  __syncthreads();
+  split_epilogue<T, NW, kMfmaRows, 128>(sm, p, tid, tile, split, total, nrows, r0, b, hk);
+}
+
+}  // namespace helm

@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "attn_kernel.h"
+#include "attn_mfma.h"
 #include "helm_amd.h"
 
 namespace helm {
@@ -69,10 +70,17 @@ int env_int(const char* name, int dflt) {
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // ---- kernel choice and split planning -----------------------------------
+// Three kernels, chosen per call:
+//   mfma    — matrix-core kernel (attn_mfma.h): 16-bit q == KV type, D = 128,
+//             16-byte aligned operands; up to 16 query rows per tile;
+//   fast    — vector-ALU dot2 kernel: same types, G <= 8 rows per tile;
+//   generic — any D <= 256, fp32 or mixed q, 4 rows per tile.
+// HELM_AMD_KERNEL = mfma | valu | generic restricts the choice (valu: no
+// matrix cores; generic: the element-wise kernel only).
 struct Plan {
-  int fast, gm, epl, n_qtiles, bpp, pps, max_splits;
-  size_t ticket_bytes, ml_bytes, o_bytes;
-  size_t total() const { return ticket_bytes + ml_bytes + o_bytes; }
+  int mfma, fast, nw, fused, gm, rows, epl, n_qtiles, bpp, pps, max_splits;
+  size_t ticket_bytes, count_bytes, ml_bytes, o_bytes;
+  size_t total() const { return ticket_bytes + count_bytes + ml_bytes + o_bytes; }
 };
 
 int pick_epl(int D) {
@@ -81,16 +89,59 @@ int pick_epl(int D) {
   return 0;
 }
 
-// Smallest pages-per-split the automatic choice uses: every wave gets at
-// least two 16-token blocks.
-int min_pps(int bpp) { return std::max(1, (2 * kWaves + bpp - 1) / bpp); }
+// Smallest pages-per-split the automatic choice uses: every one of the nw
+// waves gets at least two 16-token blocks.
+int min_pps(int bpp, int nw) { return std::max(1, (2 * nw + bpp - 1) / bpp); }
+
+// Waves per workgroup of the matrix-core kernel (HELM_AMD_WAVES = 4 | 8).
+int mfma_waves() { return env_int("HELM_AMD_WAVES", 4) == 8 ? 8 : 4; }
+
+// Split merge.  merge_splits_kernel spreads the merge of every tile over
+// many workgroups; merging in-kernel (the last split of a tile to arrive
+// reads every partial) saves that launch but is bound by one CU's
+// load latency, so it is used only for tiles of at most kFusedMaxSplits
+// splits.  HELM_AMD_MERGE = fused | kernel forces one.
+constexpr int kFusedMaxSplits = 8;
+int fused_merge(int max_splits) {
+  const char* v = std::getenv("HELM_AMD_MERGE");
+  if (v && !std::strcmp(v, "kernel")) return 0;
+  if (v && !std::strcmp(v, "fused")) return 1;
+  return max_splits <= kFusedMaxSplits ? 1 : 0;
+}
+
+int kernel_choice() {
+  const char* v = std::getenv("HELM_AMD_KERNEL");
+  if (!v || !*v || !std::strcmp(v, "auto") || !std::strcmp(v, "mfma")) return 2;
+  if (!std::strcmp(v, "valu")) return 1;
+  return 0;
+}
 
 void size_plan(Plan& pl, int B, int Hkv, int D) {
   const size_t tiles = (size_t)B * Hkv * pl.n_qtiles;
   pl.ticket_bytes = align_up(tiles * 4, 256);
-  pl.ml_bytes = align_up(tiles * pl.max_splits * pl.gm * 2 * 4, 256);
-  pl.o_bytes = align_up(tiles * pl.max_splits * pl.gm * (size_t)D * 4, 256);
+  pl.count_bytes = align_up(tiles * 4, 256);
+  pl.ml_bytes = align_up(tiles * pl.max_splits * pl.rows * 2 * 4, 256);
+  pl.o_bytes = align_up(tiles * pl.max_splits * pl.rows * (size_t)D * 4, 256);
 }
+
+// Rows, tiles and the split limits of a kernel choice.
+void plan_shape(Plan& pl, int G, int q_len, int D, int max_tok_per_page) {
+  pl.nw = pl.mfma ? mfma_waves() : kWaves;
+  if (pl.mfma) {
+    pl.gm = kMfmaRows;
+    pl.rows = std::min(kMfmaRows, G * q_len);
+    pl.epl = 8;
+  } else {
+    pl.gm = pl.fast ? G : 4;
+    pl.rows = pl.gm;
+    pl.epl = pl.fast ? 8 : pick_epl(D);
+  }
+  pl.n_qtiles = (G * q_len + pl.gm - 1) / pl.gm;
+  pl.bpp = std::max(1, (max_tok_per_page + kBlockTok - 1) / kBlockTok);
+}
+
+int max_pps_of(const Plan& pl) { return pl.mfma ? kMfmaMaxPps : kMaxPps; }
+int max_splits_of(const Plan& pl) { return pl.mfma ? kMfmaMaxSplits : kMaxSplits; }
 
 // work_pages: pages one (sequence, head, tile) walks on average; max_pages:
 // the longest sequence (bounds the split count).
@@ -108,28 +159,32 @@ int make_plan(Plan& pl, int kv_dtype, int q_dtype, int B, int Hq, int Hkv,
     return fail(HELM_E_UNSUPPORTED,
                 "query dtype must equal the KV dtype or be float32");
   const int G = Hq / Hkv;
-  pl.fast = (kv_dtype == q_dtype && kv_dtype != HELM_F32 && D == 128 &&
-             G <= 8 && aligned16 && env_int("HELM_AMD_GENERIC", 0) == 0)
-                ? 1 : 0;
-  pl.gm = pl.fast ? G : 4;
-  pl.epl = pl.fast ? 8 : pick_epl(D);
-  pl.n_qtiles = (G * q_len + pl.gm - 1) / pl.gm;
-  pl.bpp = std::max(1, (max_tok_per_page + kBlockTok - 1) / kBlockTok);
+  const int choice = kernel_choice();
+  const bool same16 = kv_dtype == q_dtype && kv_dtype != HELM_F32 && D == 128 && aligned16;
+  pl.mfma = (choice >= 2 && same16) ? 1 : 0;
+  pl.fast = (!pl.mfma && choice >= 1 && same16 && G <= 8) ? 1 : 0;
+  plan_shape(pl, G, q_len, D, max_tok_per_page);
   int pps = pps_req > 0 ? pps_req : env_int("HELM_AMD_PPS", 0);
   if (pps <= 0) {
     const double units = (double)B * Hkv * pl.n_qtiles;
-    const int target = env_int("HELM_AMD_WG_PER_CU", 2) * device_cus();
+    // one workgroup per CU: longer splits mean fewer partials to merge
+    const int target = env_int("HELM_AMD_WG_PER_CU", 1) * device_cus();
     const double splits = std::max(1.0, target / units);
     pps = (int)std::ceil(std::max(1.0, avg_pages) / splits);
-    pps = std::max(pps, min_pps(pl.bpp));
+    pps = std::max(pps, min_pps(pl.bpp, pl.nw));
+    pps = std::min(pps, max_pps_of(pl));
   }
-  pps = std::max(pps, (max_pages + kMaxSplits - 1) / kMaxSplits);
-  if (pps > kMaxPps)
+  pps = std::min(pps, max_pps_of(pl));
+  pps = std::max(pps, (max_pages + max_splits_of(pl) - 1) / max_splits_of(pl));
+  if (pps > max_pps_of(pl))
     return fail(HELM_E_UNSUPPORTED,
-                "context longer than kMaxSplits * kMaxPps pages per sequence");
+                "context longer than the split limit of the chosen kernel");
   pl.pps = std::max(pps, 1);
   pl.max_splits = std::max(1, (max_pages + pl.pps - 1) / pl.pps);
+  pl.fused = fused_merge(pl.max_splits);
   size_plan(pl, B, Hkv, D);
+  // the in-kernel merge addresses the partials with 31-bit byte offsets
+  if (pl.o_bytes >= 0x7ffffff0u) pl.fused = 0;
   return HELM_OK;
 }
 
@@ -162,7 +217,7 @@ void fill_params(AttnParams& a, const Plan& pl, const void* q, void* out,
   a.G = Hq / Hkv;
   a.S = q_len;
   a.D = D;
-  a.rows_per_tile = pl.gm;
+  a.rows_per_tile = pl.rows;
   a.n_qtiles = pl.n_qtiles;
   a.scale = scale;
   a.softcap = softcap;
@@ -180,8 +235,10 @@ void fill_params(AttnParams& a, const Plan& pl, const void* q, void* out,
   a.max_splits = pl.max_splits;
   a.full_d = 0;
   a.tickets = reinterpret_cast<uint32_t*>(ws);
-  a.ws_ml = reinterpret_cast<float*>(ws + pl.ticket_bytes);
-  a.ws_o = reinterpret_cast<float*>(ws + pl.ticket_bytes + pl.ml_bytes);
+  a.counts = reinterpret_cast<int*>(ws + pl.ticket_bytes);
+  a.fused = pl.fused;
+  a.ws_ml = reinterpret_cast<float*>(ws + pl.ticket_bytes + pl.count_bytes);
+  a.ws_o = reinterpret_cast<float*>(ws + pl.ticket_bytes + pl.count_bytes + pl.ml_bytes);
 }
 
 hipError_t dispatch(const LaunchSpec& s, hipStream_t st) {
@@ -191,6 +248,26 @@ hipError_t dispatch(const LaunchSpec& s, hipStream_t st) {
     case HELM_F32: return launch_attn_f32(s, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+// Combines the split partials of every tile into the output (after the
+// split kernels, on the same stream).
+hipError_t launch_merge(const LaunchSpec& s, int B, int Hkv, hipStream_t st) {
+  if (s.p.fused) return hipSuccess;
+  const dim3 grid(B * Hkv * s.p.n_qtiles, s.p.rows_per_tile);
+  switch (s.q_dtype) {
+    case HELM_F16:
+      hipLaunchKernelGGL(merge_splits_kernel<f16_t>, grid, dim3(kThreads), 0, st, s.p);
+      break;
+    case HELM_BF16:
+      hipLaunchKernelGGL(merge_splits_kernel<bf16_t>, grid, dim3(kThreads), 0, st, s.p);
+      break;
+    case HELM_F32:
+      hipLaunchKernelGGL(merge_splits_kernel<float>, grid, dim3(kThreads), 0, st, s.p);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 // ---- page append kernel -----------------------------------------------------
@@ -265,7 +342,8 @@ using namespace helm;
 struct helm_engine {
   int device = 0;
   hipStream_t copy = nullptr;
-  // workspace (tickets zeroed at allocation, left zero by every call)
+  // workspace: tickets (zeroed at allocation, left zero by every call),
+  // split counts and partials
   char* ws = nullptr;
   size_t ws_bytes = 0;
   // staging ring for host pages
@@ -465,14 +543,16 @@ size_t helm_query_workspace_bytes(int B, int Hq, int Hkv, int q_len, int D,
     return 0;
   const int G = Hq / Hkv;
   size_t best = 0;
-  for (int gm : {G <= 8 ? G : 4, 4}) {
+  // the largest of the plans any kernel choice can make for this shape
+  for (int kind = 0; kind < 3; ++kind) {
     Plan pl{};
-    pl.gm = gm;
-    pl.n_qtiles = (G * q_len + gm - 1) / gm;
-    pl.bpp = std::max(1, (page_size + kBlockTok - 1) / kBlockTok);
-    int pps = pages_per_split > 0 ? std::min(pages_per_split, kMaxPps)
-                                  : min_pps(pl.bpp);
-    pps = std::max(pps, (max_pages + kMaxSplits - 1) / kMaxSplits);
+    pl.mfma = kind == 2;
+    pl.fast = kind == 1 && G <= 8;
+    plan_shape(pl, G, q_len, D, page_size);
+    int pps = pages_per_split > 0 ? std::min(pages_per_split, max_pps_of(pl))
+                                  : min_pps(pl.bpp, 4);
+    pps = std::min(pps, max_pps_of(pl));
+    pps = std::max(pps, (max_pages + max_splits_of(pl) - 1) / max_splits_of(pl));
     pl.max_splits = std::max(1, (max_pages + pps - 1) / pps);
     size_plan(pl, B, Hkv, D);
     best = std::max(best, pl.total());
@@ -529,9 +609,15 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
   s.epl = pl.epl;
   s.gm = pl.gm;
   s.fast = pl.fast;
+  s.mfma = pl.mfma;
+  s.nw = pl.nw;
+  s.feat = (mask ? kFeatMask : 0) | (softcap > 0.f ? kFeatCap : 0);
   s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.n_qtiles, B);
-  hipError_t e = dispatch(s, reinterpret_cast<hipStream_t>(stream));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e = dispatch(s, st);
   if (e != hipSuccess) return hip_fail(e, "paged_attn launch");
+  e = launch_merge(s, B, Hkv, st);
+  if (e != hipSuccess) return hip_fail(e, "merge launch");
   return HELM_OK;
 }
 
@@ -660,15 +746,15 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
                      std::max(max_pages, 1), (double)n_all / B, 0, al);
   if (rc != HELM_OK) return rc;
   if (n_host) {
-    // every launch owns whole splits; keep the call within kMaxSplits
+    // every launch owns whole splits; keep the call within the split limit
     std::vector<std::pair<int, int>> ranges;
     for (const Launch& L : launches) ranges.push_back({L.lo, L.hi});
-    while (chained_splits(ranges, pl.pps) > kMaxSplits) {
-      if (pl.pps >= kMaxPps)
+    while (chained_splits(ranges, pl.pps) > max_splits_of(pl)) {
+      if (pl.pps >= max_pps_of(pl))
         return fail(HELM_E_UNSUPPORTED, "too many staged chunks for one call");
-      pl.pps = std::min(kMaxPps, pl.pps * 2);
+      pl.pps = std::min(max_pps_of(pl), pl.pps * 2);
     }
-    if ((int)launches.size() > kMaxSplits)
+    if ((int)launches.size() > max_splits_of(pl))
       return fail(HELM_E_UNSUPPORTED, "too many staged chunks for one call");
   }
   int total_splits = 0;
@@ -679,7 +765,9 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   }
   pl.max_splits = n_host ? std::max(1, total_splits)
                          : std::max(1, (max_pages + pl.pps - 1) / pl.pps);
+  pl.fused = fused_merge(pl.max_splits);
   size_plan(pl, B, Hkv, D);
+  if (pl.o_bytes >= 0x7ffffff0u) pl.fused = 0;
   rc = engine_ensure_ws(eng, pl.total(), st);
   if (rc != HELM_OK) return rc;
 
@@ -707,11 +795,17 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   s.epl = pl.epl;
   s.gm = pl.gm;
   s.fast = pl.fast;
+  s.mfma = pl.mfma;
+  s.nw = pl.nw;
+  s.feat = (mask ? kFeatMask : 0) | (softcap > 0.f ? kFeatCap : 0) |
+           (causal ? kFeatCausal : 0);
 
   if (!n_host) {
     s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.n_qtiles, B);
     hipError_t e = dispatch(s, st);
     if (e != hipSuccess) return hip_fail(e, "stream_attn launch");
+    e = launch_merge(s, B, Hkv, st);
+    if (e != hipSuccess) return hip_fail(e, "merge launch");
     return engine_mark_upload_consumed(eng, st);
   }
 
@@ -744,6 +838,8 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
       eng->slot_used[slot] = 1;
     }
   }
+  hipError_t e = launch_merge(s, 1, Hkv, st);
+  if (e != hipSuccess) return hip_fail(e, "merge launch");
   return engine_mark_upload_consumed(eng, st);
 }
 

@@ -32,6 +32,49 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+class PreparedDecode:
+    """helm_paged_decode_attn with its argument list built once, for callers
+    that issue the same shape every step (serving loops, benchmarks): one
+    ctypes call per ``run``.  ``run(k_pool, v_pool)`` may pass another pool of
+    identical shape and strides (rotated pools); q, page table, lengths and
+    out stay the ones given to ``prepare_paged_decode``."""
+
+    def __init__(self, args: list, pool_index: int, fn):
+        self._args = args
+        self._pool_index = pool_index
+        self._fn = fn
+        self.out = None
+
+    def run(self, k_pool: Optional[torch.Tensor] = None,
+            v_pool: Optional[torch.Tensor] = None) -> torch.Tensor:
+        a = self._args
+        if k_pool is not None:
+            a = list(a)
+            a[self._pool_index] = k_pool.data_ptr()
+            a[self._pool_index + 1] = v_pool.data_ptr()
+        rc = self._fn(*a)
+        if rc:
+            _native.check("helm_paged_decode_attn", rc)
+        return self.out
+
+
+def prepare_paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                         page_table: torch.Tensor, seq_lens: torch.Tensor,
+                         max_pages: Optional[int] = None, total_pages: int = 0,
+                         scale: Optional[float] = None, softcap: Optional[float] = None,
+                         out: Optional[torch.Tensor] = None,
+                         pages_per_split: int = 0) -> PreparedDecode:
+    """Validates the shapes once and returns a PreparedDecode bound to torch's
+    current stream on q's device (same arguments as paged_decode_attention,
+    without a mask)."""
+    args, keep = _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages,
+                              scale, softcap, None, out, pages_per_split)
+    prep = PreparedDecode(args, 2, _native.load().helm_paged_decode_attn)
+    prep.out = keep["out"]
+    prep._keep = keep
+    return prep
+
+
 def paged_decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                            page_table: torch.Tensor, seq_lens: torch.Tensor,
                            max_pages: Optional[int] = None, total_pages: int = 0,
@@ -45,6 +88,15 @@ def paged_decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
     page_table: int32 [B, >=max_pages] slot ids; seq_lens: int32 [B] tokens
     (device).  attention_mask: additive fp32-convertible [B|1, 1|Hq, q_len|1,
     >=max tokens].  Returns out [B,Hq,q_len,D] in q's dtype."""
+    args, keep = _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages,
+                              scale, softcap, attention_mask, out, pages_per_split)
+    _native.call("helm_paged_decode_attn", *args)
+    return keep["out"]
+
+
+def _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages, scale, softcap,
+                 attention_mask, out, pages_per_split):
+    """Checks the operands and returns (C-ABI argument list, tensors to keep alive)."""
     if q.device.type != "cuda":
         raise RuntimeError("paged_decode_attention needs HIP tensors")
     B, Hq, S, D = q.shape
@@ -57,6 +109,8 @@ def paged_decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
         raise ValueError("pool pages need dense [page, D] rows")
     if page_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
         raise TypeError("page_table and seq_lens must be int32")
+    if page_table.dim() != 2 or page_table.size(0) != B or seq_lens.numel() != B:
+        raise ValueError("page_table must be [B, >=max_pages] and seq_lens [B]")
     if max_pages is None:
         max_pages = page_table.size(1)
     if scale is None:
@@ -79,10 +133,10 @@ def paged_decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
     lib = _native.load()
     need = lib.helm_query_workspace_bytes(B, Hq, Hkv, S, D, max_pages, P, pages_per_split)
     ws = workspace(q.device, need)
-    _native.call("helm_paged_decode_attn", q.data_ptr(), out.data_ptr(), k_pool.data_ptr(),
-                 v_pool.data_ptr(), k_pool.stride(0), k_pool.stride(1), page_table.data_ptr(),
-                 page_table.stride(0), seq_lens.data_ptr(), B, Hq, Hkv, S, D, P, max_pages,
-                 total_pages, float(scale), float(softcap) if softcap else 0.0, mask_ptr, mbs,
-                 mhs, mqs, kcode, qcode, pages_per_split, ws.data_ptr(), ws.numel(),
-                 _engine.stream_ptr(q.device))
-    return out
+    args = [q.data_ptr(), out.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0),
+            k_pool.stride(1), page_table.data_ptr(), page_table.stride(0), seq_lens.data_ptr(), B,
+            Hq, Hkv, S, D, P, max_pages, total_pages, float(scale),
+            float(softcap) if softcap else 0.0, mask_ptr, mbs, mhs, mqs, kcode, qcode,
+            pages_per_split, ws.data_ptr(), ws.numel(), _engine.stream_ptr(q.device)]
+    keep = {"q": q, "out": out, "mask": m, "ws": ws, "table": page_table, "lens": seq_lens}
+    return args, keep

@@ -103,9 +103,10 @@ void* helm_engine_copy_stream(helm_engine* eng);
 
 /* ---- attention ------------------------------------------------------------ */
 
-/* Workspace (bytes) helm_paged_decode_attn needs for this shape.  The first
- * helm_ticket_bytes(...) bytes of the workspace are merge tickets: they must
- * be zero before the first call and every completed call leaves them zero. */
+/* Workspace (bytes) helm_paged_decode_attn needs for this shape: per-tile
+ * merge tickets and split counts, and the split partials (m, l, o[D]) of
+ * every query row.  It must be zero before its first use; every completed
+ * call leaves the ticket region zero again. */
 size_t helm_query_workspace_bytes(int B, int Hq, int Hkv, int q_len, int D,
                                   int max_pages, int page_size,
                                   int pages_per_split);

@@ -27,6 +27,18 @@ DEV = torch.device("cuda:0")
 TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-5}
 
 
+@pytest.fixture(params=[("auto", "auto"), ("auto", "fused"), ("auto", "kernel"),
+                        ("valu", "auto"), ("valu", "fused")],
+                ids=lambda p: f"{p[0]}-{p[1]}")
+def kernel(request, monkeypatch):
+    """Runs a test on the matrix-core kernel (the automatic choice for 16-bit
+    D = 128 pages) and on the vector-ALU kernels, with the split merge chosen
+    automatically, forced in-kernel (fused) and forced to merge_splits_kernel."""
+    monkeypatch.setenv("HELM_AMD_KERNEL", request.param[0])
+    monkeypatch.setenv("HELM_AMD_MERGE", request.param[1])
+    return request.param
+
+
 def _pool_reference(case, w, b, mask=None, softcap=None):
     """fp64 oracle for sequence b of a pool case (gathers its pages on CPU)."""
     T = case["lens_list"][b]
@@ -56,7 +68,7 @@ def _check_pool(w, case, out, atol=None):
     ("qwen3-8b-32k", None),           # full 32k Qwen3-8B shape, bf16
     ("llama2-13b-128k-offload75", 8192),
 ])
-def test_pool_decode_matches_fp64(name, T):
+def test_pool_decode_matches_fp64(name, T, kernel):
     w = W.WORKLOADS[name]
     lens = [T] * w.B if T else None
     case = W.make_pool_case(w, seed=17, device=DEV, lens=lens)
@@ -66,7 +78,7 @@ def test_pool_decode_matches_fp64(name, T):
     print(name, "max err", _check_pool(w, case, out))
 
 
-def test_pool_decode_ragged_batch_full_size():
+def test_pool_decode_ragged_batch_full_size(kernel):
     w = W.WORKLOADS["qwen3-14b-ragged-b8"]
     case = W.make_pool_case(w, seed=3, device=DEV)
     out = paged_decode_attention(case["q"], case["k_pool"], case["v_pool"], case["table"],
@@ -77,7 +89,7 @@ def test_pool_decode_ragged_batch_full_size():
 
 
 @pytest.mark.parametrize("pps", [1, 3, 8, 64, 256])
-def test_pool_decode_split_invariance(pps):
+def test_pool_decode_split_invariance(pps, kernel):
     """Any split count gives the same attention (merge correctness)."""
     w = W.WORKLOADS["qwen3-8b-32k"]
     case = W.make_pool_case(w, seed=5, device=DEV, lens=[3000])
@@ -87,7 +99,7 @@ def test_pool_decode_split_invariance(pps):
     _check_pool(w, case, out)
 
 
-def test_pool_decode_page_table_permutation_invariance():
+def test_pool_decode_page_table_permutation_invariance(kernel):
     """Full-size property: relocating pages (new table, moved slots) leaves
     the output bit-identical for the same split plan."""
     w = W.WORKLOADS["qwen3-8b-32k"]
@@ -105,7 +117,7 @@ def test_pool_decode_page_table_permutation_invariance():
     assert torch.equal(out1, out2)
 
 
-def test_pool_decode_mask_and_softcap():
+def test_pool_decode_mask_and_softcap(kernel):
     w = W.WORKLOADS["qwen3-8b-32k"]
     case = W.make_pool_case(w, seed=21, device=DEV, lens=[1000])
     g = torch.Generator().manual_seed(0)
@@ -147,7 +159,7 @@ def _paged(sizes, H, D, kvh, dtype, seed, device=DEV):
     ([5, 16, 16], 40, 8, 128, torch.bfloat16), ([7, 9], 6, 2, 96, torch.float32),
 ])
 @pytest.mark.parametrize("masked", [False, True])
-def test_streaming_matches_oracle(sizes, H, kvh, D, dtype, masked):
+def test_streaming_matches_oracle(sizes, H, kvh, D, dtype, masked, kernel):
     q, pages, ks, vs = _paged(sizes, H, D, kvh, dtype, seed=sum(sizes) * 7 + H)
     T = sum(sizes)
     mask = None
@@ -217,7 +229,7 @@ def test_streaming_fully_masked_page_and_all_masked():
     torch.testing.assert_close(out.cpu(), helm, atol=1e-5, rtol=0)
 
 
-def test_streaming_prefill_chunk_causal_mask():
+def test_streaming_prefill_chunk_causal_mask(kernel):
     """q_len > 1 (later prefill chunk) with the pipeline's chunk mask
     (pipeline_runtime.py:94-113): queries at [past, past+n) see keys <= own."""
     q_, pages, ks, vs = _paged([16, 16, 16, 5], 8, 64, 4, torch.float16, seed=4)
@@ -234,7 +246,7 @@ def test_streaming_prefill_chunk_causal_mask():
     assert np.abs(out.cpu().double().numpy() - ref).max() <= 2e-3
 
 
-def test_streaming_path1_causal_top_left():
+def test_streaming_path1_causal_top_left(kernel):
     """All-GPU, no mask, q_len > 1: HELM's Path 1 SDPA is_causal (top-left)."""
     q_, pages, ks, vs = _paged([8, 8], 4, 16, 2, torch.float32, seed=6)
     q = torch.randn(1, 4, 5, 16, generator=torch.Generator().manual_seed(6))
@@ -254,3 +266,53 @@ def test_streaming_batched_query_over_batched_pages():
     assert out.shape == (2, 4, 1, 16)
     ref = A.attention_fp64(q, k, v)
     np.testing.assert_allclose(out.cpu().double().numpy(), ref, atol=1e-5)
+
+
+@pytest.mark.parametrize("Hq,Hkv,S,dtype", [(40, 2, 1, torch.bfloat16), (8, 4, 16, torch.bfloat16),
+                                            (4, 4, 5, torch.float16)])
+def test_streaming_d128_row_tiles_causal_and_chunk_mask(Hq, Hkv, S, dtype, kernel):
+    """D = 128 with more than 16 query rows per KV head (several row tiles):
+    a later prefill chunk under the pipeline's chunk mask, and Path 1's
+    top-left causal mask."""
+    g = torch.Generator().manual_seed(Hq * 7 + S)
+    sizes = [16, 16, 16, 16, 9]
+    T = sum(sizes)
+    ks = [torch.randn(1, Hkv, n, 128, generator=g).to(dtype) for n in sizes]
+    vs = [torch.randn(1, Hkv, n, 128, generator=g).to(dtype) for n in sizes]
+    pages, start = [], 0
+    for i, (k, v) in enumerate(zip(ks, vs)):
+        pages.append(_page(k.to(DEV), v.to(DEV), i, start))
+        start += k.size(2)
+    q = torch.randn(1, Hq, S, 128, generator=g).to(dtype)
+    K, V = torch.cat(ks, 2).float(), torch.cat(vs, 2).float()
+    past = T - S
+    mn = torch.finfo(torch.float32).min
+    mask = torch.where(torch.arange(T)[None, :] <= past + torch.arange(S)[:, None],
+                       torch.zeros(()), torch.full((), mn))[None, None]
+    out = perform_streaming_attention(q.to(DEV), pages, attention_mask=mask.to(DEV))
+    ref = A.attention_fp64(q.float(), K, V, mask=mask.numpy())
+    assert np.abs(out.cpu().double().numpy() - ref).max() <= TOL[dtype]
+    if S > 1:
+        out = perform_streaming_attention(q.to(DEV), pages)        # Path 1: is_causal
+        ref = A.attention_fp64(q.float(), K, V, causal=True)
+        assert np.abs(out.cpu().double().numpy() - ref).max() <= TOL[dtype]
+
+
+def test_kernels_agree_at_full_size():
+    """The matrix-core and vector-ALU kernels give the same attention (to
+    fp32 rounding of their different summation orders) on the full 32k
+    Qwen3-8B shape."""
+    import os
+    w = W.WORKLOADS["qwen3-8b-32k"]
+    case = W.make_pool_case(w, seed=31, device=DEV)
+    outs = {}
+    for kind in ("auto", "valu"):
+        os.environ["HELM_AMD_KERNEL"] = kind
+        try:
+            o = paged_decode_attention(case["q"], case["k_pool"], case["v_pool"], case["table"],
+                                       case["lens"], max_pages=case["max_pages"])
+        finally:
+            os.environ.pop("HELM_AMD_KERNEL", None)
+        torch.cuda.synchronize()
+        outs[kind] = o.float()
+    assert (outs["auto"] - outs["valu"]).abs().max().item() <= 2 ** -7

@@ -51,10 +51,14 @@ def test_workspace_sizing_host_only():
     # Qwen3-8B shape, 2048 pages of 16 tokens
     n = lib.helm_query_workspace_bytes(1, 32, 8, 1, 128, 2048, 16, 0)
     assert n > 0
-    # grows with pages up to the per-tile split cap (256 splits), then flat;
-    # invalid shapes give 0
-    assert lib.helm_query_workspace_bytes(1, 32, 8, 1, 128, 1024, 16, 0) < n
-    assert lib.helm_query_workspace_bytes(1, 32, 8, 1, 128, 65536, 16, 0) == n
+    # grows with the context and stays a small fraction of the KV bytes it
+    # serves (2 * 8 heads * 16 tokens * 128 dims * 2 B per page); invalid
+    # shapes give 0
+    sizes = [lib.helm_query_workspace_bytes(1, 32, 8, 1, 128, p, 16, 0)
+             for p in (256, 1024, 2048, 8192, 65536)]
+    assert sizes == sorted(sizes) and sizes[2] == n
+    for pages, ws in zip((256, 1024, 2048, 8192, 65536), sizes):
+        assert ws <= 0.05 * pages * 65536 + (1 << 20)
     assert lib.helm_query_workspace_bytes(1, 30, 8, 1, 128, 2048, 16, 0) == 0
 
 
