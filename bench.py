@@ -54,22 +54,30 @@ def parse():
     ap.add_argument("--pps", type=int, default=0, help="pages per split (0 = auto)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (PMC byte-count calibration)")
+    ap.add_argument("--all", action="store_true",
+                    help="also measure every benchmark configuration (gpurun_out/bench_all.json)")
     return ap.parse_args()
 
 
-def gpu_headline(args, torch, W, paged):
-    w = W.WORKLOADS["qwen3-8b-32k"]
+def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=None, steps=None):
+    """Pool-layout decode attention of one workload, all pages resident.
+    Pools are rotated so that at least 1 GiB of KV passes between two reads
+    of the same pool (the 256 MB Infinity Cache cannot serve it)."""
+    w = W.WORKLOADS[name]
     dev = torch.device("cuda:0")
-    case = W.make_pool_case(w, seed=1, device=dev)
+    case = W.make_pool_case(w, seed=seed, device=dev)
+    if n_pools is None:
+        pool_b = case["pool"].numel() * case["pool"].element_size()
+        n_pools = max(args.pools, min(128, -(-(1 << 30) // pool_b)))
     pools = [case["pool"]] + [torch.empty_like(case["pool"]).copy_(case["pool"])
-                              for _ in range(args.pools - 1)]
+                              for _ in range(n_pools - 1)]
     lens = case["lens_list"]
     alg = W.algorithmic_bytes(w, lens)
     # argument list built once: a step is one C-ABI call (decode kernel +
     # split merge) on torch's current stream, over the next rotated pool
     prep = paged.prepare_paged_decode(case["q"], case["k_pool"], case["v_pool"], case["table"],
                                       case["lens"], max_pages=case["max_pages"],
-                                      pages_per_split=args.pps)
+                                      total_pages=sum(case["n_pages"]), pages_per_split=args.pps)
     views = [(p[:, 0], p[:, 1]) for p in pools]
 
     def step(i):
@@ -78,21 +86,22 @@ def gpu_headline(args, torch, W, paged):
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    steps = steps or args.steps
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         step(i)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_events = e0.elapsed_time(e1)
-    per_call_s = ms_events / 1e3 / args.steps
+    per_call_s = ms_events / 1e3 / steps
     return {
         "w": w, "case": case, "alg_bytes": alg, "kv_bytes": W.kv_bytes(w, lens),
-        "per_call_s": per_call_s, "wall_ms_per_step": wall * 1e3 / args.steps,
-        "ms_per_step": ms_events / args.steps,
+        "per_call_s": per_call_s, "wall_ms_per_step": wall * 1e3 / steps,
+        "ms_per_step": ms_events / steps, "pools": n_pools, "lens": lens, "prep": prep,
     }
 
 
@@ -112,17 +121,19 @@ def h2d_peak(torch):
     return best
 
 
-def gpu_offload(args, torch, W):
-    """Oldest 50% of the 32k context in pinned host pages, streamed through
-    the engine's staging ring while the resident half is attended."""
+def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=None):
+    """The oldest offload_frac of the context in pinned host pages, streamed
+    through the engine's staging ring while the resident pages are attended."""
     from helm_amd import _native
     from helm_amd.runtime import engine
-    w = W.WORKLOADS["qwen3-8b-32k-offload50"]
+    w = W.WORKLOADS[name]
     dev = torch.device("cuda:0")
-    case = W.make_pool_case(w, seed=2, device=dev)
+    case = W.make_pool_case(w, seed=seed, device=dev)
     n = case["n_pages"][0]
     n_host = int(n * w.offload_frac)
-    slot_b = 2 * w.Hkv * w.page_size * w.D * 2
+    es = torch.tensor([], dtype=w.dtype).element_size()
+    slot_b = 2 * w.Hkv * w.page_size * w.D * es
+    kcode = _native.dtype_code(w.dtype)
     host = torch.empty((n_host, 2, w.Hkv, w.page_size, w.D), dtype=w.dtype).pin_memory()
     table = case["table_cpu"][0, :n].long()
     host.copy_(case["pool"][table[:n_host].to(dev)].cpu())
@@ -144,18 +155,19 @@ def gpu_offload(args, torch, W):
     def call():
         _native.call("helm_stream_attn", eng, case["q"].data_ptr(), out.data_ptr(), 1, w.Hq,
                      w.Hkv, 1, w.D, _native.ptr(pages), _native.ptr(seq_off), case["scale"], 0.0,
-                     None, 0, 0, 0, 0, _native.HELM_BF16, _native.HELM_BF16, stream.cuda_stream)
+                     None, 0, 0, 0, 0, kcode, kcode, stream.cuda_stream)
 
     for _ in range(3):
         call()
     torch.cuda.synchronize()
+    steps = steps or args.offload_steps
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _ in range(args.offload_steps):
+    for _ in range(steps):
         call()
     e1.record(stream)
     torch.cuda.synchronize()
-    per = e0.elapsed_time(e1) / 1e3 / args.offload_steps
+    per = e0.elapsed_time(e1) / 1e3 / steps
     host_bytes = n_host * slot_b
     peak = h2d_peak(torch)
     # parity spot check of this exact configuration against the oracle
@@ -169,7 +181,34 @@ def gpu_offload(args, torch, W):
         "host_link_GBs": host_bytes / per / 1e9, "measured_h2d_GBs": peak,
         "frac_of_measured_h2d": host_bytes / per / 1e9 / peak,
         "pcie5_x16_theoretical_GBs": PCIE5_X16_GBS, "max_abs_err_vs_fp64": err,
+        "resident_bytes": (n - n_host) * slot_b,
     }
+
+
+def all_configs(args, torch, W, paged):
+    """Every decode-attention configuration of the benchmark set, one line
+    each on stderr and all of them in gpurun_out/bench_all.json."""
+    rows = []
+    for name, seed in (("qwen3-0.6b-2k", 0), ("qwen3-8b-32k", 1), ("qwen3-14b-ragged-b8", 3)):
+        h = gpu_headline(args, torch, W, paged, name=name, seed=seed, steps=100)
+        gbs = h["alg_bytes"] / h["per_call_s"] / 1e9
+        r = {"workload": name, "us_per_call": h["per_call_s"] * 1e6, "GBs": gbs,
+             "hbm_frac": gbs / HBM_PEAK_GBS, "alg_bytes": h["alg_bytes"], "pools": h["pools"],
+             "total_tokens": sum(h["lens"])}
+        rows.append(r)
+        log(json.dumps(r))
+        del h
+        torch.cuda.empty_cache()
+    for name, seed in (("qwen3-8b-32k-offload50", 2), ("llama2-13b-128k-offload75", 4)):
+        o = gpu_offload(args, torch, W, name=name, seed=seed, steps=10)
+        o["workload"] = name
+        rows.append(o)
+        log(json.dumps(o))
+        torch.cuda.empty_cache()
+    os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
+    with open(os.path.join(ROOT, "gpurun_out", "bench_all.json"), "w") as f:
+        json.dump(rows, f, indent=1)
+    return rows
 
 
 def cpu_baseline(args, torch, W):
@@ -231,6 +270,9 @@ def main():
         torch.cuda.synchronize()
         log("copy calibration: 3 x 1 GiB device copies done")
 
+    if args.all:
+        all_configs(args, torch, W, paged)
+
     off = None
     if not args.no_offload:
         log("offload: qwen3-8b-32k, oldest 50% in pinned host")
@@ -246,7 +288,7 @@ def main():
         log(json.dumps(cpu))
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "paged_attn_qwen3-8b-32k_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", "paged_decode_qwen3-8b-32k_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")

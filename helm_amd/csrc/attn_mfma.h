@@ -41,6 +41,10 @@ constexpr int kMfmaRows = 16;     // query rows per tile (MFMA M dimension)
 constexpr int kMfmaMaxPps = 64;   // pages per split: page records live one per lane
 constexpr int kMfmaMaxSplits = 4096;
 constexpr float kMfmaSlack = 8.f;
+#ifndef HELM_MFMA_NBUF
+#define HELM_MFMA_NBUF 3
+#endif
+constexpr int kMfmaBufs = HELM_MFMA_NBUF;  // register buffers of the block pipeline
 
 enum MfmaFeat { kFeatMask = 1, kFeatCap = 2, kFeatCausal = 4 };
 
@@ -344,22 +348,22 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
     }
   };
 
-  // ---- main loop: three register buffers, two blocks' loads in flight ------
+  // ---- main loop: a ring of kMfmaBufs register buffers, kMfmaBufs - 1
+  // blocks' loads in flight while one block is computed ----------------------
   {
     constexpr int W = NW;
+    constexpr int NB = kMfmaBufs;
     const int nmine = nblk > wave ? (nblk - wave + W - 1) / W : 0;
-    Blk ba, bb, bc;
-    load_block(wave, ba);
-    load_block(wave + W, bb);
-    for (int k = 0; k < nmine; k += 3) {
-      load_block(wave + (k + 2) * W, bc);
-      compute_block(ba);
-      if (k + 1 >= nmine) break;
-      load_block(wave + (k + 3) * W, ba);
-      compute_block(bb);
-      if (k + 2 >= nmine) break;
-      load_block(wave + (k + 4) * W, bb);
-      compute_block(bc);
+    Blk buf[NB];
+#pragma unroll
+    for (int i = 0; i < NB - 1; ++i) load_block(wave + i * W, buf[i]);
+    for (int k = 0; k < nmine; k += NB) {
+#pragma unroll
+      for (int u = 0; u < NB; ++u) {
+        if (k + u >= nmine) break;
+        load_block(wave + (k + u + NB - 1) * W, buf[(u + NB - 1) % NB]);
+        compute_block(buf[u]);
+      }
     }
   }
 

@@ -350,8 +350,6 @@ struct helm_engine {
   char* ring = nullptr;
   size_t chunk_bytes = 0;
   int ring_slots = 0;
-  std::vector<hipEvent_t> copy_done, slot_free;
-  std::vector<int> slot_used;
   int next_slot = 0;
   // descriptor uploads (pinned host -> device), a ring so the host can run ahead
   static constexpr int kUp = 8;
@@ -387,7 +385,6 @@ int engine_ensure_ring(helm_engine* e, size_t min_chunk) {
   e->ring = nullptr;
   e->chunk_bytes = align_up(std::max(min_chunk, e->chunk_bytes), 1 << 20);
   HELM_HIP(hipMalloc(&e->ring, e->chunk_bytes * e->ring_slots));
-  std::fill(e->slot_used.begin(), e->slot_used.end(), 0);
   return HELM_OK;
 }
 
@@ -424,7 +421,9 @@ int engine_mark_upload_consumed(helm_engine* e, hipStream_t st) {
   return HELM_OK;
 }
 
-// D2H / H2D copies on the engine's copy stream, ordered after `st`.
+// D2H / H2D copies on `st`, after everything already queued there; regions
+// adjacent on both sides become one copy.  sync != 0 returns once they are
+// done.
 int engine_copies(helm_engine* e, int n, const uint64_t* src,
                   const uint64_t* dst, const uint64_t* bytes, hipMemcpyKind kind,
                   int sync, hipStream_t st) {
@@ -436,8 +435,6 @@ int engine_copies(helm_engine* e, int n, const uint64_t* src,
   for (int i = 0; i < n; ++i) idx[i] = i;
   std::sort(idx.begin(), idx.end(),
             [&](int a, int b) { return src[a] < src[b]; });
-  HELM_HIP(hipEventRecord(e->ev_a, st));
-  HELM_HIP(hipStreamWaitEvent(e->copy, e->ev_a, 0));
   int i = 0;
   while (i < n) {
     uint64_t s0 = src[idx[i]], d0 = dst[idx[i]], len = bytes[idx[i]];
@@ -448,15 +445,12 @@ int engine_copies(helm_engine* e, int n, const uint64_t* src,
     }
     if (len)
       HELM_HIP(hipMemcpyAsync(reinterpret_cast<void*>(d0),
-                              reinterpret_cast<const void*>(s0), len, kind,
-                              e->copy));
+                              reinterpret_cast<const void*>(s0), len, kind, st));
     i = j;
   }
-  HELM_HIP(hipEventRecord(e->ev_b, e->copy));
   if (sync) {
+    HELM_HIP(hipEventRecord(e->ev_b, st));
     HELM_HIP(hipEventSynchronize(e->ev_b));
-  } else {
-    HELM_HIP(hipStreamWaitEvent(st, e->ev_b, 0));
   }
   return HELM_OK;
 }
@@ -476,23 +470,14 @@ int helm_engine_create(int device, size_t chunk_bytes, int ring_slots,
   HELM_HIP(hipSetDevice(device));
   helm_engine* e = new helm_engine();
   e->device = device;
-  e->chunk_bytes = chunk_bytes ? chunk_bytes : (size_t)16 << 20;
-  e->ring_slots = ring_slots > 0 ? ring_slots : 4;
-  e->copy_done.resize(e->ring_slots);
-  e->slot_free.resize(e->ring_slots);
-  e->slot_used.assign(e->ring_slots, 0);
+  e->chunk_bytes = chunk_bytes ? chunk_bytes : (size_t)64 << 20;
+  e->ring_slots = ring_slots > 0 ? ring_slots : 2;
   int rc = HELM_OK;
   auto chk = [&](hipError_t err, const char* what) {
     if (err != hipSuccess && rc == HELM_OK) rc = hip_fail(err, what);
   };
   chk(hipStreamCreateWithFlags(&e->copy, hipStreamNonBlocking),
       "hipStreamCreateWithFlags");
-  for (int i = 0; i < e->ring_slots; ++i) {
-    chk(hipEventCreateWithFlags(&e->copy_done[i], hipEventDisableTiming),
-        "hipEventCreate");
-    chk(hipEventCreateWithFlags(&e->slot_free[i], hipEventDisableTiming),
-        "hipEventCreate");
-  }
   for (int i = 0; i < helm_engine::kUp; ++i)
     chk(hipEventCreateWithFlags(&e->up_done[i], hipEventDisableTiming),
         "hipEventCreate");
@@ -520,10 +505,6 @@ int helm_engine_destroy(helm_engine* e) {
     if (e->up_dev[i]) (void)hipFree(e->up_dev[i]);
     if (e->up_done[i]) (void)hipEventDestroy(e->up_done[i]);
   }
-  for (auto ev : e->copy_done)
-    if (ev) (void)hipEventDestroy(ev);
-  for (auto ev : e->slot_free)
-    if (ev) (void)hipEventDestroy(ev);
   if (e->ev_a) (void)hipEventDestroy(e->ev_a);
   if (e->ev_b) (void)hipEventDestroy(e->ev_b);
   if (e->copy) (void)hipStreamDestroy(e->copy);
@@ -809,34 +790,32 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
     return engine_mark_upload_consumed(eng, st);
   }
 
-  // ---- mixed residency (B == 1): device pages now, chunks as they land -----
+  // ---- mixed residency (B == 1) ---------------------------------------------
+  // Every launch and copy of the call is queued on `st`, in order: the device
+  // pages' launch, then per staged chunk its hipMemcpyAsync and the launch
+  // that reads it, then the split merge.  Stream order alone covers the
+  // copy -> kernel dependency and the reuse of a ring slot.  (Splitting the
+  // device pages onto a second stream, joined by event waits, measured
+  // slower here: every cross-stream event wait stalls the host thread for
+  // milliseconds on this runtime, starving the queue.)
   s.p.total_splits = total_splits;
   for (size_t li = 0; li < launches.size(); ++li) {
     const Launch& L = launches[li];
-    if (L.chunk >= 0) {
-      const int slot = chunk_slot[L.chunk];
-      if (eng->slot_used[slot])
-        HELM_HIP(hipStreamWaitEvent(eng->copy, eng->slot_free[slot], 0));
-      char* dst = eng->ring + (size_t)slot * eng->chunk_bytes;
-      for (const Run& r : chunk_runs[L.chunk])
-        HELM_HIP(hipMemcpyAsync(dst + r.dst_off,
-                                reinterpret_cast<const void*>(r.src), r.bytes,
-                                hipMemcpyHostToDevice, eng->copy));
-      HELM_HIP(hipEventRecord(eng->copy_done[slot], eng->copy));
-      HELM_HIP(hipStreamWaitEvent(st, eng->copy_done[slot], 0));
-    }
     s.p.lo = L.lo;
     s.p.hi = L.hi;
     s.p.split_base = split_base[li];
     const int nsp = (L.hi - L.lo + pl.pps - 1) / pl.pps;
     s.grid = dim3(std::max(1, nsp), Hkv * pl.n_qtiles, 1);
-    hipError_t e = dispatch(s, st);
-    if (e != hipSuccess) return hip_fail(e, "stream_attn chunk launch");
     if (L.chunk >= 0) {
       const int slot = chunk_slot[L.chunk];
-      HELM_HIP(hipEventRecord(eng->slot_free[slot], st));
-      eng->slot_used[slot] = 1;
+      char* dst = eng->ring + (size_t)slot * eng->chunk_bytes;
+      for (const Run& r : chunk_runs[L.chunk])
+        HELM_HIP(hipMemcpyAsync(dst + r.dst_off,
+                                reinterpret_cast<const void*>(r.src), r.bytes,
+                                hipMemcpyHostToDevice, st));
     }
+    hipError_t e = dispatch(s, st);
+    if (e != hipSuccess) return hip_fail(e, "stream_attn chunk launch");
   }
   hipError_t e = launch_merge(s, 1, Hkv, st);
   if (e != hipSuccess) return hip_fail(e, "merge launch");

@@ -1,7 +1,7 @@
-"""Per-device native engine handles (copy stream, workspace, staging ring).
+"""Per-device native engine handles (side stream, workspace, staging ring).
 
 One `helm_engine` per HIP device, created on first use and destroyed at
-interpreter exit.  The engine's copy stream is what HELM's per-device
+interpreter exit.  The engine's side stream is what HELM's per-device
 ``_get_kv_copy_stream`` (helm/runtime/kv_cache.py:383-391) memoizes.
 """
 from __future__ import annotations
@@ -30,8 +30,8 @@ def get_engine(device: torch.device) -> ctypes.c_void_p:
     eng = _engines.get(idx)
     if eng is None:
         _native.load()
-        chunk = int(os.environ.get("HELM_AMD_CHUNK_MB", "16")) << 20
-        slots = int(os.environ.get("HELM_AMD_RING_SLOTS", "4"))
+        chunk = int(os.environ.get("HELM_AMD_CHUNK_MB", "64")) << 20
+        slots = int(os.environ.get("HELM_AMD_RING_SLOTS", "2"))
         handle = ctypes.c_void_p()
         with torch.cuda.device(idx):
             _native.call("helm_engine_create", idx, chunk, slots, ctypes.byref(handle))
@@ -40,7 +40,7 @@ def get_engine(device: torch.device) -> ctypes.c_void_p:
 
 
 def copy_stream(device: torch.device) -> torch.cuda.ExternalStream:
-    """The engine's copy stream as a torch stream object (memoized per device)."""
+    """The engine's side stream as a torch stream object (memoized per device)."""
     idx = device_index(device)
     s = _copy_streams.get(idx)
     if s is None:

@@ -10,8 +10,9 @@ watermark, oldest-first eviction, contiguous fast path) and
 * eviction moves all selected pages with one batched, coalesced
   ``helm_evict_pages`` copy into pinned host slots (kv_cache.py:179-222);
 * attention is ``helm_stream_attn``: split-K HIP kernels over the page list,
-  with host pages prefetched through a device staging ring on the engine's
-  copy stream while the device pages are being processed (kv_cache.py:405-662).
+  with host pages prefetched through a device staging ring by hipMemcpyAsync
+  on the caller's stream, each staged chunk attended right behind its copy
+  (kv_cache.py:405-662).
 
 There is no CPU compute path: a query that is not on a HIP device raises.
 """
@@ -419,7 +420,7 @@ class KVCacheManager:
 
 # ── copy stream (kv_cache.py:383-396) ──────────────────────────────────────────
 def _get_kv_copy_stream(device: torch.device) -> torch.cuda.Stream:
-    """The per-device copy stream that evictions and prefetches run on."""
+    """The per-device side stream of the native engine (memoized per device)."""
     return _engine.copy_stream(device)
 
 

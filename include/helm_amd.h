@@ -6,7 +6,7 @@
  * `void*`.  No torch types cross this boundary.  The caller owns every buffer
  * it passes in; the library never frees caller memory.  The only memory the
  * library owns is held by a `helm_engine` (workspace, staging ring, pinned
- * descriptor-upload buffers, one copy stream) and is released by
+ * descriptor-upload buffers, one side stream) and is released by
  * helm_engine_destroy().
  *
  * Status convention: 0 = success; a positive value is the hipError_t that
@@ -89,16 +89,16 @@ typedef struct helm_engine helm_engine;
 const char* helm_last_error_string(void);
 int helm_abi_version(void);
 
-/* ---- engine: per-device state (copy stream, workspace, staging ring) ----- */
+/* ---- engine: per-device state (side stream, workspace, staging ring) ----- */
 
 /* Creates the per-device engine.  chunk_bytes / ring_slots size the device
  * staging ring that cold pages are prefetched through (0 = defaults:
- * 16 MiB x 4).  Replaces the per-device copy stream of
+ * 64 MiB x 2).  Its side stream replaces the per-device copy stream of
  * helm/runtime/kv_cache.py:383-391 (_get_kv_copy_stream). */
 int helm_engine_create(int device, size_t chunk_bytes, int ring_slots,
                        helm_engine** out);
 int helm_engine_destroy(helm_engine* eng);
-/* The engine's copy stream (hipStream_t). */
+/* The engine's side stream (hipStream_t). */
 void* helm_engine_copy_stream(helm_engine* eng);
 
 /* ---- attention ------------------------------------------------------------ */
@@ -139,10 +139,11 @@ int helm_paged_decode_attn(const void* q, void* out,
  * all four paths.  `pages` (host array) holds the active pages of every
  * sequence, sequence b owning pages[seq_off[b] .. seq_off[b+1]) (host array of
  * B+1).  Pages flagged HELM_PAGE_HOST are copied into the engine's device
- * staging ring on the engine's copy stream with hipMemcpyAsync (runs of
- * adjacent host pages become one copy) while attention over the device pages
- * runs on `stream`; each staged chunk is consumed as soon as its copy event
- * fires.  causal != 0 applies a top-left causal mask (key t visible to query
+ * staging ring with hipMemcpyAsync on `stream` (runs of adjacent host pages
+ * become one copy, up to chunk_bytes per chunk), each chunk's attention
+ * launch queued right behind its copy, after the launch over the device
+ * pages; the split merge follows, all on `stream`.  causal != 0 applies a
+ * top-left causal mask (key t visible to query
  * row s iff t <= s), HELM's is_causal=q_len>1 of Path 1.  A sequence with no
  * pages yields zeros.  Host pages require B == 1. */
 int helm_stream_attn(helm_engine* eng, const void* q, void* out,
@@ -163,11 +164,12 @@ int helm_page_append(const helm_append_seg* segs, int n_segs, int Hkv, int D,
                      int dtype, void* stream);
 
 /* Eviction copies: n regions of bytes[i] from device src[i] to pinned host
- * dst[i], issued on the engine's copy stream after everything already queued
- * on `stream`; regions adjacent on both sides are merged into one copy.  With
- * sync != 0 the call returns after the copies completed (HELM's synchronous
- * move_page, helm/runtime/kv_allocator.py:104-116); otherwise `stream` is made
- * to wait for them.  Replaces KVAllocator.move_page GPU->CPU. */
+ * dst[i], issued with hipMemcpyAsync on `stream` after everything already
+ * queued there; regions adjacent on both sides are merged into one copy.
+ * With sync != 0 the call returns after the copies completed (HELM's
+ * synchronous move_page, helm/runtime/kv_allocator.py:104-116); otherwise
+ * later work on `stream` is ordered after them.  Replaces
+ * KVAllocator.move_page GPU->CPU. */
 int helm_evict_pages(helm_engine* eng, int n, const uint64_t* src_dev,
                      const uint64_t* dst_host, const uint64_t* bytes,
                      int sync, void* stream);
