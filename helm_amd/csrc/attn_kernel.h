@@ -564,11 +564,13 @@ __device__ __forceinline__ void split_epilogue(Smem<NW, GM, DMAX>& sm, const Att
 // Combines the split partials of one (tile, row) and writes the output row:
 // out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, M = max_s m_s — the
 // final normalisation of HELM's loop, out / clamp(sum, 1e-12)
-// (helm/runtime/kv_cache.py:554-555).  grid = (tiles, rows_per_tile); a tile
-// whose sequence has no pages (split count 0) gets zeros
-// (kv_cache.py:441-442).  Thread (sub, c) owns output column chunk c and the
-// splits sub, sub + nsub, ...; all of its loads of a batch are in flight at
-// once, and the nsub partial results of a column meet in LDS.
+// (helm/runtime/kv_cache.py:554-555).  grid = (tiles, rows_per_tile, column
+// groups): a workgroup merges one group of the row's column chunks, so the
+// partials are read by many CUs at once.  A tile whose sequence has no pages
+// (split count 0) gets zeros (kv_cache.py:441-442).  Thread (sub, c) owns
+// column chunk c and the splits sub, sub + nsub, ...; all of its loads of a
+// batch are in flight at once, and the nsub partial results of a column meet
+// in LDS.
 constexpr int kMergeBatch = 8;
 
 template <typename TQ>
@@ -592,27 +594,43 @@ __global__ __launch_bounds__(kThreads) void merge_splits_kernel(AttnParams p) {
   const int total = p.counts[tile];
 
   const int cw = (D % 4 == 0) ? 4 : 1;
-  const int ncol = D / cw;
+  const int ncol_all = D / cw;
+  const int per_group = (ncol_all + gridDim.z - 1) / gridDim.z;
+  const int cbeg = blockIdx.z * per_group;
+  const int ncol = min(per_group, ncol_all - cbeg);
+  if (ncol <= 0) return;
   const int nsub = ncol >= kThreads ? 1 : kThreads / ncol;
   const int sub = tid / ncol;
-  const int c0 = tid % ncol;
+  const int c0 = cbeg + tid % ncol;
   const int64_t base_part = (int64_t)tile * p.max_splits * RS + row;
-  for (int c = c0; c < ncol && sub < nsub; c += kThreads) {
+  for (int c = c0; c < cbeg + ncol && sub < nsub; c += kThreads) {
     float M = -INFINITY, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = sub; s0 < total; s0 += nsub * kMergeBatch) {
+    // The first batch is loaded before the split count arrives (bounded by
+    // the workspace's split capacity) and masked afterwards: one memory trip
+    // instead of two.
+    const int bound = p.max_splits;
+    for (int s0 = sub; s0 < bound; s0 += nsub * kMergeBatch) {
+      if (s0 > sub && s0 >= total) break;
       float2 ml[kMergeBatch];
       float4 v[kMergeBatch];
 #pragma unroll
       for (int k = 0; k < kMergeBatch; ++k) {
         const int sp = s0 + k * nsub;
-        if (sp < total) {
+        if (sp < bound) {
           const int64_t pi = base_part + (int64_t)sp * RS;
           ml[k] = *reinterpret_cast<const float2*>(p.ws_ml + pi * 2);
           const float* src = p.ws_o + pi * D + c * cw;
           v[k] = (cw == 4) ? *reinterpret_cast<const float4*>(src)
                            : make_float4(*src, 0.f, 0.f, 0.f);
         } else {
+          ml[k] = make_float2(-INFINITY, 0.f);
+          v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        if (s0 + k * nsub >= total) {
           ml[k] = make_float2(-INFINITY, 0.f);
           v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
@@ -664,7 +682,8 @@ __global__ __launch_bounds__(kThreads) void merge_splits_kernel(AttnParams p) {
       }
       const float inv = 1.f / fmaxf(L, 1e-12f);
       const float a[4] = {acc.x, acc.y, acc.z, acc.w};
-      for (int j = 0; j < cw; ++j) store_elem<TQ>(out_row + (tid * cw + j) * QB, a[j] * inv);
+      for (int j = 0; j < cw; ++j)
+        store_elem<TQ>(out_row + ((cbeg + tid) * cw + j) * QB, a[j] * inv);
     }
   }
 }

@@ -107,16 +107,20 @@ struct DescLanes {
   int used, tok_off, head_stride;
 };
 
-__device__ __forceinline__ PoolLanes lane_pages(const PoolSrc& s, int b, int pg0, int npg,
-                                                int lane) {
+// Issued before the sequence length is known: the pool's table row is read
+// up to its declared width, so the first K/V loads wait for one memory trip.
+__device__ __forceinline__ PoolLanes lane_pages(const PoolSrc& s, int b, int pg0, int lane) {
   PoolLanes L;
-  L.slot = s.table[(int64_t)b * s.table_stride + pg0 + min(lane, npg - 1)];
+  L.slot = s.max_pages > 0
+               ? s.table[(int64_t)b * s.table_stride + min(pg0 + lane, s.max_pages - 1)]
+               : 0;
   return L;
 }
-__device__ __forceinline__ DescLanes lane_pages(const DescSrc& s, int b, int pg0, int npg,
-                                                int lane) {
+__device__ __forceinline__ DescLanes lane_pages(const DescSrc& s, int b, int pg0, int lane) {
   const int base = sload(s.seq_off + b);
-  const helm_page d = s.pages[base + pg0 + min(lane, npg - 1)];
+  const int cnt = sload(s.seq_off + b + 1) - base;
+  helm_page d{};
+  if (cnt > 0) d = s.pages[base + max(0, min(pg0 + lane, cnt - 1))];
   DescLanes L;
   L.klo = static_cast<uint32_t>(d.k);
   L.khi = static_cast<uint32_t>(d.k >> 32);
@@ -190,35 +194,10 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   const int r0 = qt * kMfmaRows;
   const int nrows = min(kMfmaRows, G * S - r0);
 
-  // ---- this workgroup's page range -------------------------------------------
-  const int np = src.n_pages(b);
-  const int lo = min(p.lo, np);
-  const int hi = min(p.hi, np);
-  const int nsplit_launch = (hi - lo + p.pps - 1) / p.pps;
-  const int total = p.total_splits > 0 ? p.total_splits : nsplit_launch;
-  // split 0 publishes the tile's split count; a tile without pages gets
-  // zeros (HELM kv_cache.py:441-442), from split 0 in fused mode and from
-  // merge_splits_kernel otherwise
-  if (split_local == 0 && tid == 0) p.counts[tile] = total;
-  if (total == 0) {
-    if (p.fused && split_local == 0) {
-      for (int idx = tid; idx < nrows * 128; idx += NT) {
-        const int rr = r0 + idx / 128;
-        const int h = hk * G + rr / S, s = rr % S;
-        const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * 128 + idx % 128;
-        store_elem<T>(reinterpret_cast<char*>(p.out) + o_off * 2, 0.f);
-      }
-    }
-    return;
-  }
-  if (split_local >= nsplit_launch) return;
-  const int split = p.split_base + split_local;
-  const int pg0 = lo + split_local * p.pps;
-  const int npg = min(pg0 + p.pps, hi) - pg0;  // 1..kMfmaMaxPps
-
-  // page records first: their latency overlaps the query load
-  const typename LanesOf<Src>::type lanes = lane_pages(src, b, pg0, npg, lane);
-
+  // ---- loads that need no sequence length: page records, query rows --------
+  // (pg0 below equals this whenever the workgroup has pages to process)
+  const typename LanesOf<Src>::type lanes =
+      lane_pages(src, b, p.lo + split_local * p.pps, lane);
   // ---- query operand: row n of the tile at dim chunks 4i + q4 ---------------
   const bool row_ok = n < nrows;
   const int rr = r0 + (row_ok ? n : 0);
@@ -235,6 +214,32 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
       qop[i] = row_ok ? mf_u32x4{v.x, v.y, v.z, v.w} : mf_u32x4{0u, 0u, 0u, 0u};
     }
   }
+  // ---- this workgroup's page range -------------------------------------------
+  const int np = src.n_pages(b);
+  const int lo = min(p.lo, np);
+  const int hi = min(p.hi, np);
+  const int nsplit_launch = (hi - lo + p.pps - 1) / p.pps;
+  const int total = p.total_splits > 0 ? p.total_splits : nsplit_launch;
+  // split 0 publishes the tile's split count; a tile without pages gets
+  // zeros (HELM kv_cache.py:441-442): from split 0 in fused mode, from
+  // merge_splits_kernel otherwise
+  if (split_local == 0 && tid == 0) p.counts[tile] = total;
+  const bool active = total > 0 && split_local < nsplit_launch;
+  if (!active) {
+    if (total == 0 && p.fused && split_local == 0) {
+      for (int idx = tid; idx < nrows * 128; idx += NT) {
+        const int zr = r0 + idx / 128;
+        const int h = hk * G + zr / S, s = zr % S;
+        const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * 128 + idx % 128;
+        store_elem<T>(reinterpret_cast<char*>(p.out) + o_off * 2, 0.f);
+      }
+    }
+    return;
+  }
+  const int split = p.split_base + split_local;
+  const int pg0 = lo + split_local * p.pps;
+  const int npg = min(pg0 + p.pps, hi) - pg0;  // 1..kMfmaMaxPps
+
   const float* mrow = nullptr;
   if constexpr (kMask)
     mrow = p.mask + (int64_t)b * p.mask_bstride + (int64_t)(hk * G + g_row) * p.mask_hstride +

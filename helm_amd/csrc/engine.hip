@@ -98,9 +98,9 @@ int mfma_waves() { return env_int("HELM_AMD_WAVES", 4) == 8 ? 8 : 4; }
 
 // Split merge.  merge_splits_kernel spreads the merge of every tile over
 // many workgroups; merging in-kernel (the last split of a tile to arrive
-// reads every partial) saves that launch but is bound by one CU's
-// load latency, so it is used only for tiles of at most kFusedMaxSplits
-// splits.  HELM_AMD_MERGE = fused | kernel forces one.
+// reads every partial) saves that launch but is bound by one CU's load
+// latency, so it is used only for tiles of at most kFusedMaxSplits splits.
+// HELM_AMD_MERGE = fused | kernel forces one.
 constexpr int kFusedMaxSplits = 8;
 int fused_merge(int max_splits) {
   const char* v = std::getenv("HELM_AMD_MERGE");
@@ -254,7 +254,10 @@ hipError_t dispatch(const LaunchSpec& s, hipStream_t st) {
 // split kernels, on the same stream).
 hipError_t launch_merge(const LaunchSpec& s, int B, int Hkv, hipStream_t st) {
   if (s.p.fused) return hipSuccess;
-  const dim3 grid(B * Hkv * s.p.n_qtiles, s.p.rows_per_tile);
+  // column groups: spread each row's partial reads over several CUs
+  const int chunks = (s.p.D % 4 == 0) ? s.p.D / 4 : s.p.D;
+  const int groups = std::max(1, std::min(env_int("HELM_AMD_MERGE_GROUPS", 1), chunks));
+  const dim3 grid(B * Hkv * s.p.n_qtiles, s.p.rows_per_tile, groups);
   switch (s.q_dtype) {
     case HELM_F16:
       hipLaunchKernelGGL(merge_splits_kernel<f16_t>, grid, dim3(kThreads), 0, st, s.p);

@@ -33,7 +33,8 @@ TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-5}
 def kernel(request, monkeypatch):
     """Runs a test on the matrix-core kernel (the automatic choice for 16-bit
     D = 128 pages) and on the vector-ALU kernels, with the split merge chosen
-    automatically, forced in-kernel (fused) and forced to merge_splits_kernel."""
+    automatically, in-kernel by the last split (fused) and by
+    merge_splits_kernel."""
     monkeypatch.setenv("HELM_AMD_KERNEL", request.param[0])
     monkeypatch.setenv("HELM_AMD_MERGE", request.param[1])
     return request.param
@@ -316,3 +317,16 @@ def test_kernels_agree_at_full_size():
         torch.cuda.synchronize()
         outs[kind] = o.float()
     assert (outs["auto"] - outs["valu"]).abs().max().item() <= 2 ** -7
+
+
+@pytest.mark.parametrize("groups", [2, 4, 32])
+def test_merge_kernel_column_groups(groups, monkeypatch):
+    """merge_splits_kernel split over column groups gives the same attention."""
+    monkeypatch.setenv("HELM_AMD_MERGE", "kernel")
+    monkeypatch.setenv("HELM_AMD_MERGE_GROUPS", str(groups))
+    w = W.WORKLOADS["qwen3-14b-ragged-b8"]
+    case = W.make_pool_case(w, seed=13, device=DEV, lens=[5000, 77, 1200, 3333, 16, 1, 4096, 900])
+    out = paged_decode_attention(case["q"], case["k_pool"], case["v_pool"], case["table"],
+                                 case["lens"], max_pages=case["max_pages"], pages_per_split=8)
+    torch.cuda.synchronize()
+    _check_pool(w, case, out)
