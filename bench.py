@@ -54,6 +54,12 @@ def parse():
     ap.add_argument("--pps", type=int, default=0, help="pages per split (0 = auto)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (PMC byte-count calibration)")
+    ap.add_argument("--full-step", action="store_true",
+                    help="also time the 40-layer Qwen3-14B B4 x 64k decode step (64 GB device "
+                         "KV budget, and a 32 GB budget that forces eviction)")
+    ap.add_argument("--full-step-steps", type=int, default=64)
+    ap.add_argument("--full-step-budgets", default="64,32",
+                    help="device KV budgets (GB) of the full-step runs")
     ap.add_argument("--all", action="store_true",
                     help="also measure every benchmark configuration (gpurun_out/bench_all.json)")
     return ap.parse_args()
@@ -157,17 +163,29 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
                      w.Hkv, 1, w.D, _native.ptr(pages), _native.ptr(seq_off), case["scale"], 0.0,
                      None, 0, 0, 0, 0, kcode, kcode, stream.cuda_stream)
 
-    for _ in range(3):
-        call()
-    torch.cuda.synchronize()
     steps = steps or args.offload_steps
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(steps):
-        call()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    per = e0.elapsed_time(e1) / 1e3 / steps
+
+    def timed():
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / steps
+
+    # host pages staged through the device ring by hipMemcpyAsync, then the
+    # default: read in place by the kernel over the host link
+    prev = os.environ.pop("HELM_AMD_HOST_READ", None)
+    os.environ["HELM_AMD_HOST_READ"] = "copy"
+    per_staged = timed()
+    del os.environ["HELM_AMD_HOST_READ"]
+    per = timed()
+    if prev is not None:
+        os.environ["HELM_AMD_HOST_READ"] = prev
     host_bytes = n_host * slot_b
     peak = h2d_peak(torch)
     # parity spot check of this exact configuration against the oracle
@@ -182,7 +200,97 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
         "frac_of_measured_h2d": host_bytes / per / 1e9 / peak,
         "pcie5_x16_theoretical_GBs": PCIE5_X16_GBS, "max_abs_err_vs_fp64": err,
         "resident_bytes": (n - n_host) * slot_b,
+        "host_read": "in place (kernel reads pinned host pages over the link)",
+        "staged_ms_per_call": per_staged * 1e3,
+        "staged_host_link_GBs": host_bytes / per_staged / 1e9,
     }
+
+
+def gpu_full_step(args, torch, W, budget_gb, steps, name="qwen3-14b-40l-b4-64k", seed=5):
+    """The 40-layer Qwen3-14B decode step through HELM's runtime API.
+
+    Four sequences of 65,536 tokens per layer in 16-token pages taken from a
+    seeded shuffle of the free list, one KVCacheManager per sequence sharing
+    one KVAllocator, the device KV budget split evenly over the sequences (as
+    KVOffloadManager does, kv_offload.py:683-688).  A step runs, for each of
+    the 40 layers, ``_decode_batched``: append each sequence's new token (a
+    fresh page every 16 tokens), enforce the residency watermark (evicting the
+    oldest full pages to pinned host RAM when over budget), and attend over
+    every page (host pages streamed back through the staging ring).
+    """
+    import random
+    from helm_amd.runtime import kv_cache as KC
+    from helm_amd.runtime.kv_allocator import KVAllocator
+    from helm_amd.runtime.kv_cache import KVCacheManager
+    from helm_amd.runtime.kv_offload import _decode_batched
+    w = W.WORKLOADS[name]
+    dev = torch.device("cuda:0")
+    P, L, B = w.page_size, w.layers, w.B
+    per_item = int(budget_gb * 1e9) // B
+    alloc = KVAllocator(L, w.Hkv, w.D, page_size=P, dtype=w.dtype)
+    n_pages = L * B * (w.T // P + steps // P + 2)
+    t_setup = time.perf_counter()
+    alloc.reserve_batch(n_pages, dev)
+    random.Random(seed).shuffle(alloc.gpu_free_pool)
+    kvcms = [KVCacheManager(alloc, gpu_high_watermark_bytes=per_item) for _ in range(B)]
+    for m in kvcms:
+        m.initialize_layer_caches(L)
+    KC.reset_paging_stats()
+    g = torch.Generator(device=dev).manual_seed(seed)
+    for layer in range(L):
+        for m in kvcms:
+            k = torch.randn((1, w.Hkv, w.T, w.D), generator=g, device=dev, dtype=w.dtype)
+            v = torch.randn((1, w.Hkv, w.T, w.D), generator=g, device=dev, dtype=w.dtype)
+            m.append_prefill(layer, k, v)
+            del k, v
+    torch.cuda.synchronize()
+    setup_s = time.perf_counter() - t_setup
+    prefill_stats = KC.get_paging_stats()
+    q = torch.randn((L, B, w.Hq, 1, w.D), generator=g, device=dev, dtype=w.dtype)
+    kn = torch.randn((L, B, w.Hkv, 1, w.D), generator=g, device=dev, dtype=w.dtype)
+    vn = torch.randn((L, B, w.Hkv, 1, w.D), generator=g, device=dev, dtype=w.dtype)
+    scale = 1.0 / math.sqrt(w.D)
+    KC.reset_paging_stats()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    out = None
+    for s in range(steps):
+        for layer in range(L):
+            out = _decode_batched(kvcms, q[layer], kn[layer], vn[layer], layer, scale)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = e0.elapsed_time(e1) / 1e3
+    stats = KC.get_paging_stats()
+    # spot check: the last layer's output of the last step against the oracle
+    from oracle.attention import attention_fp64_batched
+    pages = kvcms[0].layers[L - 1].pages
+    K = torch.cat([p.k_tensor[0, :, :p.used_tokens].cpu() for p in pages], 1)
+    V = torch.cat([p.v_tensor[0, :, :p.used_tokens].cpu() for p in pages], 1)
+    ref = attention_fp64_batched(q[L - 1, 0].cpu(), K, V)
+    err = (out[0].double().cpu() - ref).abs().max().item()
+    ctx = w.T + steps
+    kv_step = L * B * ctx * w.token_bytes()
+    host_pages = sum(layer._n_host for m in kvcms for layer in m.layers.values())
+    res = {
+        "workload": f"{name}: 40 layers x (append + decode attention), B={B}, Hq={w.Hq}, "
+                    f"Hkv={w.Hkv}, D={w.D}, bf16, {w.T} tokens per sequence in pages of {P}",
+        "device_kv_budget_GB": budget_gb, "steps": steps,
+        "steps_per_s": steps / wall, "ms_per_step": wall * 1e3 / steps,
+        "gpu_ms_per_step": gpu_s * 1e3 / steps,
+        "kv_GBs": kv_step * steps / wall / 1e9,
+        "host_pages_at_end": host_pages,
+        "host_frac_at_end": host_pages / (L * B * -(-ctx // P)),
+        "evicted_in_setup": prefill_stats["pages_evicted"],
+        "paging_stats_timed": stats,
+        "setup_s": setup_s, "max_abs_err_vs_fp64": err,
+    }
+    del kvcms, alloc, q, kn, vn, out
+    torch.cuda.empty_cache()
+    return res
 
 
 def all_configs(args, torch, W, paged):
@@ -273,6 +381,17 @@ def main():
     if args.all:
         all_configs(args, torch, W, paged)
 
+    full = None
+    if args.full_step or args.all:
+        full = {}
+        budgets = [float(x) for x in args.full_step_budgets.split(",") if x]
+        for budget in budgets:
+            label = f"budget_{budget:g}GB" + ("" if budget >= 64 else "_eviction")
+            log(f"full step: qwen3-14b 40 layers, B4 x 64k, device KV budget {budget:.0f} GB")
+            r = gpu_full_step(args, torch, W, budget, args.full_step_steps)
+            log(json.dumps(r))
+            full[label] = r
+
     off = None
     if not args.no_offload:
         log("offload: qwen3-8b-32k, oldest 50% in pinned host")
@@ -317,6 +436,7 @@ def main():
                      "alg_bytes_per_launch": h["alg_bytes"],
                      "avg_launch_us": round(h["per_call_s"] * 1e6, 3)},
         "offload50": off,
+        "full_step_40l": full,
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["path2_concat_sdpa"]["GBs"], 3), "unit": "GB/s",
             "cores": threads, "kind": "port",

@@ -53,6 +53,9 @@ SIGNATURES = {
         _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_int, _c_void_p, _c_void_p, _f32, _f32, _c_void_p, _i64, _i64,
         _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
+    "helm_host_pages_in_place": (ctypes.c_int, [_c_void_p, _c_void_p, ctypes.c_int,
+                                                ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                _c_void_p]),
     "helm_page_append": (ctypes.c_int, [_c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, _c_void_p]),
     "helm_evict_pages": (ctypes.c_int, [_c_void_p, ctypes.c_int, _c_void_p, _c_void_p,

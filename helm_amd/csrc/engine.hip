@@ -363,6 +363,8 @@ struct helm_engine {
   int up_used[kUp] = {};
   int up_next = 0;
   hipEvent_t ev_a = nullptr, ev_b = nullptr;
+  // pinned host allocations [base, end) the device reads at the same address
+  std::vector<std::pair<uint64_t, uint64_t>> host_ranges;
 };
 
 namespace {
@@ -391,28 +393,183 @@ int engine_ensure_ring(helm_engine* e, size_t min_chunk) {
   return HELM_OK;
 }
 
-// Returns a device buffer holding `n` bytes copied from `src`, uploaded on
-// `st` through a pinned staging buffer.
-int engine_upload(helm_engine* e, const void* src, size_t n, hipStream_t st,
-                  char** dev_out) {
+// ---- host pages read in place --------------------------------------------------
+// A host page is read by the kernel directly over the host link (no staging
+// copy) when its K and V regions each lie inside one pinned host allocation
+// that the device maps at the host address.  The kernels bound every load by
+// the page's used tokens (buffer-resource limits), so they never touch bytes
+// past page_extent().
+
+// HELM_AMD_HOST_READ: "copy" stages every host page, "direct" reads every
+// readable one in place, default "auto" decides per call (host_runs_favor_copy).
+int host_read_mode() {
+  const char* e = std::getenv("HELM_AMD_HOST_READ");
+  if (e && std::strcmp(e, "copy") == 0) return 0;
+  if (e && std::strcmp(e, "direct") == 0) return 2;
+  return 1;
+}
+
+bool host_read_in_place() { return host_read_mode() != 0; }
+
+// The staging copies reach the link's rate only in large runs: hipMemcpyAsync
+// costs ~9 us per call here, so host pages that coalesce (adjacent in host
+// memory, e.g. evicted in address order) into runs averaging >= 2 MiB are
+// copied; scattered pages are read in place by the kernel.
+constexpr uint64_t kStageMinRun = 2u << 20;
+
+bool host_runs_favor_copy(const helm_page* pages, const std::vector<char>& sel,
+                          int Hkv, int D, int eb) {
+  std::vector<std::pair<uint64_t, uint64_t>> regions;
+  for (size_t i = 0; i < sel.size(); ++i) {
+    if (!sel[i]) continue;
+    const uint64_t rb = page_extent(pages[i], Hkv, D, eb);
+    regions.push_back({pages[i].k, rb});
+    regions.push_back({pages[i].v, rb});
+  }
+  if (regions.empty()) return false;
+  std::sort(regions.begin(), regions.end());
+  uint64_t runs = 1, total = regions[0].second, end = regions[0].first + regions[0].second;
+  for (size_t i = 1; i < regions.size(); ++i) {
+    if (regions[i].first != end) ++runs;
+    end = regions[i].first + regions[i].second;
+    total += regions[i].second;
+  }
+  return total / runs >= kStageMinRun;
+}
+
+// [base, end) of the pinned host allocation holding `p`, if the device reads
+// it at the same address.
+bool query_host_range(uint64_t p, uint64_t* base, uint64_t* end) {
+  hipPointerAttribute_t a{};
+  if (hipPointerGetAttributes(&a, reinterpret_cast<void*>(p)) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  if (a.type != hipMemoryTypeHost ||
+      reinterpret_cast<uint64_t>(a.devicePointer) != p ||
+      reinterpret_cast<uint64_t>(a.hostPointer) != p)
+    return false;
+  hipDeviceptr_t b = nullptr;
+  size_t sz = 0;
+  if (hipMemGetAddressRange(&b, &sz, reinterpret_cast<hipDeviceptr_t>(p)) !=
+      hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  *base = reinterpret_cast<uint64_t>(b);
+  *end = *base + sz;
+  return sz > 0 && p >= *base && p < *end;
+}
+
+// Index of the cached range holding [p, p + n), or -1.
+int find_host_range(const helm_engine* e, uint64_t p, uint64_t n) {
+  const auto& v = e->host_ranges;
+  auto it = std::upper_bound(
+      v.begin(), v.end(), p,
+      [](uint64_t x, const std::pair<uint64_t, uint64_t>& r) { return x < r.first; });
+  if (it == v.begin()) return -1;
+  --it;
+  if (p >= it->first && p + n <= it->second) return (int)(it - v.begin());
+  return -1;
+}
+
+int add_host_range(helm_engine* e, uint64_t base, uint64_t end) {
+  auto& v = e->host_ranges;
+  if (v.size() >= 4096) v.clear();
+  // drop stale entries overlapping the new allocation
+  v.erase(std::remove_if(v.begin(), v.end(),
+                         [&](const std::pair<uint64_t, uint64_t>& r) {
+                           return r.first < end && base < r.second;
+                         }),
+          v.end());
+  auto it = std::lower_bound(
+      v.begin(), v.end(), std::make_pair(base, end));
+  it = v.insert(it, {base, end});
+  return (int)(it - v.begin());
+}
+
+// Marks direct[i] = 1 for the host pages the kernel can read in place.  Every
+// allocation used is confirmed against the runtime on this call (a cached
+// range whose allocation changed is dropped and its pages re-queried).
+void resolve_host_pages(helm_engine* e, const helm_page* pages, int n, int Hkv,
+                        int D, int eb, std::vector<char>& direct) {
+  direct.assign(n, 0);
+  if (!host_read_in_place()) return;
+  for (int pass = 0; pass < 2; ++pass) {
+    std::vector<int> used_idx;
+    auto region_ok = [&](uint64_t p, uint64_t bytes) {
+      int idx = find_host_range(e, p, bytes);
+      if (idx < 0) {
+        uint64_t b = 0, en = 0;
+        if (!query_host_range(p, &b, &en) || p + bytes > en) return false;
+        add_host_range(e, b, en);
+      }
+      return true;
+    };
+    for (int i = 0; i < n; ++i) {
+      const helm_page& pg = pages[i];
+      if (!(pg.flags & HELM_PAGE_HOST)) continue;
+      const uint64_t bytes = page_extent(pg, Hkv, D, eb);
+      direct[i] = region_ok(pg.k, bytes) && region_ok(pg.v, bytes);
+    }
+    // confirm every range this call relies on
+    bool stale = false;
+    std::vector<std::pair<uint64_t, uint64_t>> keep;
+    for (int i = 0; i < n; ++i) {
+      if (!direct[i]) continue;
+      const uint64_t bytes = page_extent(pages[i], Hkv, D, eb);
+      for (uint64_t p : {pages[i].k, pages[i].v}) {
+        const int idx = find_host_range(e, p, bytes);
+        if (idx < 0) { stale = true; break; }
+        keep.push_back(e->host_ranges[idx]);
+      }
+    }
+    std::sort(keep.begin(), keep.end());
+    keep.erase(std::unique(keep.begin(), keep.end()), keep.end());
+    for (const auto& r : keep) {
+      uint64_t b = 0, en = 0;
+      if (!query_host_range(r.first, &b, &en) || b != r.first || en != r.second) {
+        stale = true;
+        break;
+      }
+    }
+    if (!stale) return;
+    e->host_ranges.clear();
+    direct.assign(n, 0);
+  }
+  direct.assign(n, 0);  // still inconsistent: stage every host page
+}
+
+// Two-phase upload through a ring of pinned staging buffers: reserve hands
+// out the next slot's pinned host buffer (the caller writes `n` bytes there)
+// and its device twin; commit queues the copy on `st`.  The slot is reused
+// once the kernels that read it have run (engine_mark_upload_consumed).
+int engine_upload_reserve(helm_engine* e, size_t n, char** host, char** dev) {
   const int i = e->up_next;
-  e->up_next = (e->up_next + 1) % helm_engine::kUp;
   if (e->up_used[i]) HELM_HIP(hipEventSynchronize(e->up_done[i]));
+  e->up_used[i] = 0;
   if (n > e->up_bytes[i]) {
     if (e->up_host[i]) HELM_HIP(hipHostFree(e->up_host[i]));
     if (e->up_dev[i]) HELM_HIP(hipFree(e->up_dev[i]));
     e->up_host[i] = nullptr;
     e->up_dev[i] = nullptr;
+    e->up_bytes[i] = 0;
     const size_t sz = align_up(std::max(n, (size_t)65536) * 2, 4096);
     HELM_HIP(hipHostMalloc(reinterpret_cast<void**>(&e->up_host[i]), sz,
                            hipHostMallocDefault));
     HELM_HIP(hipMalloc(&e->up_dev[i], sz));
     e->up_bytes[i] = sz;
   }
-  std::memcpy(e->up_host[i], src, n);
+  *host = e->up_host[i];
+  *dev = e->up_dev[i];
+  return HELM_OK;
+}
+
+int engine_upload_commit(helm_engine* e, size_t n, hipStream_t st) {
+  const int i = e->up_next;
+  e->up_next = (e->up_next + 1) % helm_engine::kUp;
   HELM_HIP(hipMemcpyAsync(e->up_dev[i], e->up_host[i], n,
                           hipMemcpyHostToDevice, st));
-  *dev_out = e->up_dev[i];
   e->up_used[i] = 1;
   // the event is recorded by the caller after the consuming kernels
   return HELM_OK;
@@ -625,8 +782,7 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   if (n_all > 0 && !pages) return fail(HELM_E_INVALID, "null pages");
 
   // ---- validate -------------------------------------------------------------
-  int max_pages = 0, max_tok = 1, n_host = 0;
-  size_t max_region = 0;
+  int max_pages = 0, max_tok = 1, n_hostflag = 0;
   for (int b = 0; b < B; ++b) {
     const int n = seq_off[b + 1] - seq_off[b];
     if (n < 0) return fail(HELM_E_INVALID, "seq_off not monotone");
@@ -637,15 +793,30 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
     if (p.used <= 0 || !p.k || !p.v || p.head_stride < p.used * D)
       return fail(HELM_E_INVALID, "bad page descriptor " + std::to_string(i));
     max_tok = std::max(max_tok, p.used);
-    if (p.flags & HELM_PAGE_HOST) {
+    if (p.flags & HELM_PAGE_HOST) ++n_hostflag;
+  }
+  // host pages in mapped pinned memory are read in place; the rest are staged
+  std::vector<char> direct;
+  if (n_hostflag) resolve_host_pages(eng, pages, n_all, Hkv, D, eb, direct);
+  else direct.assign(n_all, 0);
+  if (n_hostflag && B == 1 && host_read_mode() == 1 &&
+      host_runs_favor_copy(pages, direct, Hkv, D, eb))
+    direct.assign(n_all, 0);
+  int n_host = 0;
+  size_t max_region = 0;
+  for (int i = 0; i < n_all; ++i) {
+    if ((pages[i].flags & HELM_PAGE_HOST) && !direct[i]) {
       ++n_host;
-      max_region = std::max(max_region, 2 * page_extent(p, Hkv, D, eb));
+      max_region = std::max(max_region, 2 * page_extent(pages[i], Hkv, D, eb));
     }
   }
   if (n_host && B != 1)
-    return fail(HELM_E_UNSUPPORTED, "host-resident pages need B == 1");
+    return fail(HELM_E_UNSUPPORTED,
+                "host pages outside mapped pinned memory need B == 1");
 
-  // ---- descriptor order: device pages, then host pages chunk by chunk -------
+  // ---- descriptor order: per sequence the host pages read in place (the
+  // longest-running splits start first), then device pages; staged host
+  // pages follow chunk by chunk -------------------------------------------
   std::vector<helm_page> desc;
   desc.reserve(n_all);
   std::vector<int32_t> off(B + 1, 0);
@@ -654,19 +825,30 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   std::vector<Launch> launches;
   std::vector<std::vector<Run>> chunk_runs;
   std::vector<int> chunk_slot;
+  auto push_resident = [&](int lo, int hi) {
+    for (int i = lo; i < hi; ++i)
+      if (direct[i]) {
+        desc.push_back(pages[i]);
+        desc.back().flags = 0;
+      }
+    for (int i = lo; i < hi; ++i)
+      if (!(pages[i].flags & HELM_PAGE_HOST)) desc.push_back(pages[i]);
+  };
 
+  // all pages on the device: the caller's records are uploaded as they are
+  const bool as_given = !n_hostflag;
   if (!n_host) {
-    desc.assign(pages, pages + n_all);
+    if (n_hostflag)
+      for (int b = 0; b < B; ++b) push_resident(seq_off[b], seq_off[b + 1]);
     for (int b = 0; b <= B; ++b) off[b] = seq_off[b];
   } else {
     int rc = engine_ensure_ring(eng, max_region);
     if (rc != HELM_OK) return rc;
-    for (int i = 0; i < n_all; ++i)
-      if (!(pages[i].flags & HELM_PAGE_HOST)) desc.push_back(pages[i]);
+    push_resident(0, n_all);
     if (!desc.empty()) launches.push_back({0, (int)desc.size(), -1});
     std::vector<int> hidx;
     for (int i = 0; i < n_all; ++i)
-      if (pages[i].flags & HELM_PAGE_HOST) hidx.push_back(i);
+      if ((pages[i].flags & HELM_PAGE_HOST) && !direct[i]) hidx.push_back(i);
     std::sort(hidx.begin(), hidx.end(),
               [&](int a, int b) { return pages[a].k < pages[b].k; });
     size_t used_b = 0;
@@ -722,9 +904,13 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
 
   // ---- kernel choice on the final addresses ---------------------------------
   bool al = aligned(q, 16) && aligned(out, 16) && (D * qb) % 16 == 0;
-  for (const helm_page& p : desc)
+  const helm_page* dsrc = as_given ? pages : desc.data();
+  const size_t n_desc = as_given ? (size_t)n_all : desc.size();
+  for (size_t i = 0; i < n_desc; ++i) {
+    const helm_page& p = dsrc[i];
     al = al && (p.k % 16 == 0) && (p.v % 16 == 0) &&
          ((int64_t)p.head_stride * eb) % 16 == 0;
+  }
   Plan pl{};
   int rc = make_plan(pl, kv_dtype, q_dtype, B, Hq, Hkv, q_len, D, max_tok,
                      std::max(max_pages, 1), (double)n_all / B, 0, al);
@@ -756,13 +942,16 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   if (rc != HELM_OK) return rc;
 
   // ---- upload descriptors + sequence offsets --------------------------------
-  const size_t dbytes = desc.size() * sizeof(helm_page);
-  std::vector<char> blob(align_up(dbytes, 16) + (B + 1) * sizeof(int32_t));
-  if (dbytes) std::memcpy(blob.data(), desc.data(), dbytes);
-  std::memcpy(blob.data() + align_up(dbytes, 16), off.data(),
-              (B + 1) * sizeof(int32_t));
+  const size_t dbytes = n_desc * sizeof(helm_page);
+  const size_t blob_bytes = align_up(dbytes, 16) + (B + 1) * sizeof(int32_t);
+  char* host_blob = nullptr;
   char* dev_blob = nullptr;
-  rc = engine_upload(eng, blob.data(), blob.size(), st, &dev_blob);
+  rc = engine_upload_reserve(eng, blob_bytes, &host_blob, &dev_blob);
+  if (rc != HELM_OK) return rc;
+  if (dbytes) std::memcpy(host_blob, dsrc, dbytes);
+  std::memcpy(host_blob + align_up(dbytes, 16), off.data(),
+              (B + 1) * sizeof(int32_t));
+  rc = engine_upload_commit(eng, blob_bytes, st);
   if (rc != HELM_OK) return rc;
 
   LaunchSpec s{};
@@ -823,6 +1012,23 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   hipError_t e = launch_merge(s, 1, Hkv, st);
   if (e != hipSuccess) return hip_fail(e, "merge launch");
   return engine_mark_upload_consumed(eng, st);
+}
+
+int helm_host_pages_in_place(helm_engine* eng, const helm_page* pages, int n,
+                             int Hkv, int D, int kv_dtype, uint8_t* in_place) {
+  if (!eng || (n > 0 && (!pages || !in_place)))
+    return fail(HELM_E_INVALID, "null pointer argument");
+  if (n < 0 || Hkv <= 0 || D <= 0) return fail(HELM_E_INVALID, "bad shape");
+  const int eb = elem_bytes(kv_dtype);
+  if (!eb) return fail(HELM_E_INVALID, "unknown dtype");
+  for (int i = 0; i < n; ++i)
+    if (pages[i].used <= 0 || !pages[i].k || !pages[i].v ||
+        pages[i].head_stride < pages[i].used * D)
+      return fail(HELM_E_INVALID, "bad page descriptor " + std::to_string(i));
+  std::vector<char> direct;
+  resolve_host_pages(eng, pages, n, Hkv, D, eb, direct);
+  for (int i = 0; i < n; ++i) in_place[i] = direct[i] ? 1 : 0;
+  return HELM_OK;
 }
 
 int helm_page_append(const helm_append_seg* segs, int n_segs, int Hkv, int D,

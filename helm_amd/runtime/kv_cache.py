@@ -18,6 +18,7 @@ There is no CPU compute path: a query that is not on a HIP device raises.
 """
 from __future__ import annotations
 
+import heapq
 import math
 import os
 from dataclasses import dataclass
@@ -92,17 +93,123 @@ def _page_bytes(page: KVPage) -> int:
     return page.k_tensor.numel() * page.k_tensor.element_size() * 2
 
 
+def _page_record_fields(page: KVPage):
+    """(k address, v address, head stride, on host) of a [1, Hkv, P, D] page
+    whose rows are dense, or None when the kernel cannot read it in place."""
+    k, v = page.k_tensor, page.v_tensor
+    if (k.dim() != 4 or v.shape != k.shape or k.size(0) != 1 or k.dtype != v.dtype
+            or k.stride(3) != 1 or v.stride(3) != 1 or k.stride(2) != k.size(3)
+            or v.stride(2) != v.size(3) or v.stride(1) != k.stride(1)):
+        return None
+    return k.data_ptr(), v.data_ptr(), k.stride(1), k.device.type != "cuda"
+
+
 # ── layer cache (kv_cache.py:77-86) ───────────────────────────────────────────
 class LayerKVCache:
+    """A layer's pages in token order, plus the kernel's view of them.
+
+    Besides HELM's fields the layer keeps one ``helm_page`` record per page
+    (address, used tokens, token offset, host flag), updated as pages are
+    appended, filled and evicted through the cache manager, so that an
+    attention call hands the kernel this array instead of rebuilding a
+    descriptor per page.  Pages are expected to change only through
+    ``append_page`` and the manager; ``records()`` returns None when a page
+    was appended that the kernel cannot read in place.
+    """
+
     def __init__(self, layer_id: int):
         self.layer_id = layer_id
         self.pages: List[KVPage] = []
         self.tail_page: Optional[KVPage] = None
         self.total_tokens: int = 0
+        self._rec = np.zeros(16, dtype=_native.PAGE_DTYPE)
+        self._rec_ok = True
+        self._rec_sig = None            # (dtype, Hkv, D) of the first page
+        self._tier: List[tuple] = []    # per page: (tier, host bytes) as counted
+        self._n_host = 0                # pages held in host memory
+        self._host_bytes = 0            # their used K+V bytes
+        self._n_other = 0               # pages neither GPU- nor CPU-resident
+
+    def _reset(self) -> None:
+        """Drops every page (the list is emptied in place)."""
+        self.pages.clear()
+        self.tail_page = None
+        self.total_tokens = 0
+        self._rec_ok, self._rec_sig = True, None
+        self._tier.clear()
+        self._n_host = self._host_bytes = self._n_other = 0
 
     def append_page(self, page: KVPage):
         self.pages.append(page)
         self.tail_page = page
+        n = len(self.pages)
+        if n > self._rec.shape[0]:
+            grown = np.zeros(max(n, 2 * self._rec.shape[0]), dtype=_native.PAGE_DTYPE)
+            grown[:n - 1] = self._rec[:n - 1]
+            self._rec = grown
+        r = self._rec[n - 1:n]
+        r["tok_off"] = (int(self._rec["tok_off"][n - 2]) + int(self._rec["used"][n - 2])
+                        if n > 1 else 0)
+        self._tier.append((0, 0))
+        self._set_record(n - 1, page)
+
+    def _set_record(self, idx: int, page: KVPage) -> None:
+        """Writes page `idx`'s record and counts its residency tier."""
+        tier, hb = self._tier[idx]
+        if tier == 1:
+            self._n_host -= 1
+            self._host_bytes -= hb
+        elif tier == 2:
+            self._n_other -= 1
+        host = page.device.type != "cuda"
+        if host and page.state == 'CPU':
+            tier, hb = 1, _used_bytes(page)
+            self._n_host += 1
+            self._host_bytes += hb
+        elif not host and page.state == 'GPU':
+            tier, hb = 0, 0
+        else:
+            tier, hb = 2, 0
+            self._n_other += 1
+        self._tier[idx] = (tier, hb)
+        fields = _page_record_fields(page)
+        sig = (page.k_tensor.dtype, page.k_tensor.size(1) if page.k_tensor.dim() == 4 else -1,
+               page.k_tensor.size(-1) if page.k_tensor.dim() else -1)
+        if self._rec_sig is None:
+            self._rec_sig = sig
+        if fields is None or sig != self._rec_sig:
+            self._rec_ok = False
+            return
+        r = self._rec[idx:idx + 1]
+        r["k"], r["v"], r["head_stride"] = fields[0], fields[1], fields[2]
+        r["used"] = page.used_tokens
+        r["flags"] = _native.HELM_PAGE_HOST if fields[3] else 0
+
+    def _tail_filled(self) -> None:
+        """The tail page gained tokens (its record's used count follows)."""
+        self._rec["used"][len(self.pages) - 1] = self.tail_page.used_tokens
+
+    def _replace_page(self, idx: int, page: KVPage) -> None:
+        """Page `idx` moved tiers: `page` takes its place and record."""
+        old = self.pages[idx]
+        self.pages[idx] = page
+        if self.tail_page is old:
+            self.tail_page = page
+        self._set_record(idx, page)
+
+    def records(self):
+        """The pages' ``helm_page`` records in token order (a view), or None."""
+        if not self._rec_ok:
+            return None
+        return self._rec[:len(self.pages)]
+
+
+def _used_bytes(page: KVPage) -> int:
+    """K+V bytes of the used tokens of a [1, Hkv, P, D] page."""
+    k = page.k_tensor
+    if k.dim() != 4:
+        return 0
+    return page.used_tokens * k.size(0) * k.size(1) * k.size(3) * k.element_size() * 2
 
 
 # ── token writes ───────────────────────────────────────────────────────────────
@@ -165,7 +272,18 @@ def _evict_sync() -> bool:
 
 # ── cache manager (kv_cache.py:88-376) ─────────────────────────────────────────
 class KVCacheManager:
-    """Owns every layer's pages: appends, residency watermark, eviction."""
+    """Owns every layer's pages: appends, residency watermark, eviction.
+
+    HELM totals the evictable GPU bytes by scanning every layer's pages after
+    each appended page, and sorts them to pick victims (kv_cache.py:179-235).
+    Here the evictable pages (GPU-resident, full, not a tail) are kept in a
+    heap ordered as HELM's stable sort orders them (start token, then layer
+    order, then page order) with their bytes as a running total, so the policy
+    check is O(1) and an eviction costs O(log n) per page moved.  The heap
+    follows the pages as this manager changes them; when ``layers`` itself is
+    changed from outside (a layer deleted or replaced) it is rebuilt from a
+    full scan.
+    """
 
     def __init__(self, allocator, gpu_high_watermark_bytes: int = 512 * 1024 * 1024):
         self.allocator = allocator
@@ -179,17 +297,69 @@ class KVCacheManager:
         self.cont_prefill_len: int = 0
         self.use_contiguous: bool = False
         self._appends = _AppendQueue()
+        # evictable pages: (start_token, layer order, page index, seq, layer, page, bytes)
+        self._evq: list = []
+        self._ev_bytes = 0
+        self._ev_seq = 0
+        self._seen: dict = {}        # the `layers` mapping the heap was built for
+        self._order: dict = {}       # id(layer) -> the layer's place in `layers`
+        self._next_order = 0
 
     def initialize_layer_caches(self, num_layers: int):
         for i in range(num_layers):
             self.layers[i] = LayerKVCache(layer_id=i)
+        self._resync()
+
+    # ── evictable-page bookkeeping ──────────────────────────────────────────
+    @staticmethod
+    def _is_evictable(page: KVPage, tail: Optional[KVPage]) -> bool:
+        return (page.state == 'GPU' and page.device.type == 'cuda' and page is not tail
+                and page.used_tokens == page.capacity_tokens)
+
+    def _push_evictable(self, layer: LayerKVCache, idx: int, page: KVPage) -> None:
+        nb = _page_bytes(page)
+        heapq.heappush(self._evq, (page.start_token, self._order[id(layer)], idx, self._ev_seq,
+                                   layer, page, nb))
+        self._ev_seq += 1
+        self._ev_bytes += nb
+
+    def _resync(self) -> None:
+        """Rebuilds the evictable-page heap from a scan of every layer."""
+        self._evq, self._ev_bytes, self._ev_seq = [], 0, 0
+        self._order, self._next_order = {}, 0
+        for layer in self.layers.values():
+            self._order[id(layer)] = self._next_order
+            self._next_order += 1
+            tail = layer.tail_page
+            for idx, page in enumerate(layer.pages):
+                if self._is_evictable(page, tail):
+                    self._push_evictable(layer, idx, page)
+        self._seen = dict(self.layers)
+
+    def _sync_layers(self) -> None:
+        if self.layers != self._seen:
+            self._resync()
 
     def _layer(self, layer_id: int) -> LayerKVCache:
+        self._sync_layers()
         layer = self.layers.get(layer_id)
         if layer is None:
             layer = self.layers[layer_id] = LayerKVCache(layer_id)
+            self._seen[layer_id] = layer
+            self._order[id(layer)] = self._next_order
+            self._next_order += 1
         return layer
 
+    def _add_page(self, layer: LayerKVCache, page: KVPage) -> None:
+        """Appends `page` as the new tail; the old tail may become evictable."""
+        old = layer.tail_page
+        layer.append_page(page)
+        idx = len(layer.pages) - 2
+        if old is not None and idx >= 0 and layer.pages[idx] is old and \
+                self._is_evictable(old, page):
+            self._push_evictable(layer, idx, old)
+
+    # ── appends ──────────────────────────────────────────────────────────────
     def append_prefill(self, layer_id: int, K_prefill: torch.Tensor, V_prefill: torch.Tensor):
         """Split a [1,Hkv,S,D] chunk into page-sized blocks, each a new page
         starting at the layer's running token count; the residency policy runs
@@ -208,7 +378,7 @@ class KVCacheManager:
                 page.used_tokens = chunk_len
                 _write_tokens(self._appends, page, 0, K_prefill[:, :, start_idx:end_idx, :],
                               V_prefill[:, :, start_idx:end_idx, :])
-                layer.append_page(page)
+                self._add_page(layer, page)
                 layer.total_tokens += chunk_len
                 self._enforce_residency_policy()
         finally:
@@ -231,11 +401,12 @@ class KVCacheManager:
             page.layer_id = layer_id
             page.start_token = layer.total_tokens
             page.used_tokens = 0
-            layer.append_page(page)
+            self._add_page(layer, page)
         page = layer.tail_page
         _write_tokens(self._appends, page, page.used_tokens, K_new, V_new)
         page.used_tokens += 1
         layer.total_tokens += 1
+        layer._tail_filled()
 
     def iterate_layer_pages(self, layer_id: int):
         if layer_id not in self.layers:
@@ -249,8 +420,7 @@ class KVCacheManager:
         for layer in self.layers.values():
             tail = layer.tail_page
             for page in layer.pages:
-                if (page.state == 'GPU' and page.device.type == 'cuda' and page is not tail
-                        and page.used_tokens == page.capacity_tokens):
+                if self._is_evictable(page, tail):
                     out.append((layer, page))
         return out
 
@@ -260,41 +430,34 @@ class KVCacheManager:
         if bytes_to_evict <= 0:
             return
         self._appends.flush()
-        gpu_pages = self._evictable()
-        gpu_pages.sort(key=lambda t: t[1].start_token)
+        self._sync_layers()
         chosen, evicted_bytes = [], 0
-        for layer, page in gpu_pages:
-            if evicted_bytes >= bytes_to_evict:
-                break
-            chosen.append((layer, page))
-            evicted_bytes += _page_bytes(page)
+        while self._evq and evicted_bytes < bytes_to_evict:
+            _, _, idx, _, layer, page, nb = heapq.heappop(self._evq)
+            self._ev_bytes -= nb
+            if not (idx < len(layer.pages) and layer.pages[idx] is page
+                    and self._is_evictable(page, layer.tail_page)):
+                continue            # changed since it was queued
+            chosen.append((layer, idx, page))
+            evicted_bytes += nb
         if not chosen:
             _record_eviction(0, 0)
             return
-        new_pages = self.allocator.move_pages([p for _, p in chosen], torch.device('cpu'),
+        new_pages = self.allocator.move_pages([p for _, _, p in chosen], torch.device('cpu'),
                                               sync=_evict_sync())
         moved_bytes = 0
-        for (layer, page), new_page in zip(chosen, new_pages):
+        for (layer, idx, page), new_page in zip(chosen, new_pages):
             assert new_page.start_token == page.start_token, "Page invariant broken during migration"
-            idx = next(i for i, p in enumerate(layer.pages) if p is page)
-            layer.pages[idx] = new_page
-            if layer.tail_page is page:
-                layer.tail_page = new_page
+            layer._replace_page(idx, new_page)
             moved_bytes += _page_bytes(new_page)
         _record_eviction(len(new_pages), moved_bytes)
 
     def _enforce_residency_policy(self):
         """Evict the excess of evictable GPU bytes over the watermark
         (kv_cache.py:224-235)."""
-        gpu_bytes = 0
-        for layer in self.layers.values():
-            tail = layer.tail_page
-            for page in layer.pages:
-                if (page.state == 'GPU' and page.device.type == 'cuda' and page is not tail
-                        and page.used_tokens == page.capacity_tokens):
-                    gpu_bytes += _page_bytes(page)
-        if gpu_bytes > self.gpu_high_watermark_bytes:
-            self.evict_pages(gpu_bytes - self.gpu_high_watermark_bytes)
+        self._sync_layers()
+        if self._ev_bytes > self.gpu_high_watermark_bytes:
+            self.evict_pages(self._ev_bytes - self.gpu_high_watermark_bytes)
 
     def seq_len(self):
         if 0 in self.layers:
@@ -310,10 +473,9 @@ class KVCacheManager:
             for page in layer.pages:
                 if page.state != 'DEAD':
                     self.allocator.free(page)
-            layer.pages.clear()
-            layer.tail_page = None
-            layer.total_tokens = 0
+            layer._reset()
         self.layers.clear()
+        self._resync()
 
     def all_gpu_resident(self, layer_id: int) -> bool:
         if layer_id not in self.layers:
@@ -476,18 +638,7 @@ def _attend(query: torch.Tensor, seqs: Sequence[Sequence[_Segment]], Hkv: int, k
             scale: float, attention_mask: Optional[torch.Tensor], softcap: Optional[float],
             causal: bool) -> torch.Tensor:
     """One helm_stream_attn call: query [B,Hq,S,D], seqs[b] = ordered segments."""
-    device = query.device
-    B, Hq, S, D = query.shape
-    if Hq % Hkv != 0:
-        raise ValueError(f"num_q_heads {Hq} is not a multiple of num_kv_heads {Hkv}")
-    kcode = _native.dtype_code(kv_dtype)
-    q = query
-    if q.dtype != kv_dtype and q.dtype != torch.float32:
-        q = q.float()
-    q = q.contiguous()
-    qcode = _native.dtype_code(q.dtype)
-    out = torch.empty(q.shape, dtype=q.dtype, device=device)
-
+    B = query.size(0)
     n = sum(len(s) for s in seqs)
     arr = np.zeros(n, dtype=_native.PAGE_DTYPE)
     seq_off = np.zeros(B + 1, dtype=np.int32)
@@ -502,6 +653,28 @@ def _attend(query: torch.Tensor, seqs: Sequence[Sequence[_Segment]], Hkv: int, k
             i += 1
         seq_off[b + 1] = i
         t_max = max(t_max, tok)
+    return _attend_records(query, arr, seq_off, t_max, Hkv, kv_dtype, scale, attention_mask,
+                           softcap, causal)
+
+
+def _attend_records(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarray, t_max: int,
+                    Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
+                    softcap: Optional[float], causal: bool) -> torch.Tensor:
+    """One helm_stream_attn call over prepared ``helm_page`` records: sequence
+    b owns records seq_off[b]:seq_off[b+1] (token offsets per sequence), the
+    longest sequence holds t_max tokens."""
+    device = query.device
+    B, Hq, S, D = query.shape
+    if Hq % Hkv != 0:
+        raise ValueError(f"num_q_heads {Hq} is not a multiple of num_kv_heads {Hkv}")
+    kcode = _native.dtype_code(kv_dtype)
+    q = query
+    if q.dtype != kv_dtype and q.dtype != torch.float32:
+        q = q.float()
+    q = q.contiguous()
+    qcode = _native.dtype_code(q.dtype)
+    out = torch.empty(q.shape, dtype=q.dtype, device=device)
+    n = int(seq_off[B])
 
     mask_ptr, mbs, mhs, mqs = None, 0, 0, 0
     m = None

@@ -138,14 +138,21 @@ int helm_paged_decode_attn(const void* q, void* out,
  * drop-in for perform_streaming_attention (helm/runtime/kv_cache.py:405-662),
  * all four paths.  `pages` (host array) holds the active pages of every
  * sequence, sequence b owning pages[seq_off[b] .. seq_off[b+1]) (host array of
- * B+1).  Pages flagged HELM_PAGE_HOST are copied into the engine's device
- * staging ring with hipMemcpyAsync on `stream` (runs of adjacent host pages
- * become one copy, up to chunk_bytes per chunk), each chunk's attention
- * launch queued right behind its copy, after the launch over the device
- * pages; the split merge follows, all on `stream`.  causal != 0 applies a
- * top-left causal mask (key t visible to query
- * row s iff t <= s), HELM's is_causal=q_len>1 of Path 1.  A sequence with no
- * pages yields zeros.  Host pages require B == 1. */
+ * B+1).  A page flagged HELM_PAGE_HOST whose K and V each lie in one pinned
+ * host allocation that the device maps at the same address (hipHostMalloc,
+ * torch pin_memory) can be read in place by the attention kernel over the
+ * host link, like a device page (see helm_host_pages_in_place); it is, unless
+ * B == 1 and the call's host pages coalesce into large address runs (mean
+ * >= 2 MiB), which copy faster.  Other host pages
+ * are copied into the engine's device staging ring with hipMemcpyAsync on
+ * `stream` (runs of adjacent host pages become one copy, up to chunk_bytes
+ * per chunk), each chunk's attention launch queued right behind its copy,
+ * after the launch over the resident pages; the split merge follows, all on
+ * `stream`.  causal != 0 applies a top-left causal mask (key t visible to
+ * query row s iff t <= s), HELM's is_causal=q_len>1 of Path 1.  A sequence
+ * with no pages yields zeros.  Staged host pages require B == 1
+ * (HELM_E_UNSUPPORTED otherwise).  Environment HELM_AMD_HOST_READ=copy stages
+ * every host page, =direct reads every readable one in place. */
 int helm_stream_attn(helm_engine* eng, const void* q, void* out,
                      int B, int Hq, int Hkv, int q_len, int D,
                      const helm_page* pages, const int32_t* seq_off,
@@ -153,6 +160,16 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out,
                      const float* mask, int64_t mask_bstride,
                      int64_t mask_hstride, int64_t mask_qstride, int causal,
                      int kv_dtype, int q_dtype, void* stream);
+
+/* For each of n page records: in_place[i] = 1 when page i is flagged
+ * HELM_PAGE_HOST and helm_stream_attn would read it in place (its K and V
+ * regions, Hkv heads of head_stride elements, each inside one pinned host
+ * allocation mapped at the same address; a B == 1 call may still stage such
+ * pages when they form large runs), else 0.  Queries the HIP runtime
+ * only; launches nothing.  Reports what perform_streaming_attention's host
+ * pages cost (kv_cache.py:584-662): read over the link, or staged. */
+int helm_host_pages_in_place(helm_engine* eng, const helm_page* pages, int n,
+                             int Hkv, int D, int kv_dtype, uint8_t* in_place);
 
 /* ---- page movement -------------------------------------------------------- */
 

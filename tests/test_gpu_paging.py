@@ -22,6 +22,18 @@ DEV = torch.device("cuda:0")
 CPU = torch.device("cpu")
 
 
+@pytest.fixture(params=["auto", "direct", "copy"])
+def host_read(request, monkeypatch):
+    """Host pages read in place by the kernel or staged through the device ring
+    by hipMemcpyAsync: chosen per call (default), always in place when
+    readable (HELM_AMD_HOST_READ=direct), always staged (=copy)."""
+    if request.param == "auto":
+        monkeypatch.delenv("HELM_AMD_HOST_READ", raising=False)
+    else:
+        monkeypatch.setenv("HELM_AMD_HOST_READ", request.param)
+    return request.param
+
+
 def _positional_kv(n, start, H=2, D=8, dtype=torch.float32, device=DEV):
     """K[h, t, d] = (start + t) * 1000 + h * 10 + d / 16 — every element names
     its token, head and dim exactly (bit-exact gather checks)."""
@@ -156,7 +168,7 @@ def test_residency_matches_paging_model(watermark_pages):
 
 @pytest.mark.parametrize("dtype,H,kvh", [(torch.bfloat16, 32, 8), (torch.float16, 40, 40),
                                         (torch.float32, 4, 2)])
-def test_mixed_residency_attention(dtype, H, kvh):
+def test_mixed_residency_attention(dtype, H, kvh, host_read):
     """Attention after evicting the oldest pages equals the fp64 oracle over
     the same tokens; the prefetch counters record the host pages."""
     D, P, T = 128, 16, 700
@@ -194,7 +206,7 @@ def _ring_engine(chunk, slots):
     return lib, h
 
 
-def test_staging_ring_reuse_many_chunks():
+def test_staging_ring_reuse_many_chunks(host_read):
     """More staged chunks than ring slots: every slot is reused several times
     in one call and across calls; results stay exact to the oracle."""
     w = W.Workload("t", 1, 32, 8, 128, torch.bfloat16, T=4096)
@@ -240,6 +252,122 @@ def test_staging_ring_reuse_many_chunks():
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
+def _kv_records(parts, Hkv, D, P):
+    """helm_page records over [(slots tensor, slot index, host flag)], in order."""
+    slot_b = 2 * Hkv * P * D * 2
+    rec = np.zeros(len(parts), dtype=_native.PAGE_DTYPE)
+    for j, (t, i, host) in enumerate(parts):
+        base = t.data_ptr() + i * slot_b
+        rec[j] = (base, base + slot_b // 2, P, P * j, P * D, _native.HELM_PAGE_HOST if host else 0)
+    return rec
+
+
+def test_host_pages_in_place_and_mixed_host_memory(host_read):
+    """Pinned host pages are read in place, pageable ones staged: the in-place
+    query says which; a call mixing device, pinned and pageable pages equals
+    the oracle; a batched call is refused only when a page must be staged."""
+    from helm_amd.runtime import engine
+    Hkv, D, P, Hq = 8, 128, 16, 32
+    g = torch.Generator().manual_seed(4)
+    pinned = torch.randn(8, 2, Hkv, P, D, generator=g).bfloat16().pin_memory()
+    pageable = torch.randn(8, 2, Hkv, P, D, generator=g).bfloat16()
+    devp = torch.randn(8, 2, Hkv, P, D, generator=g).bfloat16().to(DEV)
+    parts = []
+    for i in range(8):
+        parts += [(pinned, i, True), (devp, i, False), (pageable, i, True)]
+    rec = _kv_records(parts, Hkv, D, P)
+    eng = engine.get_engine(DEV)
+    flags = np.zeros(len(rec), dtype=np.uint8)
+    _native.call("helm_host_pages_in_place", eng, _native.ptr(rec), len(rec), Hkv, D,
+                 _native.HELM_BF16, _native.ptr(flags))
+    want = [1 if (t is pinned and host_read != "copy") else 0 for t, _, _ in parts]
+    assert flags.tolist() == want
+    q = torch.randn(2, Hq, 1, D, generator=g).bfloat16()
+    K = torch.cat([t[i, 0].cpu().float() for t, i, _ in parts], 1)
+    V = torch.cat([t[i, 1].cpu().float() for t, i, _ in parts], 1)
+    ref = A.attention_fp64_batched(q[0].float(), K, V)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(recs, qd):
+        B = qd.size(0)
+        arr = np.concatenate(recs)
+        off = np.cumsum([0] + [len(r) for r in recs]).astype(np.int32)
+        out = torch.empty_like(qd)
+        _native.call("helm_stream_attn", eng, qd.data_ptr(), out.data_ptr(), B, Hq, Hkv, 1, D,
+                     _native.ptr(arr), _native.ptr(off), 1 / math.sqrt(D), 0.0, None, 0, 0, 0,
+                     0, _native.HELM_BF16, _native.HELM_BF16, stream)
+        return out
+
+    qd = q.to(DEV)
+    out = call([rec], qd[:1])
+    assert (out[0].double().cpu() - ref).abs().max().item() <= 1e-2
+    with pytest.raises(NotImplementedError):
+        call([rec, rec], qd)
+    pin_only = _kv_records([p for p in parts if p[0] is not pageable], Hkv, D, P)
+    K2 = torch.cat([t[i, 0].cpu().float() for t, i, _ in parts if t is not pageable], 1)
+    V2 = torch.cat([t[i, 1].cpu().float() for t, i, _ in parts if t is not pageable], 1)
+    if host_read != "copy":
+        out = call([pin_only, pin_only], qd)
+        for b in range(2):
+            ref2 = A.attention_fp64_batched(q[b].float(), K2, V2)
+            assert (out[b].double().cpu() - ref2).abs().max().item() <= 1e-2
+    else:
+        with pytest.raises(NotImplementedError):
+            call([pin_only, pin_only], qd)
+    torch.cuda.synchronize()
+
+
+def test_large_contiguous_host_runs(host_read):
+    """64 MiB of host pages in one address run (staged by default, in place
+    with HELM_AMD_HOST_READ=direct) behind scattered device pages: both
+    equal the oracle."""
+    from helm_amd.runtime import engine
+    Hkv, D, P, Hq, n = 8, 128, 16, 32, 1024
+    g = torch.Generator().manual_seed(8)
+    host = torch.randn(n, 2, Hkv, P, D, generator=g).bfloat16().pin_memory()
+    devp = torch.randn(256, 2, Hkv, P, D, generator=g).bfloat16().to(DEV)
+    perm = torch.randperm(256, generator=g).tolist()
+    parts = [(host, i, True) for i in range(n)] + [(devp, i, False) for i in perm]
+    rec = _kv_records(parts, Hkv, D, P)
+    q = torch.randn(1, Hq, 1, D, generator=g).bfloat16()
+    out = torch.empty(1, Hq, 1, D, dtype=torch.bfloat16, device=DEV)
+    qd = q.to(DEV)
+    off = np.array([0, len(rec)], dtype=np.int32)
+    _native.call("helm_stream_attn", engine.get_engine(DEV), qd.data_ptr(), out.data_ptr(), 1,
+                 Hq, Hkv, 1, D, _native.ptr(rec), _native.ptr(off), 1 / math.sqrt(D), 0.0, None,
+                 0, 0, 0, 0, _native.HELM_BF16, _native.HELM_BF16,
+                 torch.cuda.current_stream().cuda_stream)
+    K = torch.cat([host[:, 0].permute(1, 0, 2, 3).reshape(Hkv, -1, D).float(),
+                   devp[perm, 0].permute(1, 0, 2, 3).reshape(Hkv, -1, D).cpu().float()], 1)
+    V = torch.cat([host[:, 1].permute(1, 0, 2, 3).reshape(Hkv, -1, D).float(),
+                   devp[perm, 1].permute(1, 0, 2, 3).reshape(Hkv, -1, D).cpu().float()], 1)
+    ref = A.attention_fp64_batched(q[0].float(), K, V)
+    assert (out[0].double().cpu() - ref).abs().max().item() <= 1e-2
+
+
+def test_in_place_query_forgets_freed_pinned_memory():
+    """A pinned allocation that was released is no longer reported readable
+    in place (the engine re-checks cached allocations on every call); no
+    kernel runs on the released memory."""
+    from helm_amd.runtime import engine
+    if not hasattr(torch._C, "_host_emptyCache"):
+        pytest.skip("torch cannot release cached pinned memory")
+    Hkv, D, P = 2, 128, 16
+    eng = engine.get_engine(DEV)
+    t = torch.zeros(4, 2, Hkv, P, D, dtype=torch.bfloat16).pin_memory()
+    rec = _kv_records([(t, i, True) for i in range(4)], Hkv, D, P)
+    flags = np.zeros(4, dtype=np.uint8)
+    _native.call("helm_host_pages_in_place", eng, _native.ptr(rec), 4, Hkv, D,
+                 _native.HELM_BF16, _native.ptr(flags))
+    assert flags.tolist() == [1, 1, 1, 1]
+    del t
+    torch.cuda.synchronize()
+    torch._C._host_emptyCache()
+    _native.call("helm_host_pages_in_place", eng, _native.ptr(rec), 4, Hkv, D,
+                 _native.HELM_BF16, _native.ptr(flags))
+    assert flags.tolist() == [0, 0, 0, 0]
+
+
 def test_decode_batched_poison_pad_on_gpu():
     """test_kv_offload.py:168-245 on the GPU path."""
     torch.manual_seed(0)
@@ -264,7 +392,7 @@ def test_decode_batched_poison_pad_on_gpu():
         kvcm.clear()
 
 
-def test_decode_batched_ragged_batch_and_offload():
+def test_decode_batched_ragged_batch_and_offload(host_read):
     """Batched decode over per-item managers with ragged lengths (one kernel
     call) and with evicted pages (per-item streaming) agree with the oracle."""
     H, kvh, D = 8, 2, 64
@@ -293,6 +421,69 @@ def test_decode_batched_ragged_batch_and_offload():
             assert (out[i].double().cpu() - ref).abs().max().item() <= 2e-3
         for m in kvcms:
             m.clear()
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_decode_from_layer_records_matches_page_list_path(masked, monkeypatch, host_read):
+    """Decode steps over several layers with the watermark evicting a page at
+    every page boundary: the layer-record path (host pages streamed through
+    the staging ring) and HELM's page-list path (HELM_DISABLE_ASYNC_KV: host
+    pages copied to the device first) agree with the fp64 oracle every step
+    and record the same paging counters."""
+    Hq, kvh, D, P, L = 8, 2, 128, 16, 3
+    lens = [70, 45]
+    page_bytes = 2 * kvh * P * D * 2
+    g = torch.Generator().manual_seed(11)
+    pre = [[(torch.randn(1, kvh, n, D, generator=g).bfloat16(),
+             torch.randn(1, kvh, n, D, generator=g).bfloat16()) for n in lens] for _ in range(L)]
+    steps = 20
+    qs = torch.randn(steps, L, 2, Hq, 1, D, generator=g).bfloat16()
+    kds = torch.randn(steps, L, 2, kvh, 1, D, generator=g).bfloat16()
+    vds = torch.randn(steps, L, 2, kvh, 1, D, generator=g).bfloat16()
+    results = {}
+    for mode in ("records", "pages"):
+        if mode == "pages":
+            monkeypatch.setenv("HELM_DISABLE_ASYNC_KV", "1")
+        a = KVAllocator(L, kvh, D, page_size=P, dtype=torch.bfloat16)
+        kvcms = [KVCacheManager(a, gpu_high_watermark_bytes=3 * page_bytes) for _ in lens]
+        for lid in range(L):
+            for m, (k, v) in zip(kvcms, pre[lid]):
+                m.append_prefill(lid, k.to(DEV), v.to(DEV))
+        KC.reset_paging_stats()
+        outs = []
+        for s in range(steps):
+            for lid in range(L):
+                mask = None
+                if masked:
+                    n = lens[0] + s + 1
+                    mask = torch.zeros(2, 1, 1, n)
+                    mask[..., ::7] = float("-inf")
+                    mask = mask.to(DEV)
+                outs.append(_decode_batched(kvcms, qs[s, lid].to(DEV), kds[s, lid].to(DEV),
+                                            vds[s, lid].to(DEV), lid, 1 / math.sqrt(D),
+                                            attention_mask=mask).cpu())
+        results[mode] = (outs, KC.get_paging_stats())
+        assert any(layer._n_host for m in kvcms for layer in m.layers.values())
+        # the last step of every layer against the oracle
+        for lid in range(L):
+            for i, m in enumerate(kvcms):
+                K, V = _gather(m, lid)
+                n = K.size(2)
+                mask = None
+                if masked:
+                    mask = torch.zeros(1, 1, n, dtype=torch.float64)
+                    mask[..., ::7] = float("-inf")
+                ref = A.attention_fp64_batched(qs[steps - 1, lid, i].float(), K[0].float(),
+                                               V[0].float(), mask=mask)
+                got = outs[(steps - 1) * L + lid][i].double()
+                assert (got - ref).abs().max().item() <= 1e-2
+        for m in kvcms:
+            m.clear()
+        monkeypatch.delenv("HELM_DISABLE_ASYNC_KV", raising=False)
+    (o_rec, s_rec), (o_pg, s_pg) = results["records"], results["pages"]
+    assert s_rec == s_pg and s_rec["prefetch_calls"] > 0
+    for x, y in zip(o_rec, o_pg):
+        assert (x.float() - y.float()).abs().max().item() <= 1e-2
 
 
 def test_tiny_llama_greedy_matches_hf_with_eviction():

@@ -245,3 +245,113 @@ def test_offload_config_defaults():
     cfg = KVOffloadConfig(num_layers=36, num_kv_heads=8, head_dim=128, dtype=torch.bfloat16)
     assert cfg.page_size == 64 and cfg.cont_capacity == 0
     assert cfg.gpu_watermark_bytes == 512 * 2 * 8 * 128 * 2 * 36
+
+
+# ── residency bookkeeping at scale, on CPU ───────────────────────────────────
+class _CpuBackedGpuAllocator(KVAllocator):
+    """Hands the manager pages marked GPU-resident whose tensors live in CPU
+    memory, so the residency and eviction bookkeeping runs without a GPU
+    (evicted pages become real CPU pages)."""
+
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        self._moving = False
+
+    def allocate(self, device):
+        if self._moving:
+            return super().allocate(device)
+        page = super().allocate(CPU)
+        page.device, page.state = torch.device("cuda", 0), "GPU"
+        return page
+
+    def move_pages(self, pages, target_device, sync=True):
+        self._moving = True
+        try:
+            return super().move_pages(pages, target_device, sync)
+        finally:
+            self._moving = False
+
+
+def _pos_kv(n, start, H, D):
+    pos = torch.arange(start, start + n, dtype=torch.float32)
+    k = pos.view(1, 1, n, 1).expand(1, H, n, D).contiguous()
+    return k, -k
+
+
+@pytest.mark.parametrize("seed,watermark_pages", [(0, 0), (1, 3), (2, 11), (3, 40)])
+def test_eviction_order_matches_paging_model(seed, watermark_pages):
+    """Oldest-first eviction across many layers, ties broken by layer then page
+    order, equals the paging model's full rescan and stable sort
+    (kv_cache.py:179-235) over a long random append sequence."""
+    H, D, P, L = 2, 4, 4, 6
+    page_bytes = 2 * H * P * D * 4
+    wm = watermark_pages * page_bytes
+    a = _CpuBackedGpuAllocator(L, H, D, page_size=P, dtype=torch.float32)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=wm)
+    model = CacheModel(AllocatorModel(P, page_bytes), wm)
+    KC.reset_paging_stats()
+    rng = np.random.default_rng(seed)
+    totals = [0] * L
+    for _ in range(400):
+        lid = int(rng.integers(0, L))
+        if rng.random() < 0.2:
+            n = int(rng.integers(1, 3 * P))
+            mgr.append_prefill(lid, *_pos_kv(n, totals[lid], H, D))
+            model.append_prefill(lid, n)
+            totals[lid] += n
+        else:
+            mgr.append_decode(lid, *_pos_kv(1, totals[lid], H, D))
+            model.append_decode(lid)
+            totals[lid] += 1
+    for lid in model.layers:
+        got = [(p.start_token, p.used_tokens, p.state) for p in mgr.layers[lid].pages]
+        ref = [(p.start_token, p.used_tokens, p.state) for p in model.layers[lid].pages]
+        assert got == ref
+        k = torch.cat([p.k_tensor[0, 0, :p.used_tokens, 0] for p in mgr.layers[lid].pages])
+        assert torch.equal(k, torch.from_numpy(model.gathered(lid)).float())
+    s = KC.get_paging_stats()
+    assert (s["evict_calls"], s["pages_evicted"], s["bytes_evicted"]) == (
+        model.stats["evict_calls"], model.stats["pages_evicted"], model.stats["bytes_evicted"])
+    # the running total equals HELM's rescan of evictable bytes
+    assert mgr._ev_bytes == page_bytes * len(mgr._evictable())
+
+
+def test_layer_records_follow_pages():
+    """Each layer's page records carry the pages' addresses, used counts and
+    running token offsets through prefill, decode and eviction."""
+    H, D, P = 2, 8, 4
+    a = _CpuBackedGpuAllocator(2, H, D, page_size=P, dtype=torch.float16)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=2 * (2 * H * P * D * 2))
+    rng = np.random.default_rng(5)
+    for _ in range(60):
+        lid = int(rng.integers(0, 2))
+        if rng.random() < 0.3:
+            mgr.append_prefill(lid, *_kv(int(rng.integers(1, 10))))
+        else:
+            mgr.append_decode(lid, *_kv(1))
+        for layer in mgr.layers.values():
+            r = layer.records()
+            pages = layer.pages
+            assert r is not None and len(r) == len(pages)
+            assert list(r["used"]) == [p.used_tokens for p in pages]
+            assert list(r["tok_off"]) == list(np.cumsum([0] + [p.used_tokens for p in pages])[:-1])
+            assert list(r["k"]) == [p.k_tensor.data_ptr() for p in pages]
+            assert list(r["v"]) == [p.v_tensor.data_ptr() for p in pages]
+            assert set(r["head_stride"]) == {P * D}
+            assert layer._n_host == sum(p.state == "CPU" for p in pages)
+            assert layer._host_bytes == sum(p.used_tokens * H * D * 2 * 2 for p in pages
+                                            if p.state == "CPU")
+
+
+def test_external_layer_changes_rebuild_the_heap():
+    H, D, P = 2, 4, 4
+    a = _CpuBackedGpuAllocator(3, H, D, page_size=P, dtype=torch.float32)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 9)
+    for lid in range(3):
+        mgr.append_prefill(lid, *_pos_kv(3 * P, 0, H, D))
+    assert mgr._ev_bytes == 6 * (2 * H * P * D * 4)
+    del mgr.layers[1]
+    mgr.append_decode(0, *_pos_kv(1, 3 * P, H, D))
+    assert mgr._ev_bytes == (2 + 2) * (2 * H * P * D * 4) + (2 * H * P * D * 4)
+    mgr.clear()
+    assert mgr._ev_bytes == 0 and mgr._evq == []
