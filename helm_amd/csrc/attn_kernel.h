@@ -335,23 +335,39 @@ struct PoolSrc {
   }
 };
 
-// Explicit page descriptors (device addresses), sequence b owns
-// pages[seq_off[b] .. seq_off[b+1]).
+// Explicit page descriptors (device addresses).  Either sequence b owns
+// pages[seq_off[b] .. seq_off[b+1]) (both device arrays), or (by_value) the
+// launch carries each sequence's own record array, page count and token count
+// in its arguments: then a page's used tokens are capped at the tokens the
+// sequence holds past the page's offset, so the last page's record may keep
+// its full capacity while tokens are appended to it.
+constexpr int kSeqArgs = 16;
+
 struct DescSrc {
   const helm_page* pages;
   const int32_t* seq_off;
   int elem_bytes;
+  int by_value;
+  const helm_page* seq_pages[kSeqArgs];
+  int seq_n[kSeqArgs];
+  int seq_tokens[kSeqArgs];
 
+  __device__ __forceinline__ const helm_page* base(int b) const {
+    return by_value ? seq_pages[b] : pages + sload(seq_off + b);
+  }
   __device__ __forceinline__ int n_pages(int b) const {
-    return sload(seq_off + b + 1) - sload(seq_off + b);
+    return by_value ? seq_n[b] : sload(seq_off + b + 1) - sload(seq_off + b);
+  }
+  __device__ __forceinline__ int used_of(const helm_page& d, int b) const {
+    return by_value ? min(d.used, seq_tokens[b] - d.tok_off) : d.used;
   }
   __device__ __forceinline__ PageView page(int b, int p, int hk) const {
-    const helm_page d = sload(pages + sload(seq_off + b) + p);
+    const helm_page d = sload(base(b) + p);
     PageView pv;
     const int64_t off = (int64_t)hk * d.head_stride * elem_bytes;
     pv.k = reinterpret_cast<const char*>(d.k) + off;
     pv.v = reinterpret_cast<const char*>(d.v) + off;
-    pv.used = d.used;
+    pv.used = used_of(d, b);
     pv.tok_off = d.tok_off;
     pv.head_stride_b = 0;
     return pv;

@@ -117,16 +117,16 @@ __device__ __forceinline__ PoolLanes lane_pages(const PoolSrc& s, int b, int pg0
   return L;
 }
 __device__ __forceinline__ DescLanes lane_pages(const DescSrc& s, int b, int pg0, int lane) {
-  const int base = sload(s.seq_off + b);
-  const int cnt = sload(s.seq_off + b + 1) - base;
+  const helm_page* base = s.base(b);
+  const int cnt = s.n_pages(b);
   helm_page d{};
-  if (cnt > 0) d = s.pages[base + max(0, min(pg0 + lane, cnt - 1))];
+  if (cnt > 0) d = base[max(0, min(pg0 + lane, cnt - 1))];
   DescLanes L;
   L.klo = static_cast<uint32_t>(d.k);
   L.khi = static_cast<uint32_t>(d.k >> 32);
   L.vlo = static_cast<uint32_t>(d.v);
   L.vhi = static_cast<uint32_t>(d.v >> 32);
-  L.used = d.used;
+  L.used = s.used_of(d, b);
   L.tok_off = d.tok_off;
   L.head_stride = d.head_stride;
   return L;

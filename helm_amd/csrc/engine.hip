@@ -1014,6 +1014,96 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   return engine_mark_upload_consumed(eng, st);
 }
 
+int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
+                         int Hq, int Hkv, int q_len, int D,
+                         const uint64_t* seq_pages, const int32_t* seq_npages,
+                         const int32_t* seq_tokens, int page_tokens,
+                         int aligned16, float scale, float softcap,
+                         const float* mask, int64_t mask_bstride,
+                         int64_t mask_hstride, int64_t mask_qstride, int causal,
+                         int kv_dtype, int q_dtype, void* stream) {
+  if (!eng || !q || !out || !seq_pages || !seq_npages || !seq_tokens)
+    return fail(HELM_E_INVALID, "null pointer argument");
+  if (B <= 0 || Hkv <= 0 || D <= 0 || page_tokens <= 0)
+    return fail(HELM_E_INVALID, "bad shape");
+  if (B > kSeqArgs)
+    return fail(HELM_E_UNSUPPORTED,
+                "more than " + std::to_string(kSeqArgs) + " sequences per call");
+  const int eb = elem_bytes(kv_dtype);
+  const int qb = elem_bytes(q_dtype);
+  if (!eb || !qb) return fail(HELM_E_INVALID, "unknown dtype");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int max_pages = 0;
+  int64_t all_pages = 0;
+  for (int b = 0; b < B; ++b) {
+    if (seq_npages[b] < 0 || seq_tokens[b] < 0 ||
+        (int64_t)seq_tokens[b] > (int64_t)seq_npages[b] * page_tokens ||
+        (seq_npages[b] > 0 && !seq_pages[b]))
+      return fail(HELM_E_INVALID, "bad sequence " + std::to_string(b));
+    max_pages = std::max(max_pages, seq_npages[b]);
+    all_pages += seq_npages[b];
+  }
+  const bool al = aligned16 && aligned(q, 16) && aligned(out, 16) &&
+                  (D * qb) % 16 == 0;
+  Plan pl{};
+  int rc = make_plan(pl, kv_dtype, q_dtype, B, Hq, Hkv, q_len, D, page_tokens,
+                     std::max(max_pages, 1), (double)all_pages / B, 0, al);
+  if (rc != HELM_OK) return rc;
+  pl.max_splits = std::max(1, (max_pages + pl.pps - 1) / pl.pps);
+  pl.fused = fused_merge(pl.max_splits);
+  size_plan(pl, B, Hkv, D);
+  if (pl.o_bytes >= 0x7ffffff0u) pl.fused = 0;
+  rc = engine_ensure_ws(eng, pl.total(), st);
+  if (rc != HELM_OK) return rc;
+
+  LaunchSpec s{};
+  fill_params(s.p, pl, q, out, B, Hq, Hkv, q_len, D, scale, softcap, mask,
+              mask_bstride, mask_hstride, mask_qstride, causal, eng->ws);
+  s.p.full_d = (al && D == 16 * pl.epl) ? 1 : 0;
+  s.mode = 1;
+  s.desc.elem_bytes = eb;
+  s.desc.by_value = 1;
+  for (int b = 0; b < B; ++b) {
+    s.desc.seq_pages[b] = reinterpret_cast<const helm_page*>(seq_pages[b]);
+    s.desc.seq_n[b] = seq_npages[b];
+    s.desc.seq_tokens[b] = seq_tokens[b];
+  }
+  s.kv_dtype = kv_dtype;
+  s.q_dtype = q_dtype;
+  s.epl = pl.epl;
+  s.gm = pl.gm;
+  s.fast = pl.fast;
+  s.mfma = pl.mfma;
+  s.nw = pl.nw;
+  s.feat = (mask ? kFeatMask : 0) | (softcap > 0.f ? kFeatCap : 0) |
+           (causal ? kFeatCausal : 0);
+  s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.n_qtiles, B);
+  hipError_t e = dispatch(s, st);
+  if (e != hipSuccess) return hip_fail(e, "paged_attn_seqs launch");
+  e = launch_merge(s, B, Hkv, st);
+  if (e != hipSuccess) return hip_fail(e, "merge launch");
+  return HELM_OK;
+}
+
+int helm_upload(helm_engine* eng, void* dst, const void* src, size_t bytes,
+                void* stream) {
+  if (!eng || (bytes && (!dst || !src)))
+    return fail(HELM_E_INVALID, "null pointer argument");
+  if (!bytes) return HELM_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* host = nullptr;
+  char* dev = nullptr;
+  int rc = engine_upload_reserve(eng, bytes, &host, &dev);
+  if (rc != HELM_OK) return rc;
+  std::memcpy(host, src, bytes);
+  const int i = eng->up_next;
+  eng->up_next = (i + 1) % helm_engine::kUp;
+  HELM_HIP(hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, st));
+  HELM_HIP(hipEventRecord(eng->up_done[i], st));
+  eng->up_used[i] = 1;
+  return HELM_OK;
+}
+
 int helm_host_pages_in_place(helm_engine* eng, const helm_page* pages, int n,
                              int Hkv, int D, int kv_dtype, uint8_t* in_place) {
   if (!eng || (n > 0 && (!pages || !in_place)))

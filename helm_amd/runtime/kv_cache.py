@@ -129,6 +129,11 @@ class LayerKVCache:
         self._n_host = 0                # pages held in host memory
         self._host_bytes = 0            # their used K+V bytes
         self._n_other = 0               # pages neither GPU- nor CPU-resident
+        self._page_tokens = 0           # largest page capacity
+        self._aligned16 = True          # every K/V base and head stride 16-byte aligned
+        self._dev = None                # device copy of the records (uint8 tensor)
+        self._dev_dirty: List[int] = []  # records changed since the last upload
+        self._dev_all = False           # every record needs an upload
 
     def _reset(self) -> None:
         """Drops every page (the list is emptied in place)."""
@@ -138,6 +143,9 @@ class LayerKVCache:
         self._rec_ok, self._rec_sig = True, None
         self._tier.clear()
         self._n_host = self._host_bytes = self._n_other = 0
+        self._page_tokens, self._aligned16 = 0, True
+        self._dev_dirty.clear()
+        self._dev_all = True
 
     def append_page(self, page: KVPage):
         self.pages.append(page)
@@ -152,6 +160,9 @@ class LayerKVCache:
                         if n > 1 else 0)
         self._tier.append((0, 0))
         self._set_record(n - 1, page)
+        # the old tail's device record takes its final token count
+        self._mark_dirty(n - 2)
+        self._mark_dirty(n - 1)
 
     def _set_record(self, idx: int, page: KVPage) -> None:
         """Writes page `idx`'s record and counts its residency tier."""
@@ -184,6 +195,10 @@ class LayerKVCache:
         r["k"], r["v"], r["head_stride"] = fields[0], fields[1], fields[2]
         r["used"] = page.used_tokens
         r["flags"] = _native.HELM_PAGE_HOST if fields[3] else 0
+        self._page_tokens = max(self._page_tokens, page.capacity_tokens, page.used_tokens)
+        es = page.k_tensor.element_size()
+        self._aligned16 = self._aligned16 and (fields[0] % 16 == 0 and fields[1] % 16 == 0
+                                               and (fields[2] * es) % 16 == 0)
 
     def _tail_filled(self) -> None:
         """The tail page gained tokens (its record's used count follows)."""
@@ -196,6 +211,54 @@ class LayerKVCache:
         if self.tail_page is old:
             self.tail_page = page
         self._set_record(idx, page)
+        self._mark_dirty(idx)
+
+    def _mark_dirty(self, idx: int) -> None:
+        if idx < 0 or self._dev_all:
+            return
+        self._dev_dirty.append(idx)
+        if len(self._dev_dirty) > 4096:
+            self._dev_all = True
+            self._dev_dirty.clear()
+
+    def _device_records(self, device: torch.device, eng, stream: int) -> torch.Tensor:
+        """The records in device memory, brought up to date on `stream`.
+
+        The device copy differs from the host records in one field: the tail
+        page's record keeps the page's capacity as its used count, so tokens
+        appended to the tail need no upload (the kernel caps each page at the
+        tokens its sequence holds); only new pages and pages that moved tier
+        are uploaded."""
+        n = len(self.pages)
+        rb = _native.PAGE_DTYPE.itemsize
+        if self._dev is None or self._dev.device != device or self._dev.numel() < n * rb:
+            old = self._dev
+            cap = max(n, 64, 2 * (old.numel() // rb if old is not None else 0))
+            self._dev = torch.empty(cap * rb, dtype=torch.uint8, device=device)
+            if old is not None and old.device == device:
+                self._dev[:old.numel()].copy_(old)
+            else:
+                self._dev_all = True
+        if self._dev_all:
+            self._dev_all = False
+            self._dev_dirty.clear()
+            runs = [(0, n)] if n else []
+        elif self._dev_dirty:
+            idx = np.unique(np.asarray(self._dev_dirty, dtype=np.int64))
+            self._dev_dirty.clear()
+            idx = idx[(idx >= 0) & (idx < n)]
+            cut = np.flatnonzero(np.diff(idx) != 1) + 1
+            runs = [(int(r[0]), int(r[-1]) + 1) for r in np.split(idx, cut) if len(r)]
+        else:
+            return self._dev
+        base = self._dev.data_ptr()
+        for lo, hi in runs:
+            chunk = self._rec[lo:hi].copy()
+            if hi == n:
+                chunk["used"][-1] = max(int(chunk["used"][-1]), self.tail_page.capacity_tokens)
+            _native.call("helm_upload", eng, base + lo * rb, _native.ptr(chunk),
+                         (hi - lo) * rb, stream)
+        return self._dev
 
     def records(self):
         """The pages' ``helm_page`` records in token order (a view), or None."""
@@ -657,25 +720,19 @@ def _attend(query: torch.Tensor, seqs: Sequence[Sequence[_Segment]], Hkv: int, k
                            softcap, causal)
 
 
-def _attend_records(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarray, t_max: int,
-                    Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
-                    softcap: Optional[float], causal: bool) -> torch.Tensor:
-    """One helm_stream_attn call over prepared ``helm_page`` records: sequence
-    b owns records seq_off[b]:seq_off[b+1] (token offsets per sequence), the
-    longest sequence holds t_max tokens."""
+def _query_and_mask(query: torch.Tensor, Hkv: int, kv_dtype, t_max: int,
+                    attention_mask: Optional[torch.Tensor]):
+    """The query in a kernel dtype, its output buffer and the mask arguments
+    (pointer, batch / head / row strides) of one attention call."""
     device = query.device
     B, Hq, S, D = query.shape
     if Hq % Hkv != 0:
         raise ValueError(f"num_q_heads {Hq} is not a multiple of num_kv_heads {Hkv}")
-    kcode = _native.dtype_code(kv_dtype)
     q = query
     if q.dtype != kv_dtype and q.dtype != torch.float32:
         q = q.float()
     q = q.contiguous()
-    qcode = _native.dtype_code(q.dtype)
     out = torch.empty(q.shape, dtype=q.dtype, device=device)
-    n = int(seq_off[B])
-
     mask_ptr, mbs, mhs, mqs = None, 0, 0, 0
     m = None
     if attention_mask is not None:
@@ -696,11 +753,49 @@ def _attend_records(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarray, t
         mbs = m.stride(0) if Bm > 1 else 0
         mhs = m.stride(1) if Hm > 1 else 0
         mqs = m.stride(2) if Sm > 1 else 0
+    return q, out, (mask_ptr, mbs, mhs, mqs), m
 
+
+def _attend_records(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarray, t_max: int,
+                    Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
+                    softcap: Optional[float], causal: bool) -> torch.Tensor:
+    """One helm_stream_attn call over prepared ``helm_page`` records: sequence
+    b owns records seq_off[b]:seq_off[b+1] (token offsets per sequence), the
+    longest sequence holds t_max tokens."""
+    device = query.device
+    B, Hq, S, D = query.shape
+    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, t_max, attention_mask)
+    n = int(seq_off[B])
     _native.call("helm_stream_attn", _engine.get_engine(device), q.data_ptr(), out.data_ptr(),
                  B, Hq, Hkv, S, D, _native.ptr(arr) if n else None, _native.ptr(seq_off),
-                 float(scale), float(softcap) if softcap is not None else 0.0, mask_ptr,
-                 mbs, mhs, mqs, 1 if causal else 0, kcode, qcode, _engine.stream_ptr(device))
+                 float(scale), float(softcap) if softcap is not None else 0.0, *margs,
+                 1 if causal else 0, _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype),
+                 _engine.stream_ptr(device))
+    return out if out.dtype == query.dtype else out.to(query.dtype)
+
+
+def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Sequence[int],
+                   Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
+                   softcap: Optional[float], causal: bool) -> torch.Tensor:
+    """One helm_paged_attn_seqs call: sequence b is layers[b]'s pages, read
+    through the layer's device-resident records (uploaded only where they
+    changed); lens[b] tokens.  Every page must be device-resident."""
+    device = query.device
+    B, Hq, S, D = query.shape
+    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, max(lens), attention_mask)
+    eng = _engine.get_engine(device)
+    stream = _engine.stream_ptr(device)
+    ptrs = np.array([layer._device_records(device, eng, stream).data_ptr() for layer in layers],
+                    dtype=np.uint64)
+    npages = np.array([len(layer.pages) for layer in layers], dtype=np.int32)
+    tokens = np.array(lens, dtype=np.int32)
+    page_tokens = max(layer._page_tokens for layer in layers)
+    aligned = all(layer._aligned16 for layer in layers)
+    _native.call("helm_paged_attn_seqs", eng, q.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
+                 _native.ptr(ptrs), _native.ptr(npages), _native.ptr(tokens), page_tokens,
+                 1 if aligned else 0, float(scale),
+                 float(softcap) if softcap is not None else 0.0, *margs, 1 if causal else 0,
+                 _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype), stream)
     return out if out.dtype == query.dtype else out.to(query.dtype)
 
 

@@ -27,8 +27,9 @@ import torch
 
 from helm_amd.runtime.kv_allocator import KVAllocator
 from helm_amd.runtime.kv_cache import (KVCacheManager, _async_kv_prefetch_enabled, _attend,
-                                       _attend_records, _contiguous_segments, _page_segments,
-                                       _record_prefetch, perform_streaming_attention)
+                                       _attend_layers, _attend_records, _contiguous_segments,
+                                       _page_segments, _record_prefetch,
+                                       perform_streaming_attention)
 
 
 # ── config (kv_offload.py:33-79) ───────────────────────────────────────────────
@@ -152,6 +153,9 @@ def _flush_appends(queues) -> None:
         head.flush()
 
 
+_MAX_SEQ_ARGS = 16     # sequences one helm_paged_attn_seqs call carries
+
+
 def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: float,
                          attention_mask: Optional[torch.Tensor]):
     """The decode attention of `_decode_batched` from the layers' page records.
@@ -186,6 +190,10 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
     # as a prefetch (kv_offload.py:176-186, kv_cache.py:441-447)
     for layer in layers:
         _record_prefetch(layer._n_host, layer._host_bytes)
+    if bsz <= _MAX_SEQ_ARGS and not any(layer._n_host for layer in layers):
+        # every page on the device: the layers' device-resident records
+        return _attend_layers(q, layers, lens, Hkv, kv_dtype, scale, attention_mask, None,
+                              False)
     if bsz == 1 or not any(layer._n_host for layer in layers):
         return _attend_records(q, arr, seq_off, max(lens), Hkv, kv_dtype, scale,
                                attention_mask, None, False)

@@ -161,6 +161,37 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out,
                      int64_t mask_hstride, int64_t mask_qstride, int causal,
                      int kv_dtype, int q_dtype, void* stream);
 
+/* Decode / chunk attention over page records that already sit in device
+ * memory, one record array per sequence — the batched all-GPU call of
+ * _decode_batched (helm/runtime/kv_offload.py:152-174) for caches whose page
+ * lists persist between steps.  Sequence b's records are the device array
+ * seq_pages[b] (an address, host array of B) of seq_npages[b] records in
+ * token order (tok_off ascending, each page but the last holding exactly its
+ * `used` tokens); it holds seq_tokens[b] tokens, so the last record may keep
+ * the page's capacity in `used` while tokens are appended (a page's tokens
+ * are min(used, seq_tokens[b] - tok_off)).  page_tokens bounds `used`.
+ * Every page must be readable by the device: device memory, or pinned host
+ * memory mapped at the same address (helm_host_pages_in_place); records are
+ * not checked.  aligned16 != 0 promises 16-byte aligned K/V bases and head
+ * strides.  B <= 16 (HELM_E_UNSUPPORTED otherwise).  Same semantics as
+ * helm_stream_attn otherwise; the engine's workspace serves the split
+ * partials, so calls on one engine are ordered on one stream. */
+int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
+                         int Hq, int Hkv, int q_len, int D,
+                         const uint64_t* seq_pages, const int32_t* seq_npages,
+                         const int32_t* seq_tokens, int page_tokens,
+                         int aligned16, float scale, float softcap,
+                         const float* mask, int64_t mask_bstride,
+                         int64_t mask_hstride, int64_t mask_qstride, int causal,
+                         int kv_dtype, int q_dtype, void* stream);
+
+/* Copies `bytes` from host memory `src` to device memory `dst` in the order
+ * of `stream`, through the engine's pinned staging ring (src may be reused
+ * as soon as the call returns).  Keeps device-resident page records current
+ * (the page-list bookkeeping of helm/runtime/kv_cache.py:77-86). */
+int helm_upload(helm_engine* eng, void* dst, const void* src, size_t bytes,
+                void* stream);
+
 /* For each of n page records: in_place[i] = 1 when page i is flagged
  * HELM_PAGE_HOST and helm_stream_attn would read it in place (its K and V
  * regions, Hkv heads of head_stride elements, each inside one pinned host

@@ -424,28 +424,37 @@ def test_decode_batched_ragged_batch_and_offload(host_read):
 
 
 @pytest.mark.parametrize("masked", [False, True])
-def test_decode_from_layer_records_matches_page_list_path(masked, monkeypatch, host_read):
-    """Decode steps over several layers with the watermark evicting a page at
-    every page boundary: the layer-record path (host pages streamed through
-    the staging ring) and HELM's page-list path (HELM_DISABLE_ASYNC_KV: host
-    pages copied to the device first) agree with the fp64 oracle every step
-    and record the same paging counters."""
+@pytest.mark.parametrize("evict", [True, False])
+@pytest.mark.parametrize("kernel", ["auto", "valu"])
+def test_decode_from_layer_records_matches_page_list_path(masked, evict, kernel, monkeypatch,
+                                                          host_read):
+    """Decode steps over several layers, crossing page boundaries: with the
+    watermark evicting a page at every boundary (layer-record path, host
+    pages read in place or staged) or with every page resident (the layers'
+    device-resident records, uploaded only when pages are added).  Both agree
+    with HELM's page-list path (HELM_DISABLE_ASYNC_KV: host pages copied to
+    the device first) and with the fp64 oracle, and record the same paging
+    counters."""
+    if kernel != "auto":
+        monkeypatch.setenv("HELM_AMD_KERNEL", kernel)
     Hq, kvh, D, P, L = 8, 2, 128, 16, 3
-    lens = [70, 45]
+    lens = [70, 45] if evict else [1100, 45, 301]
+    B = len(lens)
     page_bytes = 2 * kvh * P * D * 2
     g = torch.Generator().manual_seed(11)
     pre = [[(torch.randn(1, kvh, n, D, generator=g).bfloat16(),
              torch.randn(1, kvh, n, D, generator=g).bfloat16()) for n in lens] for _ in range(L)]
     steps = 20
-    qs = torch.randn(steps, L, 2, Hq, 1, D, generator=g).bfloat16()
-    kds = torch.randn(steps, L, 2, kvh, 1, D, generator=g).bfloat16()
-    vds = torch.randn(steps, L, 2, kvh, 1, D, generator=g).bfloat16()
+    qs = torch.randn(steps, L, B, Hq, 1, D, generator=g).bfloat16()
+    kds = torch.randn(steps, L, B, kvh, 1, D, generator=g).bfloat16()
+    vds = torch.randn(steps, L, B, kvh, 1, D, generator=g).bfloat16()
     results = {}
     for mode in ("records", "pages"):
         if mode == "pages":
             monkeypatch.setenv("HELM_DISABLE_ASYNC_KV", "1")
         a = KVAllocator(L, kvh, D, page_size=P, dtype=torch.bfloat16)
-        kvcms = [KVCacheManager(a, gpu_high_watermark_bytes=3 * page_bytes) for _ in lens]
+        wm = 3 * page_bytes if evict else 10 ** 12
+        kvcms = [KVCacheManager(a, gpu_high_watermark_bytes=wm) for _ in lens]
         for lid in range(L):
             for m, (k, v) in zip(kvcms, pre[lid]):
                 m.append_prefill(lid, k.to(DEV), v.to(DEV))
@@ -455,15 +464,15 @@ def test_decode_from_layer_records_matches_page_list_path(masked, monkeypatch, h
             for lid in range(L):
                 mask = None
                 if masked:
-                    n = lens[0] + s + 1
-                    mask = torch.zeros(2, 1, 1, n)
+                    n = max(lens) + s + 1
+                    mask = torch.zeros(B, 1, 1, n)
                     mask[..., ::7] = float("-inf")
                     mask = mask.to(DEV)
                 outs.append(_decode_batched(kvcms, qs[s, lid].to(DEV), kds[s, lid].to(DEV),
                                             vds[s, lid].to(DEV), lid, 1 / math.sqrt(D),
                                             attention_mask=mask).cpu())
         results[mode] = (outs, KC.get_paging_stats())
-        assert any(layer._n_host for m in kvcms for layer in m.layers.values())
+        assert any(layer._n_host for m in kvcms for layer in m.layers.values()) == evict
         # the last step of every layer against the oracle
         for lid in range(L):
             for i, m in enumerate(kvcms):
@@ -481,7 +490,7 @@ def test_decode_from_layer_records_matches_page_list_path(masked, monkeypatch, h
             m.clear()
         monkeypatch.delenv("HELM_DISABLE_ASYNC_KV", raising=False)
     (o_rec, s_rec), (o_pg, s_pg) = results["records"], results["pages"]
-    assert s_rec == s_pg and s_rec["prefetch_calls"] > 0
+    assert s_rec == s_pg and (s_rec["prefetch_calls"] > 0) == evict
     for x, y in zip(o_rec, o_pg):
         assert (x.float() - y.float()).abs().max().item() <= 1e-2
 
