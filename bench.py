@@ -13,7 +13,11 @@ Also measured (extra keys of the one JSON line):
 * the CPU baseline: HELM's CPU streaming attention restated by the oracle
   (torch CPU, HELM's Path 2 and masked online-softmax loop) on the same
   shape, timed on this host's cores for a bounded sample;
-* decode steps/s at 32k = 1 / (36 layers x per-layer call time).
+* decode steps/s at 32k = 1 / (36 layers x per-layer call time);
+* the full 40-layer Qwen3-14B decode step (batch 4 x 65,536 tokens, per layer
+  token append + residency policy + attention through the runtime API), with
+  the 64 GB device KV budget (nothing evicted) and with a 32 GB budget that
+  keeps about 25% of the pages in pinned host RAM.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -54,9 +58,9 @@ def parse():
     ap.add_argument("--pps", type=int, default=0, help="pages per split (0 = auto)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (PMC byte-count calibration)")
-    ap.add_argument("--full-step", action="store_true",
-                    help="also time the 40-layer Qwen3-14B B4 x 64k decode step (64 GB device "
-                         "KV budget, and a 32 GB budget that forces eviction)")
+    ap.add_argument("--no-full-step", action="store_true",
+                    help="skip the 40-layer Qwen3-14B B4 x 64k decode step (64 GB device KV "
+                         "budget, and a 32 GB budget that forces eviction)")
     ap.add_argument("--full-step-steps", type=int, default=64)
     ap.add_argument("--full-step-budgets", default="64,32",
                     help="device KV budgets (GB) of the full-step runs")
@@ -388,7 +392,7 @@ def main():
         all_configs(args, torch, W, paged)
 
     full = None
-    if args.full_step or args.all:
+    if not args.no_full_step:
         full = {}
         budgets = [float(x) for x in args.full_step_budgets.split(",") if x]
         for budget in budgets:
