@@ -38,6 +38,7 @@ constexpr int kRowLanes = 16;   // lanes per token row (one DPP row)
 constexpr int kBlockTok = 16;   // tokens per wave block (4 rows x 4 j)
 constexpr int kMaxPps = 256;    // pages per split held in LDS
 constexpr int kMaxSplits = 256; // splits per (sequence, head, tile) merged
+constexpr int kMergeBatch = 8;  // split partials a merging thread loads at once
 constexpr float kRescaleSlack = 8.f;  // lazy online-softmax rescale threshold
 
 // ---- element types ----------------------------------------------------------
@@ -428,52 +429,24 @@ __device__ __forceinline__ float4 ld_coherent16(__amdgpu_buffer_rsrc_t r, int64_
                             __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(elem * 4), 0, 16));
 }
 
-// Shared end of a split for every decode kernel (NW waves per workgroup).
-// On entry sm.o / sm.m / sm.l hold the per-wave online-softmax states of the
-// tile's `nrows` rows (a barrier has been passed).  Merges the waves and
-// writes the split's partial (m, l, o[D]) per row.  In fused mode the
-// partials are written agent-coherently, an atomic ticket counts the tile's
-// arrivals and the last split to arrive merges all of them and writes the
-// output; otherwise merge_splits_kernel does that after the kernel.
+// Fused mode's end of a split (its partials already written agent-coherently):
+// an atomic ticket counts the tile's arrivals and the last split to arrive
+// merges all of them and writes the output.  Callers branch to it as the
+// unlikely case, so the common (non-fused) end of a split stays a short
+// straight run of code: every workgroup executes it once, from a cold
+// instruction cache.
 template <typename TQ, int NW, int GM, int DMAX>
-__device__ __forceinline__ void split_epilogue(Smem<NW, GM, DMAX>& sm, const AttnParams& p,
-                                               int tid, int tile, int split, int total,
-                                               int nrows, int r0, int b, int hk) {
+__device__ __forceinline__ void fused_merge_tail(Smem<NW, GM, DMAX>& sm,
+                                                            const AttnParams& p, int tid,
+                                                            int tile, int total, int nrows,
+                                                            int r0, int b, int hk) {
   constexpr int NT = 64 * NW;
   constexpr int QB = ElemBytes<TQ>::v;
   const int D = p.D;
-  const int RS = p.rows_per_tile;  // workspace rows per (tile, split)
-  const int64_t part = ((int64_t)tile * p.max_splits + split) * RS;
+  const int RS = p.rows_per_tile;
   const int cw = (D % 4 == 0) ? 4 : 1;
   const int ncol_all = nrows * (D / cw);
   const auto pr = partials_rsrc(p);
-  for (int idx = tid; idx < ncol_all; idx += NT) {
-    const int g = idx / (D / cw);
-    const int d0 = (idx - g * (D / cw)) * cw;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm.m[w][g]);
-    const float base = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f;
-    float O[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float a = fexp(sm.m[w][g] - base);
-      L += a * sm.l[w][g];
-      for (int j = 0; j < cw; ++j) O[j] += a * sm.o[w][g][d0 + j];
-    }
-    float* dst = &p.ws_o[(part + g) * D + d0];
-    if (p.fused) {
-      if (cw == 4) st_coherent16(pr, (part + g) * D + d0, make_float4(O[0], O[1], O[2], O[3]));
-      else st_agent(dst, O[0]);
-      if (d0 == 0) st_agent_ml(&p.ws_ml[(part + g) * 2], M, L);
-    } else {
-      for (int j = 0; j < cw; ++j) dst[j] = O[j];
-      if (d0 == 0) *reinterpret_cast<float2*>(&p.ws_ml[(part + g) * 2]) = make_float2(M, L);
-    }
-  }
-  if (!p.fused) return;
-
   // ---- ticket: the last split of the tile merges -----------------------------
   // The barrier waits (vmcnt(0)) for every wave's coherent stores before the
   // agent-scope ticket increment; the merging workgroup reads the partials
@@ -577,6 +550,190 @@ __device__ __forceinline__ void split_epilogue(Smem<NW, GM, DMAX>& sm, const Att
   if (tid == 0) p.tickets[tile] = 0u;
 }
 
+// Shared end of a split for the vector-ALU decode kernels (NW waves per
+// workgroup).  On entry sm.o / sm.m / sm.l hold the per-wave online-softmax
+// states of the tile's `nrows` rows (a barrier has been passed).  Merges the waves and
+// writes the split's partial (m, l, o[D]) per row.  In fused mode the
+// partials are written agent-coherently, an atomic ticket counts the tile's
+// arrivals and the last split to arrive merges all of them and writes the
+// output; otherwise merge_splits_kernel does that after the kernel.
+template <typename TQ, int NW, int GM, int DMAX>
+__device__ __forceinline__ void split_epilogue(Smem<NW, GM, DMAX>& sm, const AttnParams& p,
+                                               int tid, int tile, int split, int total,
+                                               int nrows, int r0, int b, int hk) {
+  constexpr int NT = 64 * NW;
+  const int D = p.D;
+  const int RS = p.rows_per_tile;  // workspace rows per (tile, split)
+  const int64_t part = ((int64_t)tile * p.max_splits + split) * RS;
+  const int cw = (D % 4 == 0) ? 4 : 1;
+  const int ncol_all = nrows * (D / cw);
+  const auto pr = partials_rsrc(p);
+  for (int idx = tid; idx < ncol_all; idx += NT) {
+    const int g = idx / (D / cw);
+    const int d0 = (idx - g * (D / cw)) * cw;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm.m[w][g]);
+    const float base = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f;
+    float O[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float a = fexp(sm.m[w][g] - base);
+      L += a * sm.l[w][g];
+      for (int j = 0; j < cw; ++j) O[j] += a * sm.o[w][g][d0 + j];
+    }
+    float* dst = &p.ws_o[(part + g) * D + d0];
+    if (p.fused) {
+      if (cw == 4) st_coherent16(pr, (part + g) * D + d0, make_float4(O[0], O[1], O[2], O[3]));
+      else st_agent(dst, O[0]);
+      if (d0 == 0) st_agent_ml(&p.ws_ml[(part + g) * 2], M, L);
+    } else {
+      for (int j = 0; j < cw; ++j) dst[j] = O[j];
+      if (d0 == 0) *reinterpret_cast<float2*>(&p.ws_ml[(part + g) * 2]) = make_float2(M, L);
+    }
+  }
+  if (__builtin_expect(p.fused, 0))
+    fused_merge_tail<TQ, NW, GM, DMAX>(sm, p, tid, tile, total, nrows, r0, b, hk);
+}
+
+// The same end of a split for the matrix-core kernel (D = 128, GM rows): the
+// waves' row states are merged and each row's partial goes out as 16-byte
+// stores, with the column arithmetic fixed at compile time.
+template <typename TQ, int NW, int GM>
+__device__ __forceinline__ void split_epilogue_d128(Smem<NW, GM, 128>& sm, const AttnParams& p,
+                                                    int tid, int tile, int split, int total,
+                                                    int nrows, int r0, int b, int hk) {
+  constexpr int NT = 64 * NW;
+  const int64_t part = ((int64_t)tile * p.max_splits + split) * p.rows_per_tile;
+  const auto pr = partials_rsrc(p);
+  for (int idx = tid; idx < nrows * 32; idx += NT) {
+    const int g = idx >> 5;
+    const int d0 = (idx & 31) * 4;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm.m[w][g]);
+    const float base = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float a = fexp(sm.m[w][g] - base);
+      L += a * sm.l[w][g];
+      const float4 v = *reinterpret_cast<const float4*>(&sm.o[w][g][d0]);
+      O.x += a * v.x; O.y += a * v.y; O.z += a * v.z; O.w += a * v.w;
+    }
+    if (p.fused) {
+      st_coherent16(pr, (part + g) * 128 + d0, O);
+      if (d0 == 0) st_agent_ml(&p.ws_ml[(part + g) * 2], M, L);
+    } else {
+      *reinterpret_cast<float4*>(&p.ws_o[(part + g) * 128 + d0]) = O;
+      if (d0 == 0) *reinterpret_cast<float2*>(&p.ws_ml[(part + g) * 2]) = make_float2(M, L);
+    }
+  }
+  if (__builtin_expect(p.fused, 0)) {
+    // ticket: the last split of the tile to arrive merges (as fused_merge_tail)
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = atomicAdd(&p.tickets[tile], 1u);
+      sm.last = (prev == static_cast<uint32_t>(total - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!sm.last) return;
+    constexpr int QB = ElemBytes<TQ>::v;
+    const int items = nrows * 32;               // (row, float4 column chunk)
+    const int nsub = items >= NT ? 1 : NT / items;
+    const int sub = tid / items;
+    const int it = tid - sub * items;
+    const int64_t part0 = (int64_t)tile * p.max_splits * p.rows_per_tile;
+    for (int i = it; i < items && sub < nsub; i += NT) {
+      const int g = i >> 5;
+      const int d0 = (i & 31) * 4;
+      float M = -INFINITY, L = 0.f;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      constexpr int kB = 16;  // one trip for up to 16 * nsub splits
+      for (int s0 = sub; s0 < total; s0 += nsub * kB) {
+        float2 ml[kB];
+        float4 v[kB];
+#pragma unroll
+        for (int k = 0; k < kB; ++k) {
+          const int sp = s0 + k * nsub;
+          if (sp < total) {
+            const int64_t pi = part0 + (int64_t)sp * p.rows_per_tile + g;
+            ml[k] = ld_agent_ml(reinterpret_cast<const float2*>(p.ws_ml) + pi);
+            v[k] = ld_coherent16(pr, pi * 128 + d0);
+          } else {
+            ml[k] = make_float2(-INFINITY, 0.f);
+            v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+        }
+        float mb = M;
+#pragma unroll
+        for (int k = 0; k < kB; ++k) mb = fmaxf(mb, ml[k].x);
+        const float base = (mb == -INFINITY) ? 0.f : mb;
+        const float a0 = fexp(M - base);
+        L *= a0;
+        acc.x *= a0; acc.y *= a0; acc.z *= a0; acc.w *= a0;
+#pragma unroll
+        for (int k = 0; k < kB; ++k) {
+          const float wgt = fexp(ml[k].x - base);
+          L = fmaf(wgt, ml[k].y, L);
+          acc.x = fmaf(wgt, v[k].x, acc.x);
+          acc.y = fmaf(wgt, v[k].y, acc.y);
+          acc.z = fmaf(wgt, v[k].z, acc.z);
+          acc.w = fmaf(wgt, v[k].w, acc.w);
+        }
+        M = mb;
+      }
+      if (nsub == 1) {
+        // one thread per item: write the output row chunk directly
+        const float inv = 1.f / fmaxf(L, 1e-12f);
+        const int rr = r0 + g;
+        const int h = hk * p.G + rr / p.S, sq = rr % p.S;
+        char* orow =
+            reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * p.S + sq) * 128 * QB;
+        store_elem<TQ>(orow + (d0 + 0) * QB, acc.x * inv);
+        store_elem<TQ>(orow + (d0 + 1) * QB, acc.y * inv);
+        store_elem<TQ>(orow + (d0 + 2) * QB, acc.z * inv);
+        store_elem<TQ>(orow + (d0 + 3) * QB, acc.w * inv);
+      } else {
+        sm.red[tid] = acc;
+        sm.redml[tid] = make_float2(M, L);
+      }
+    }
+    __syncthreads();
+    for (int i = tid; i < items && nsub > 1; i += NT) {
+      float Mx = -INFINITY;
+      for (int j = 0; j < nsub; ++j) Mx = fmaxf(Mx, sm.redml[i + j * items].x);
+      const float base = (Mx == -INFINITY) ? 0.f : Mx;
+      float Lx = 0.f;
+      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int j = 0; j < nsub; ++j) {
+        const float2 ml = sm.redml[i + j * items];
+        const float4 t = sm.red[i + j * items];
+        const float wgt = fexp(ml.x - base);
+        Lx = fmaf(wgt, ml.y, Lx);
+        o.x = fmaf(wgt, t.x, o.x);
+        o.y = fmaf(wgt, t.y, o.y);
+        o.z = fmaf(wgt, t.z, o.z);
+        o.w = fmaf(wgt, t.w, o.w);
+      }
+      const float inv = 1.f / fmaxf(Lx, 1e-12f);
+      const int g = i >> 5;
+      const int d0 = (i & 31) * 4;
+      const int rr = r0 + g;
+      const int h = hk * p.G + rr / p.S, sq = rr % p.S;
+      char* orow = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * p.S + sq) * 128 * QB;
+      store_elem<TQ>(orow + (d0 + 0) * QB, o.x * inv);
+      store_elem<TQ>(orow + (d0 + 1) * QB, o.y * inv);
+      store_elem<TQ>(orow + (d0 + 2) * QB, o.z * inv);
+      store_elem<TQ>(orow + (d0 + 3) * QB, o.w * inv);
+    }
+    if (tid == 0) p.tickets[tile] = 0u;
+  }
+}
+
+
 // Combines the split partials of one (tile, row) and writes the output row:
 // out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, M = max_s m_s — the
 // final normalisation of HELM's loop, out / clamp(sum, 1e-12)
@@ -587,7 +744,6 @@ __device__ __forceinline__ void split_epilogue(Smem<NW, GM, DMAX>& sm, const Att
 // column chunk c and the splits sub, sub + nsub, ...; all of its loads of a
 // batch are in flight at once, and the nsub partial results of a column meet
 // in LDS.
-constexpr int kMergeBatch = 8;
 
 template <typename TQ>
 __global__ __launch_bounds__(kThreads) void merge_splits_kernel(AttnParams p) {
@@ -701,6 +857,105 @@ __global__ __launch_bounds__(kThreads) void merge_splits_kernel(AttnParams p) {
       for (int j = 0; j < cw; ++j)
         store_elem<TQ>(out_row + ((cbeg + tid) * cw + j) * QB, a[j] * inv);
     }
+  }
+}
+
+// merge_splits_kernel for D = 128 with one column group, the arithmetic fixed
+// at compile time: thread (sub, c) = (tid / 32, tid % 32) owns float4 column
+// chunk c and splits sub, sub + 8, ...; the 8 subs meet in LDS.  A short,
+// division-free kernel: it runs once per call with a cold instruction cache.
+template <typename TQ>
+__global__ __launch_bounds__(kThreads) void merge_splits_d128_kernel(AttnParams p) {
+  constexpr int QB = ElemBytes<TQ>::v;
+  constexpr int kSub = kThreads / 32;
+  __shared__ float4 red[kThreads];
+  __shared__ float2 redml[kThreads];
+  const int tile = blockIdx.x;
+  const int row = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int RS = p.rows_per_tile;
+  const int qt = tile % p.n_qtiles;
+  const int hk = (tile / p.n_qtiles) % p.Hkv;
+  const int b = tile / (p.n_qtiles * p.Hkv);
+  const int rr = qt * RS + row;
+  if (rr >= p.G * p.S) return;
+  const int total = p.counts[tile];
+  const int sub = tid >> 5;
+  const int c = tid & 31;
+  const int64_t base_part = (int64_t)tile * p.max_splits * RS + row;
+  float M = -INFINITY, L = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  // the first batch is loaded before the split count arrives (bounded by the
+  // workspace's split capacity) and masked afterwards
+  const int bound = p.max_splits;
+  for (int s0 = sub; s0 < bound; s0 += kSub * kMergeBatch) {
+    if (s0 > sub && s0 >= total) break;
+    float2 ml[kMergeBatch];
+    float4 v[kMergeBatch];
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const int sp = s0 + k * kSub;
+      if (sp < bound) {
+        const int64_t pi = base_part + (int64_t)sp * RS;
+        ml[k] = *reinterpret_cast<const float2*>(p.ws_ml + pi * 2);
+        v[k] = *reinterpret_cast<const float4*>(p.ws_o + pi * 128 + c * 4);
+      } else {
+        ml[k] = make_float2(-INFINITY, 0.f);
+        v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    float mb = M;
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      if (s0 + k * kSub >= total) {
+        ml[k] = make_float2(-INFINITY, 0.f);
+        v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      mb = fmaxf(mb, ml[k].x);
+    }
+    const float base = (mb == -INFINITY) ? 0.f : mb;
+    const float a0 = fexp(M - base);
+    L *= a0;
+    acc.x *= a0; acc.y *= a0; acc.z *= a0; acc.w *= a0;
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const float wgt = fexp(ml[k].x - base);
+      L = fmaf(wgt, ml[k].y, L);
+      acc.x = fmaf(wgt, v[k].x, acc.x);
+      acc.y = fmaf(wgt, v[k].y, acc.y);
+      acc.z = fmaf(wgt, v[k].z, acc.z);
+      acc.w = fmaf(wgt, v[k].w, acc.w);
+    }
+    M = mb;
+  }
+  red[tid] = acc;
+  redml[tid] = make_float2(M, L);
+  __syncthreads();
+  if (tid < 32) {
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) Mx = fmaxf(Mx, redml[tid + 32 * j].x);
+    const float base = (Mx == -INFINITY) ? 0.f : Mx;
+    float Lx = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < kSub; ++j) {
+      const float2 ml = redml[tid + 32 * j];
+      const float4 t = red[tid + 32 * j];
+      const float wgt = fexp(ml.x - base);
+      Lx = fmaf(wgt, ml.y, Lx);
+      o.x = fmaf(wgt, t.x, o.x);
+      o.y = fmaf(wgt, t.y, o.y);
+      o.z = fmaf(wgt, t.z, o.z);
+      o.w = fmaf(wgt, t.w, o.w);
+    }
+    const float inv = 1.f / fmaxf(Lx, 1e-12f);
+    const int h = hk * p.G + rr / p.S, sq = rr % p.S;
+    char* orow = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * p.S + sq) * 128 * QB;
+    store_elem<TQ>(orow + (tid * 4 + 0) * QB, o.x * inv);
+    store_elem<TQ>(orow + (tid * 4 + 1) * QB, o.y * inv);
+    store_elem<TQ>(orow + (tid * 4 + 2) * QB, o.z * inv);
+    store_elem<TQ>(orow + (tid * 4 + 3) * QB, o.w * inv);
   }
 }
 

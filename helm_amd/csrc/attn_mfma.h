@@ -386,7 +386,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
     *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4][r], o[5][r], o[6][r], o[7][r]);
   }
   __syncthreads();
-  split_epilogue<T, NW, kMfmaRows, 128>(sm, p, tid, tile, split, total, nrows, r0, b, hk);
+  split_epilogue_d128<T, NW, kMfmaRows>(sm, p, tid, tile, split, total, nrows, r0, b, hk);
 }
 
 }  // namespace helm

@@ -258,6 +258,20 @@ hipError_t launch_merge(const LaunchSpec& s, int B, int Hkv, hipStream_t st) {
   const int chunks = (s.p.D % 4 == 0) ? s.p.D / 4 : s.p.D;
   const int groups = std::max(1, std::min(env_int("HELM_AMD_MERGE_GROUPS", 1), chunks));
   const dim3 grid(B * Hkv * s.p.n_qtiles, s.p.rows_per_tile, groups);
+  if (s.p.D == 128 && groups == 1) {
+    switch (s.q_dtype) {
+      case HELM_F16:
+        hipLaunchKernelGGL(merge_splits_d128_kernel<f16_t>, grid, dim3(kThreads), 0, st, s.p);
+        return hipGetLastError();
+      case HELM_BF16:
+        hipLaunchKernelGGL(merge_splits_d128_kernel<bf16_t>, grid, dim3(kThreads), 0, st, s.p);
+        return hipGetLastError();
+      case HELM_F32:
+        hipLaunchKernelGGL(merge_splits_d128_kernel<float>, grid, dim3(kThreads), 0, st, s.p);
+        return hipGetLastError();
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (s.q_dtype) {
     case HELM_F16:
       hipLaunchKernelGGL(merge_splits_kernel<f16_t>, grid, dim3(kThreads), 0, st, s.p);
