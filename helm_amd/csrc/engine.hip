@@ -116,12 +116,26 @@ int kernel_choice() {
   return 0;
 }
 
+// The in-kernel merge's tickets live in a fixed region at the start of every
+// workspace that nothing else uses: zero since the workspace was zeroed and
+// left zero by every call, whatever shapes earlier calls had (a region sized
+// per call would grow into bytes an earlier call used for split counts or
+// partials).  A call with more tiles than it holds merges in the second kernel.
+constexpr size_t kTicketRegionBytes = 64 << 10;  // 16,384 tiles
+
 void size_plan(Plan& pl, int B, int Hkv, int D) {
   const size_t tiles = (size_t)B * Hkv * pl.n_qtiles;
-  pl.ticket_bytes = align_up(tiles * 4, 256);
+  pl.ticket_bytes = kTicketRegionBytes;
   pl.count_bytes = align_up(tiles * 4, 256);
   pl.ml_bytes = align_up(tiles * pl.max_splits * pl.rows * 2 * 4, 256);
   pl.o_bytes = align_up(tiles * pl.max_splits * pl.rows * (size_t)D * 4, 256);
+}
+
+// Fused merge only where its tickets fit the ticket region and its 31-bit
+// partial offsets reach every partial.
+void settle_fused(Plan& pl, int B, int Hkv) {
+  const size_t tiles = (size_t)B * Hkv * pl.n_qtiles;
+  if (pl.o_bytes >= 0x7ffffff0u || tiles * 4 > kTicketRegionBytes) pl.fused = 0;
 }
 
 // Rows, tiles and the split limits of a kernel choice.
@@ -183,8 +197,7 @@ int make_plan(Plan& pl, int kv_dtype, int q_dtype, int B, int Hq, int Hkv,
   pl.max_splits = std::max(1, (max_pages + pl.pps - 1) / pl.pps);
   pl.fused = fused_merge(pl.max_splits);
   size_plan(pl, B, Hkv, D);
-  // the in-kernel merge addresses the partials with 31-bit byte offsets
-  if (pl.o_bytes >= 0x7ffffff0u) pl.fused = 0;
+  settle_fused(pl, B, Hkv);
   return HELM_OK;
 }
 
@@ -951,7 +964,7 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
                          : std::max(1, (max_pages + pl.pps - 1) / pl.pps);
   pl.fused = fused_merge(pl.max_splits);
   size_plan(pl, B, Hkv, D);
-  if (pl.o_bytes >= 0x7ffffff0u) pl.fused = 0;
+  settle_fused(pl, B, Hkv);
   rc = engine_ensure_ws(eng, pl.total(), st);
   if (rc != HELM_OK) return rc;
 
@@ -1066,7 +1079,7 @@ int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
   pl.max_splits = std::max(1, (max_pages + pl.pps - 1) / pl.pps);
   pl.fused = fused_merge(pl.max_splits);
   size_plan(pl, B, Hkv, D);
-  if (pl.o_bytes >= 0x7ffffff0u) pl.fused = 0;
+  settle_fused(pl, B, Hkv);
   rc = engine_ensure_ws(eng, pl.total(), st);
   if (rc != HELM_OK) return rc;
 

@@ -104,9 +104,10 @@ void* helm_engine_copy_stream(helm_engine* eng);
 /* ---- attention ------------------------------------------------------------ */
 
 /* Workspace (bytes) helm_paged_decode_attn needs for this shape: per-tile
- * merge tickets and split counts, and the split partials (m, l, o[D]) of
- * every query row.  It must be zero before its first use; every completed
- * call leaves the ticket region zero again. */
+ * merge tickets (a fixed region at its start, 64 KiB, used for nothing
+ * else), split counts, and the split partials (m, l, o[D]) of every query
+ * row.  It must be zero before its first use; every completed call leaves the
+ * ticket region zero again, so one workspace serves calls of any shapes. */
 size_t helm_query_workspace_bytes(int B, int Hq, int Hkv, int q_len, int D,
                                   int max_pages, int page_size,
                                   int pages_per_split);

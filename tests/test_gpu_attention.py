@@ -89,6 +89,22 @@ def test_pool_decode_ragged_batch_full_size(kernel):
     _check_pool(w, case, out)
 
 
+def test_workspace_reused_across_shapes(kernel):
+    """One workspace for a long single-sequence call (its split counts and
+    partials fill the workspace) and then a batch of short sequences with 20x
+    the tiles, merged in-kernel: the tickets sit in their own region, so the
+    second call does not see the first call's bytes as tickets."""
+    long_w = W.WORKLOADS["qwen3-8b-32k"]
+    short_w = W.Workload("short-b20", 20, 32, 8, 128, torch.bfloat16, T_range=(100, 400))
+    for w, seed in ((long_w, 1), (short_w, 5), (long_w, 2), (short_w, 6)):
+        case = W.make_pool_case(w, seed=seed, device=DEV)
+        out = paged_decode_attention(case["q"], case["k_pool"], case["v_pool"], case["table"],
+                                     case["lens"], max_pages=case["max_pages"],
+                                     total_pages=sum(case["n_pages"]))
+        torch.cuda.synchronize()
+        _check_pool(w, case, out)
+
+
 @pytest.mark.parametrize("pps", [1, 3, 8, 64, 256])
 def test_pool_decode_split_invariance(pps, kernel):
     """Any split count gives the same attention (merge correctness)."""

@@ -495,6 +495,47 @@ def test_decode_from_layer_records_matches_page_list_path(masked, evict, kernel,
         assert (x.float() - y.float()).abs().max().item() <= 1e-2
 
 
+@pytest.mark.parametrize("B,T,steps", [(4, 16384, 18), (17, 600, 3)])
+def test_decode_batched_many_pages_and_many_sequences(B, T, steps):
+    """_decode_batched at scale: 4 sequences x 16k tokens (1,024 pages each,
+    the device-resident records grown past their first capacity while steps
+    cross a page boundary) and 17 sequences (more than one call carries by
+    value, so the concatenated-records path runs); the last step equals the
+    fp64 oracle."""
+    Hq, kvh, D, P, L = 32, 8, 128, 16, 2
+    a = KVAllocator(L, kvh, D, page_size=P, dtype=torch.bfloat16)
+    kvcms = [KVCacheManager(a, gpu_high_watermark_bytes=10 ** 13) for _ in range(B)]
+    g = torch.Generator(device=DEV).manual_seed(21)
+    kv = {}
+    for lid in range(L):
+        for i, m in enumerate(kvcms):
+            n = T + 7 * i
+            k = torch.randn(1, kvh, n, D, generator=g, device=DEV).bfloat16()
+            v = torch.randn(1, kvh, n, D, generator=g, device=DEV).bfloat16()
+            m.append_prefill(lid, k, v)
+            kv[lid, i] = [k, v]
+    out = None
+    for s in range(steps):
+        for lid in range(L):
+            q = torch.randn(B, Hq, 1, D, generator=g, device=DEV).bfloat16()
+            kn = torch.randn(B, kvh, 1, D, generator=g, device=DEV).bfloat16()
+            vn = torch.randn(B, kvh, 1, D, generator=g, device=DEV).bfloat16()
+            out = _decode_batched(kvcms, q, kn, vn, lid, 1 / math.sqrt(D))
+            for i in range(B):
+                kv[lid, i][0] = torch.cat([kv[lid, i][0], kn[i:i + 1]], 2)
+                kv[lid, i][1] = torch.cat([kv[lid, i][1], vn[i:i + 1]], 2)
+    torch.cuda.synchronize()
+    for i in sorted({0, B - 1}):
+        K, V = kv[L - 1, i]
+        ref = A.attention_fp64_batched(q[i].float().cpu(), K[0].float().cpu(),
+                                       V[0].float().cpu())
+        assert (out[i].double().cpu() - ref).abs().max().item() <= 1e-2
+        k_pages, v_pages = _gather(kvcms[i], L - 1)
+        assert torch.equal(k_pages, K.cpu()) and torch.equal(v_pages, V.cpu())
+    for m in kvcms:
+        m.clear()
+
+
 def test_tiny_llama_greedy_matches_hf_with_eviction():
     """test_kv_eviction_e2e.py:10-66 pattern: a tiny random Llama generates the
     same greedy tokens through the paged, evicting cache as HF's own
