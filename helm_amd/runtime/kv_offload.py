@@ -230,13 +230,68 @@ def _append_prefill_batched(kvcms, k, v, layer_idx: int) -> list:
 def _stream_prefill_batched(kvcms, q, layer_idx: int, scale: float,
                             attention_mask: Optional[torch.Tensor] = None,
                             softcap: Optional[float] = None):
-    """A later prefill chunk attends over every cached page, per item."""
+    """A later prefill chunk attends over every cached page, per item
+    (perform_streaming_attention per item, kv_offload.py:207-227), issued from
+    the layers' page records when they serve."""
+    out = _prefill_from_records(kvcms, q, layer_idx, scale, attention_mask, softcap)
+    if out is not None:
+        return out
     outs = []
     for i in range(q.shape[0]):
         item_mask = attention_mask[i:i + 1] if attention_mask is not None else None
         outs.append(perform_streaming_attention(q[i:i + 1], kvcms[i].iterate_layer_pages(layer_idx),
                                                 scale=scale, attention_mask=item_mask,
                                                 softcap=softcap))
+    return torch.cat(outs, dim=0)
+
+
+def _prefill_from_records(kvcms, q, layer_idx: int, scale: float,
+                          attention_mask: Optional[torch.Tensor], softcap: Optional[float]):
+    """What per-item perform_streaming_attention gives for a prefill chunk
+    (every active page in token order; top-left causal when unmasked and all
+    pages are on the device, kv_cache.py:562-568), from the layers' records;
+    None when they cannot serve (the page-list path then runs)."""
+    if q.device.type != "cuda" or not _async_kv_prefetch_enabled():
+        return None
+    B, _, S, D = q.shape
+    layers = [kvcm.layers.get(layer_idx) for kvcm in kvcms[:B]]
+    if len(layers) != B:
+        return None
+    recs = []
+    for layer in layers:
+        r = layer.records() if layer is not None else None
+        if r is None or len(r) == 0 or layer._n_other or layer._rec_sig is None:
+            return None
+        recs.append(r)
+    kv_dtype, Hkv = layers[0]._rec_sig[0], layers[0]._rec_sig[1]
+    if any(layer._rec_sig != (kv_dtype, Hkv, D) for layer in layers):
+        return None
+    masked = attention_mask is not None or softcap is not None
+    host = [layer._n_host > 0 for layer in layers]
+    if not masked and any(host) and not all(host):
+        return None         # causal differs between items: the page-list path
+    causal = (not masked) and S > 1 and not any(host)
+    for layer in layers:
+        _record_prefetch(layer._n_host, layer._host_bytes)
+    lens = [int(r["tok_off"][-1]) + int(r["used"][-1]) for r in recs]
+    if B <= _MAX_SEQ_ARGS and not any(host):
+        return _attend_layers(q, layers, lens, Hkv, kv_dtype, scale, attention_mask, softcap,
+                              causal)
+    arr = recs[0] if B == 1 else np.concatenate(
+        [r.view(np.uint64) for r in recs]).view(recs[0].dtype)
+    seq_off = np.zeros(B + 1, dtype=np.int32)
+    np.cumsum([len(r) for r in recs], out=seq_off[1:])
+    try:
+        return _attend_records(q, arr, seq_off, max(lens), Hkv, kv_dtype, scale, attention_mask,
+                               softcap, causal)
+    except NotImplementedError:
+        pass        # host pages that must be staged: one call per item
+    outs = []
+    for i, r in enumerate(recs):
+        m = attention_mask[i:i + 1] if attention_mask is not None and \
+            attention_mask.size(0) > 1 else attention_mask
+        outs.append(_attend_records(q[i:i + 1], r, np.array([0, len(r)], dtype=np.int32),
+                                    lens[i], Hkv, kv_dtype, scale, m, softcap, causal))
     return torch.cat(outs, dim=0)
 
 

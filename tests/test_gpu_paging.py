@@ -13,7 +13,8 @@ from helm_amd import workloads as W
 from helm_amd.runtime import kv_cache as KC
 from helm_amd.runtime.kv_allocator import KVAllocator
 from helm_amd.runtime.kv_cache import KVCacheManager, perform_streaming_attention
-from helm_amd.runtime.kv_offload import KVOffloadConfig, KVOffloadManager, _decode_batched
+from helm_amd.runtime.kv_offload import (KVOffloadConfig, KVOffloadManager, _decode_batched,
+                                         _stream_prefill_batched)
 from oracle import attention as A
 from oracle.paging import AllocatorModel, CacheModel
 
@@ -534,6 +535,60 @@ def test_decode_batched_many_pages_and_many_sequences(B, T, steps):
         assert torch.equal(k_pages, K.cpu()) and torch.equal(v_pages, V.cpu())
     for m in kvcms:
         m.clear()
+
+
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("evict", [False, True])
+def test_stream_prefill_from_records_matches_page_list_path(masked, evict, monkeypatch):
+    """A later prefill chunk (q_len 24) over every cached page, per item as
+    HELM does (kv_offload.py:207-227): the layer-record path equals the
+    page-list path (HELM_DISABLE_ASYNC_KV) and the fp64 oracle, with the same
+    prefetch counters; unmasked all-device items get HELM's top-left causal."""
+    Hq, kvh, D, P, S = 16, 4, 128, 16, 24
+    lens = [200, 77, 130]
+    B = len(lens)
+    page_bytes = 2 * kvh * P * D * 2
+    g = torch.Generator().manual_seed(17)
+    kvs = [(torch.randn(1, kvh, n, D, generator=g).bfloat16(),
+            torch.randn(1, kvh, n, D, generator=g).bfloat16()) for n in lens]
+    q = torch.randn(B, Hq, S, D, generator=g).bfloat16()
+    T = max(lens)
+    mask = None
+    if masked:
+        mask = torch.zeros(B, 1, S, T)
+        mask[..., 3::5] = float("-inf")
+    results = {}
+    for mode in ("records", "pages"):
+        if mode == "pages":
+            monkeypatch.setenv("HELM_DISABLE_ASYNC_KV", "1")
+        a = KVAllocator(1, kvh, D, page_size=P, dtype=torch.bfloat16)
+        kvcms = [KVCacheManager(a, gpu_high_watermark_bytes=2 * page_bytes if evict else 10 ** 12)
+                 for _ in lens]
+        for m, (k, v) in zip(kvcms, kvs):
+            m.append_prefill(0, k.to(DEV), v.to(DEV))
+        KC.reset_paging_stats()
+        out = _stream_prefill_batched(kvcms, q.to(DEV), 0, 1 / math.sqrt(D),
+                                      attention_mask=mask.to(DEV) if masked else None)
+        torch.cuda.synchronize()
+        results[mode] = (out.cpu(), KC.get_paging_stats())
+        assert any(m.layers[0]._n_host for m in kvcms) == evict
+        for m in kvcms:
+            m.clear()
+        monkeypatch.delenv("HELM_DISABLE_ASYNC_KV", raising=False)
+    (o_rec, s_rec), (o_pg, s_pg) = results["records"], results["pages"]
+    assert s_rec == s_pg
+    assert (o_rec.float() - o_pg.float()).abs().max().item() <= 1e-2
+    for i, n in enumerate(lens):
+        mk = None
+        if masked:
+            mk = mask[i, :, :, :n].double()
+        elif not evict:
+            # top-left causal of HELM's Path 1: key t visible to row s iff t <= s
+            mk = torch.zeros(1, S, n, dtype=torch.float64)
+            mk[0][torch.arange(n)[None, :] > torch.arange(S)[:, None]] = float("-inf")
+        ref = A.attention_fp64_batched(q[i].float(), kvs[i][0][0].float(), kvs[i][1][0].float(),
+                                       mask=mk)
+        assert (o_rec[i].double() - ref).abs().max().item() <= 1e-2
 
 
 def test_tiny_llama_greedy_matches_hf_with_eviction():
