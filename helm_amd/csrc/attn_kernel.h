@@ -399,6 +399,7 @@ struct AttnParams {
   int* counts;        // [tiles] splits of each tile (merge-kernel mode)
   uint32_t* tickets;  // [tiles] arrivals (fused mode; zero between calls)
   int fused;          // 1: the last split of a tile merges in-kernel
+  int row_waves;      // 1 (matrix-core kernel): each wave owns a 16-row tile
 };
 
 // Per-workgroup LDS: per-wave online-softmax states of the tile's rows, and

@@ -79,6 +79,9 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // matrix cores; generic: the element-wise kernel only).
 struct Plan {
   int mfma, fast, nw, fused, gm, rows, epl, n_qtiles, bpp, pps, max_splits;
+  int row_waves;  // matrix-core kernel: one 16-row tile per wave (query chunks)
+  // workgroups per (sequence, KV head) along the query rows
+  int qblocks() const { return row_waves ? (n_qtiles + nw - 1) / nw : n_qtiles; }
   size_t ticket_bytes, count_bytes, ml_bytes, o_bytes;
   size_t total() const { return ticket_bytes + count_bytes + ml_bytes + o_bytes; }
 };
@@ -135,7 +138,8 @@ void size_plan(Plan& pl, int B, int Hkv, int D) {
 // partial offsets reach every partial.
 void settle_fused(Plan& pl, int B, int Hkv) {
   const size_t tiles = (size_t)B * Hkv * pl.n_qtiles;
-  if (pl.o_bytes >= 0x7ffffff0u || tiles * 4 > kTicketRegionBytes) pl.fused = 0;
+  if (pl.o_bytes >= 0x7ffffff0u || tiles * 4 > kTicketRegionBytes || pl.row_waves)
+    pl.fused = 0;
 }
 
 // Rows, tiles and the split limits of a kernel choice.
@@ -152,6 +156,10 @@ void plan_shape(Plan& pl, int G, int q_len, int D, int max_tok_per_page) {
   }
   pl.n_qtiles = (G * q_len + pl.gm - 1) / pl.gm;
   pl.bpp = std::max(1, (max_tok_per_page + kBlockTok - 1) / kBlockTok);
+  // query chunks of several 16-row tiles: the waves of a workgroup take one
+  // tile each over the same pages (K/V read once per workgroup from L2, not
+  // once per tile); HELM_AMD_ROW_WAVES=0 keeps one tile per workgroup
+  pl.row_waves = (pl.mfma && pl.n_qtiles >= 2 && env_int("HELM_AMD_ROW_WAVES", 1)) ? 1 : 0;
 }
 
 int max_pps_of(const Plan& pl) { return pl.mfma ? kMfmaMaxPps : kMaxPps; }
@@ -181,7 +189,7 @@ int make_plan(Plan& pl, int kv_dtype, int q_dtype, int B, int Hq, int Hkv,
   plan_shape(pl, G, q_len, D, max_tok_per_page);
   int pps = pps_req > 0 ? pps_req : env_int("HELM_AMD_PPS", 0);
   if (pps <= 0) {
-    const double units = (double)B * Hkv * pl.n_qtiles;
+    const double units = (double)B * Hkv * pl.qblocks();
     // one workgroup per CU: longer splits mean fewer partials to merge
     const int target = env_int("HELM_AMD_WG_PER_CU", 1) * device_cus();
     const double splits = std::max(1.0, target / units);
@@ -240,6 +248,7 @@ void fill_params(AttnParams& a, const Plan& pl, const void* q, void* out,
   a.D = D;
   a.rows_per_tile = pl.rows;
   a.n_qtiles = pl.n_qtiles;
+  a.row_waves = pl.row_waves;
   a.scale = scale;
   a.softcap = softcap;
   a.mask = mask;
@@ -788,7 +797,7 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
   s.mfma = pl.mfma;
   s.nw = pl.nw;
   s.feat = (mask ? kFeatMask : 0) | (softcap > 0.f ? kFeatCap : 0);
-  s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.n_qtiles, B);
+  s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.qblocks(), B);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e = dispatch(s, st);
   if (e != hipSuccess) return hip_fail(e, "paged_attn launch");
@@ -1009,7 +1018,7 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
            (causal ? kFeatCausal : 0);
 
   if (!n_host) {
-    s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.n_qtiles, B);
+    s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.qblocks(), B);
     hipError_t e = dispatch(s, st);
     if (e != hipSuccess) return hip_fail(e, "stream_attn launch");
     e = launch_merge(s, B, Hkv, st);
@@ -1032,7 +1041,7 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
     s.p.hi = L.hi;
     s.p.split_base = split_base[li];
     const int nsp = (L.hi - L.lo + pl.pps - 1) / pl.pps;
-    s.grid = dim3(std::max(1, nsp), Hkv * pl.n_qtiles, 1);
+    s.grid = dim3(std::max(1, nsp), Hkv * pl.qblocks(), 1);
     if (L.chunk >= 0) {
       const int slot = chunk_slot[L.chunk];
       char* dst = eng->ring + (size_t)slot * eng->chunk_bytes;
@@ -1112,7 +1121,7 @@ int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
   s.nw = pl.nw;
   s.feat = (mask ? kFeatMask : 0) | (softcap > 0.f ? kFeatCap : 0) |
            (causal ? kFeatCausal : 0);
-  s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.n_qtiles, B);
+  s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.qblocks(), B);
   hipError_t e = dispatch(s, st);
   if (e != hipSuccess) return hip_fail(e, "paged_attn_seqs launch");
   e = launch_merge(s, B, Hkv, st);
