@@ -181,11 +181,14 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / 1e3 / steps
 
-    # host pages staged through the device ring by hipMemcpyAsync, then the
-    # default: read in place by the kernel over the host link
+    # host pages staged through the device ring by hipMemcpyAsync, read in
+    # place by the kernel over the host link, and the engine's default (it
+    # picks per call: pages in long address runs are staged)
     prev = os.environ.pop("HELM_AMD_HOST_READ", None)
     os.environ["HELM_AMD_HOST_READ"] = "copy"
     per_staged = timed()
+    os.environ["HELM_AMD_HOST_READ"] = "direct"
+    per_direct = timed()
     del os.environ["HELM_AMD_HOST_READ"]
     per = timed()
     if prev is not None:
@@ -204,9 +207,12 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
         "frac_of_measured_h2d": host_bytes / per / 1e9 / peak,
         "pcie5_x16_theoretical_GBs": PCIE5_X16_GBS, "max_abs_err_vs_fp64": err,
         "resident_bytes": (n - n_host) * slot_b,
-        "host_read": "in place (kernel reads pinned host pages over the link)",
+        "host_read": "engine default (staged when the host pages form long address runs, "
+                     "else read in place)",
         "staged_ms_per_call": per_staged * 1e3,
         "staged_host_link_GBs": host_bytes / per_staged / 1e9,
+        "in_place_ms_per_call": per_direct * 1e3,
+        "in_place_host_link_GBs": host_bytes / per_direct / 1e9,
     }
 
 
