@@ -103,6 +103,7 @@ def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=Non
     e0.record(stream)
     for i in range(steps):
         step(i)
+    t_issued = time.perf_counter()
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -111,6 +112,7 @@ def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=Non
     return {
         "w": w, "case": case, "alg_bytes": alg, "kv_bytes": W.kv_bytes(w, lens),
         "per_call_s": per_call_s, "wall_ms_per_step": wall * 1e3 / steps,
+        "host_issue_us_per_call": (t_issued - t0) * 1e6 / steps,
         "ms_per_step": ms_events / steps, "pools": n_pools, "lens": lens, "prep": prep,
     }
 
@@ -450,7 +452,8 @@ def main():
                      "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
                      "alg_bytes_per_launch": h["alg_bytes"],
-                     "avg_launch_us": round(h["per_call_s"] * 1e6, 3)},
+                     "avg_launch_us": round(h["per_call_s"] * 1e6, 3),
+                     "host_issue_us_per_call": round(h["host_issue_us_per_call"], 2)},
         "offload50": off,
         "full_step_40l": full,
         "cpu_baseline": None if cpu is None else {
