@@ -591,6 +591,65 @@ def test_stream_prefill_from_records_matches_page_list_path(masked, evict, monke
         assert (o_rec[i].double() - ref).abs().max().item() <= 1e-2
 
 
+def _tiny_model(arch: str):
+    """A tiny random model of `arch` (fp32, eager attention) and its twin."""
+    import transformers.models as tm
+    common = dict(vocab_size=97, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                  num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=256)
+    if arch == "qwen2":
+        cfg, cls = tm.qwen2.Qwen2Config(**common), tm.qwen2.Qwen2ForCausalLM
+    elif arch == "qwen3":
+        cfg, cls = tm.qwen3.Qwen3Config(head_dim=16, **common), tm.qwen3.Qwen3ForCausalLM
+    elif arch == "mistral":
+        cfg, cls = tm.mistral.MistralConfig(**common), tm.mistral.MistralForCausalLM
+    elif arch == "olmo2":
+        cfg, cls = tm.olmo2.Olmo2Config(**common), tm.olmo2.Olmo2ForCausalLM
+    elif arch == "gemma2":
+        cfg = tm.gemma2.Gemma2Config(head_dim=16, sliding_window=8, query_pre_attn_scalar=16,
+                                      attn_logit_softcapping=50.0, final_logit_softcapping=30.0,
+                                      **common)
+        cls = tm.gemma2.Gemma2ForCausalLM
+    else:
+        cfg, cls = tm.llama.LlamaConfig(**common), tm.llama.LlamaForCausalLM
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(0)
+    ref = cls(cfg).eval().to(DEV)
+    model = cls(cfg).eval().to(DEV)
+    model.load_state_dict(ref.state_dict())
+    return ref, model
+
+
+@pytest.mark.parametrize("arch", ["llama", "qwen2", "qwen3", "mistral", "olmo2", "gemma2"])
+def test_tiny_models_decode_logits_match_hf_with_eviction(arch):
+    """Every architecture the paged forwards cover (kv_offload.py:291-651): a
+    tiny random model decodes through the paged, evicting cache with the same
+    logits as HF's own full-recompute forward over the same tokens (teacher
+    forced, so near-tied argmaxes cannot diverge the two runs)."""
+    ref_model, model = _tiny_model(arch)
+    conf = KVOffloadConfig.from_model(model, page_size=16, gpu_watermark_bytes=1024)
+    mgr = KVOffloadManager(model, conf, batch_size=1)
+    g = torch.Generator().manual_seed(2)
+    S, steps = 12, 30
+    ids = torch.randint(0, 97, (1, S + steps), generator=g).to(DEV)
+    KC.reset_paging_stats()
+    worst = 0.0
+    with torch.no_grad():
+        logits = model(ids[:, :S], position_ids=torch.arange(S, device=DEV)[None],
+                       use_cache=False).logits
+        ref = ref_model(ids[:, :S], use_cache=False).logits
+        worst = max(worst, (logits - ref).abs().max().item())
+        for t in range(steps):
+            pos = S + t
+            logits = model(ids[:, pos:pos + 1], position_ids=torch.tensor([[pos]], device=DEV),
+                           attention_mask=None, use_cache=False,
+                           cache_position=torch.tensor([pos], device=DEV)).logits
+            ref = ref_model(ids[:, :pos + 1], use_cache=False).logits[:, -1:]
+            worst = max(worst, (logits - ref).abs().max().item())
+    mgr.restore()
+    assert worst <= 2e-4, f"{arch}: max logit difference {worst}"
+    assert KC.get_paging_stats()["pages_evicted"] > 0
+
+
 def test_tiny_llama_greedy_matches_hf_with_eviction():
     """test_kv_eviction_e2e.py:10-66 pattern: a tiny random Llama generates the
     same greedy tokens through the paged, evicting cache as HF's own
