@@ -157,7 +157,8 @@ _MAX_SEQ_ARGS = 16     # sequences one helm_paged_attn_seqs call carries
 
 
 def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: float,
-                         attention_mask: Optional[torch.Tensor]):
+                         attention_mask: Optional[torch.Tensor],
+                         softcap: Optional[float] = None):
     """The decode attention of `_decode_batched` from the layers' page records.
 
     Same outcome as the page-list path below (one batched call when every
@@ -196,18 +197,18 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
                               False)
     if bsz == 1 or not any(layer._n_host for layer in layers):
         return _attend_records(q, arr, seq_off, max(lens), Hkv, kv_dtype, scale,
-                               attention_mask, None, False)
+                               attention_mask, softcap, False)
     try:
         # host pages in mapped pinned memory are read in place: one call
         return _attend_records(q, arr, seq_off, max(lens), Hkv, kv_dtype, scale,
-                               attention_mask, None, False)
+                               attention_mask, softcap, False)
     except NotImplementedError:
         pass        # some host pages must be staged: one call per item
     outs = []
     for i, r in enumerate(recs):
         m = attention_mask[i:i + 1] if attention_mask is not None else None
         outs.append(_attend_records(q[i:i + 1], r, np.array([0, len(r)], dtype=np.int32),
-                                    lens[i], Hkv, kv_dtype, scale, m, None, False))
+                                    lens[i], Hkv, kv_dtype, scale, m, softcap, False))
     return torch.cat(outs, dim=0)
 
 
@@ -375,6 +376,32 @@ _ARCHS = {
 _RESOLVE_ORDER = ("qwen3", "qwen2", "gemma2", "ministral", "olmo2", "mistral", "llama")
 
 
+def _gemma2_decode_from_records(attn_self, kvcms, q, layer: int, scale: float, softcap,
+                                attention_mask, cache_position):
+    """Gemma-2 decode attention with each item's sliding-window mask
+    (kv_offload.py:577-613) as one call over the layers' records; None when
+    the records cannot serve."""
+    bsz = q.shape[0]
+    layers = [c.layers.get(layer) for c in kvcms[:bsz]]
+    if any(L is None or L.records() is None or len(L.pages) == 0 for L in layers):
+        return None
+    lens = [int(L._rec["tok_off"][len(L.pages) - 1]) + int(L._rec["used"][len(L.pages) - 1])
+            for L in layers]
+    t_max = max(lens)
+    mask = torch.zeros(bsz, 1, 1, t_max, device=q.device, dtype=torch.float32)
+    for i in range(bsz):
+        item = _gemma2_sliding_window_mask(
+            attn_self, attention_mask[i:i + 1] if attention_mask is not None else None,
+            cache_position, lens[i], device=q.device, dtype=q.dtype)
+        if item is None:
+            continue            # no window, no caller mask: nothing masked
+        if item.dim() != 4 or item.size(1) != 1 or item.size(-1) < lens[i]:
+            return None         # per-head masks: the per-item page-list path
+        mask[i, :, :, :lens[i]] = item[0, :, -1:, :lens[i]]
+    return _decode_from_records(kvcms[:bsz], q, layer, layers[0]._rec_sig[1], q.shape[-1],
+                                scale, mask, softcap)
+
+
 def _make_forward(kvcms, arch: _Arch):
     """Attention forward for `arch` bound to the per-item caches `kvcms`."""
 
@@ -420,20 +447,26 @@ def _make_forward(kvcms, arch: _Arch):
                                                        k.shape[-2], device=q.device, dtype=q.dtype)
                 out = _local_attention(q, k, v, scale, mask, softcap)
         elif arch.gemma:
-            outs = []
             for i in range(bsz):
-                kvcms[i].append_decode(layer, k[i:i + 1], v[i:i + 1])
-                pages = kvcms[i].iterate_layer_pages(layer)
-                key_length = sum(p.used_tokens for p in pages
-                                 if p.used_tokens > 0 and p.state != "DEAD")
-                item_mask = (_gemma2_sliding_window_mask(
-                    attn_self, attention_mask[i:i + 1] if attention_mask is not None else None,
-                    cache_position, key_length, device=q.device, dtype=q.dtype)
-                    if key_length > 0 else None)
-                outs.append(perform_streaming_attention(q[i:i + 1], pages, scale=scale,
-                                                        attention_mask=item_mask,
-                                                        softcap=softcap))
-            out = torch.cat(outs, dim=0)
+                kvcms[i]._append_decode_deferred(layer, k[i:i + 1], v[i:i + 1])
+                kvcms[i]._enforce_residency_policy()
+            _flush_appends([c._appends for c in kvcms])
+            out = _gemma2_decode_from_records(attn_self, kvcms, q, layer, scale, softcap,
+                                              attention_mask, cache_position)
+            if out is None:
+                outs = []
+                for i in range(bsz):
+                    pages = kvcms[i].iterate_layer_pages(layer)
+                    key_length = sum(p.used_tokens for p in pages
+                                     if p.used_tokens > 0 and p.state != "DEAD")
+                    item_mask = (_gemma2_sliding_window_mask(
+                        attn_self, attention_mask[i:i + 1] if attention_mask is not None else None,
+                        cache_position, key_length, device=q.device, dtype=q.dtype)
+                        if key_length > 0 else None)
+                    outs.append(perform_streaming_attention(q[i:i + 1], pages, scale=scale,
+                                                            attention_mask=item_mask,
+                                                            softcap=softcap))
+                out = torch.cat(outs, dim=0)
         else:
             out = _decode_batched(kvcms, q, k, v, layer, scale, attention_mask)
 

@@ -622,9 +622,10 @@ def _tiny_model(arch: str):
 @pytest.mark.parametrize("arch", ["llama", "qwen2", "qwen3", "mistral", "olmo2", "gemma2"])
 def test_tiny_models_decode_logits_match_hf_with_eviction(arch):
     """Every architecture the paged forwards cover (kv_offload.py:291-651): a
-    tiny random model decodes through the paged, evicting cache with the same
-    logits as HF's own full-recompute forward over the same tokens (teacher
-    forced, so near-tied argmaxes cannot diverge the two runs)."""
+    tiny random model prefills in two chunks and decodes through the paged,
+    evicting cache with the same logits as HF's own full-recompute forward
+    over the same tokens (teacher forced, so near-tied argmaxes cannot
+    diverge the two runs)."""
     ref_model, model = _tiny_model(arch)
     conf = KVOffloadConfig.from_model(model, page_size=16, gpu_watermark_bytes=1024)
     mgr = KVOffloadManager(model, conf, batch_size=1)
@@ -634,10 +635,22 @@ def test_tiny_models_decode_logits_match_hf_with_eviction(arch):
     KC.reset_paging_stats()
     worst = 0.0
     with torch.no_grad():
-        logits = model(ids[:, :S], position_ids=torch.arange(S, device=DEV)[None],
+        # the prompt in two chunks: the first attends over its own K/V, the
+        # second over the cached pages with a chunk-causal additive mask
+        # (HELM's pipeline chunk masks, pipeline_runtime.py:94-113)
+        c1 = 8
+        logits = model(ids[:, :c1], position_ids=torch.arange(c1, device=DEV)[None],
                        use_cache=False).logits
         ref = ref_model(ids[:, :S], use_cache=False).logits
-        worst = max(worst, (logits - ref).abs().max().item())
+        worst = max(worst, (logits - ref[:, :c1]).abs().max().item())
+        n2 = S - c1
+        chunk_mask = torch.zeros(1, 1, n2, S, device=DEV)
+        chunk_mask[0, 0][torch.arange(S, device=DEV)[None, :] >
+                         (c1 + torch.arange(n2, device=DEV))[:, None]] = torch.finfo(torch.float32).min
+        logits = model(ids[:, c1:S], position_ids=torch.arange(c1, S, device=DEV)[None],
+                       attention_mask=chunk_mask, use_cache=False,
+                       cache_position=torch.arange(c1, S, device=DEV)).logits
+        worst = max(worst, (logits - ref[:, c1:S]).abs().max().item())
         for t in range(steps):
             pos = S + t
             logits = model(ids[:, pos:pos + 1], position_ids=torch.tensor([[pos]], device=DEV),
