@@ -213,6 +213,11 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
 
 
 def _cached_tokens(kvcm, layer_idx: int) -> int:
+    """Tokens in the layer's active pages (from its records when they serve)."""
+    layer = kvcm.layers.get(layer_idx)
+    if layer is not None and layer.records() is not None and not layer._n_other:
+        n = len(layer.pages)
+        return int(layer._rec["tok_off"][n - 1]) + int(layer._rec["used"][n - 1]) if n else 0
     return sum(page.used_tokens for page in kvcm.iterate_layer_pages(layer_idx)
                if page.used_tokens > 0 and getattr(page, "state", None) != "DEAD")
 
