@@ -163,6 +163,76 @@ __device__ __forceinline__ PageView lane_page_view(const DescSrc& s, const DescL
   return pv;
 }
 
+// One 16-token block of the online-softmax recurrence on the matrix cores:
+// k / v are the block's K and V operands (K token tau(n) at dim chunks
+// q4 + 4i; V tokens q4 + 4j at dims 8n..8n+7), mk the additive mask of the
+// lane's row for tokens 4r + q4, ntok the block's valid tokens, tok0 the
+// HELM token cursor of its first token.  Updates the row max m, this lane's
+// share of the row sum, and O (rows 4 q4 + r, dims 8n + e).
+template <class Ops, bool kMask, bool kCap, bool kCausal>
+__device__ __forceinline__ void mfma_block_step(const mf_u32x4 (&k)[4], const mf_u32x4 (&v)[4],
+                                                const float (&mk)[4], int ntok, int tok0,
+                                                const mf_u32x4 (&qop)[4], float& m, float& lsum,
+                                                mf_f32x4 (&o)[8], float scale, float cap,
+                                                float inv_cap, int s_row, int q4) {
+  // scores of row n for tokens 4r + q4
+  mf_f32x4 sc = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sc = Ops::mma(k[i], qop[i], sc);
+  float x[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float val = sc[r] * scale;
+    if constexpr (kCap) val = tanhf(val * inv_cap) * cap;
+    if constexpr (kMask) val += mk[r];
+    if constexpr (kCausal)
+      if (tok0 + 4 * r + q4 > s_row) val = -INFINITY;
+    x[r] = val;
+  }
+  if (ntok < kBlockTok) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (4 * r + q4 >= ntok) x[r] = -INFINITY;
+  }
+  const float bm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  if (__builtin_amdgcn_ballot_w64(bm > m + kMfmaSlack)) {
+    // refresh the row max (uniform across the row's four lanes)
+    float rm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    rm = fmaxf(rm, __shfl_xor(rm, 32, 64));
+    const float mn = fmaxf(m, rm);
+    const float a = fexp(m - ((mn == -INFINITY) ? 0.f : mn));
+    lsum *= a;
+    m = mn;
+    // O rows of this lane are 4*q4 + r: fetch their factors
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float ar = __shfl(a, 4 * q4 + r, 64);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e][r] *= ar;
+    }
+  }
+  const float base = (m == -INFINITY) ? 0.f : m;
+  uint32_t h16[4], l16[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float w = fexp(x[r] - base);
+    lsum += w;
+    h16[r] = Ops::to16(w);
+    l16[r] = Ops::to16(w - Ops::from16(h16[r]));
+  }
+  const mf_u32x4 pop = mf_u32x4{h16[0] | (h16[1] << 16), h16[2] | (h16[3] << 16),
+                                l16[0] | (l16[1] << 16), l16[2] | (l16[3] << 16)};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t a01 = pack_lo(v[0][w], v[1][w]);
+    const uint32_t a23 = pack_lo(v[2][w], v[3][w]);
+    const uint32_t b01 = pack_hi(v[0][w], v[1][w]);
+    const uint32_t b23 = pack_hi(v[2][w], v[3][w]);
+    o[2 * w] = Ops::mma(pop, mf_u32x4{a01, a23, a01, a23}, o[2 * w]);
+    o[2 * w + 1] = Ops::mma(pop, mf_u32x4{b01, b23, b01, b23}, o[2 * w + 1]);
+  }
+}
+
 template <class Src> struct LanesOf;
 template <> struct LanesOf<PoolSrc> { using type = PoolLanes; };
 template <> struct LanesOf<DescSrc> { using type = DescLanes; };
@@ -302,62 +372,8 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   };
 
   auto compute_block = [&](const Blk& B) {
-    // scores of row n for tokens 4r + q4
-    mf_f32x4 sc = mf_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) sc = Ops::mma(B.k[i], qop[i], sc);
-    float x[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v = sc[r] * scale;
-      if constexpr (kCap) v = tanhf(v * inv_cap) * cap;
-      if constexpr (kMask) v += B.mk[r];
-      if constexpr (kCausal)
-        if (B.tok0 + 4 * r + q4 > s_row) v = -INFINITY;
-      x[r] = v;
-    }
-    if (B.ntok < kBlockTok) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (4 * r + q4 >= B.ntok) x[r] = -INFINITY;
-    }
-    const float bm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-    if (__builtin_amdgcn_ballot_w64(bm > m + kMfmaSlack)) {
-      // refresh the row max (uniform across the row's four lanes)
-      float rm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-      rm = fmaxf(rm, __shfl_xor(rm, 32, 64));
-      const float mn = fmaxf(m, rm);
-      const float a = fexp(m - ((mn == -INFINITY) ? 0.f : mn));
-      lsum *= a;
-      m = mn;
-      // O rows of this lane are 4*q4 + r: fetch their factors
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float ar = __shfl(a, 4 * q4 + r, 64);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e][r] *= ar;
-      }
-    }
-    const float base = (m == -INFINITY) ? 0.f : m;
-    uint32_t h16[4], l16[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float w = fexp(x[r] - base);
-      lsum += w;
-      h16[r] = Ops::to16(w);
-      l16[r] = Ops::to16(w - Ops::from16(h16[r]));
-    }
-    const mf_u32x4 pop = mf_u32x4{h16[0] | (h16[1] << 16), h16[2] | (h16[3] << 16),
-                                  l16[0] | (l16[1] << 16), l16[2] | (l16[3] << 16)};
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t a01 = pack_lo(B.v[0][w], B.v[1][w]);
-      const uint32_t a23 = pack_lo(B.v[2][w], B.v[3][w]);
-      const uint32_t b01 = pack_hi(B.v[0][w], B.v[1][w]);
-      const uint32_t b23 = pack_hi(B.v[2][w], B.v[3][w]);
-      o[2 * w] = Ops::mma(pop, mf_u32x4{a01, a23, a01, a23}, o[2 * w]);
-      o[2 * w + 1] = Ops::mma(pop, mf_u32x4{b01, b23, b01, b23}, o[2 * w + 1]);
-    }
+    mfma_block_step<Ops, kMask, kCap, kCausal>(B.k, B.v, B.mk, B.ntok, B.tok0, qop, m, lsum, o,
+                                               scale, cap, inv_cap, s_row, q4);
   };
 
   // ---- main loop: a ring of kMfmaBufs register buffers, kMfmaBufs - 1
@@ -415,6 +431,215 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   }
   __syncthreads();
   split_epilogue_d128<T, NW, kMfmaRows>(sm, p, tid, tile, split, total, nrows, r0, b, hk);
+}
+
+// ---- query chunks: K/V blocks staged through LDS ----------------------------
+// For q_len > 1 with more than one 16-row tile per KV head.  A workgroup of
+// four waves owns four 16-row tiles (one per wave) and walks the split's
+// blocks in stages of four: wave w loads block w of the stage (K and V,
+// 4 KiB each) from HBM / L2 into registers one stage ahead, writes it to LDS,
+// and after one barrier every wave computes all four blocks from LDS.  K and
+// V sit in LDS as 16-byte chunks with chunk c of token t at slot c ^ (t % 16),
+// so the operand reads of a wave (16 tokens x one chunk for K, one token x
+// 16 chunks for V) are free of bank conflicts.  The per-block arithmetic is
+// mfma_block_step, as in the decode kernel; each wave writes its own split
+// partial.  No in-kernel merge: merge_splits_d128_kernel follows.
+constexpr int kChunkStage = 4;        // blocks per stage = waves per workgroup
+
+template <typename T, class Src, int FEAT>
+__global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) {
+  using Ops = MfmaOps<T>;
+  constexpr int NW = kChunkStage;
+  constexpr int kRow = 256;            // bytes per token row (128 dims x 2 B)
+  constexpr int kBlk = kBlockTok * kRow;  // 4 KiB per block of K (or V)
+  constexpr bool kMask = (FEAT & kFeatMask) != 0;
+  constexpr bool kCap = (FEAT & kFeatCap) != 0;
+  constexpr bool kCausal = (FEAT & kFeatCausal) != 0;
+  // [buffer][K, V][block of the stage][16-byte chunk]
+  __shared__ mf_u32x4 lds[2][2][kChunkStage][kBlk / 16];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int q4 = lane >> 4;
+  const int n = lane & 15;
+
+  const int split_local = blockIdx.x;
+  const int hk = blockIdx.y % p.Hkv;
+  const int qt_w = (blockIdx.y / p.Hkv) * NW + wave;
+  const bool wave_rows = qt_w < p.n_qtiles;
+  const int qt = wave_rows ? qt_w : p.n_qtiles - 1;
+  const int b = blockIdx.z;
+  const int tile = (b * p.Hkv + hk) * p.n_qtiles + qt;
+  const int S = p.S;
+  const int G = p.G;
+  const int r0 = qt * kMfmaRows;
+  const int nrows = min(kMfmaRows, G * S - r0);
+
+  const typename LanesOf<Src>::type lanes =
+      lane_pages(src, b, p.lo + split_local * p.pps, lane);
+  const bool row_ok = n < nrows;
+  const int rr = r0 + (row_ok ? n : 0);
+  const int g_row = rr / S;
+  const int s_row = rr % S;
+  mf_u32x4 qop[4];
+  {
+    const int h = hk * G + g_row;
+    const char* qp = reinterpret_cast<const char*>(p.q) +
+                     ((int64_t)(b * p.Hq + h) * S + s_row) * kRow;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qp + 16 * (4 * i + q4));
+      qop[i] = row_ok ? mf_u32x4{v.x, v.y, v.z, v.w} : mf_u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  const int np = src.n_pages(b);
+  const int lo = min(p.lo, np);
+  const int hi = min(p.hi, np);
+  const int nsplit_launch = (hi - lo + p.pps - 1) / p.pps;
+  const int total = p.total_splits > 0 ? p.total_splits : nsplit_launch;
+  if (split_local == 0 && lane == 0 && wave_rows) p.counts[tile] = total;
+  if (!(total > 0 && split_local < nsplit_launch)) return;   // uniform per workgroup
+  const int split = p.split_base + split_local;
+  const int pg0 = lo + split_local * p.pps;
+  const int npg = min(pg0 + p.pps, hi) - pg0;
+
+  const float* mrow = nullptr;
+  if constexpr (kMask)
+    mrow = p.mask + (int64_t)b * p.mask_bstride + (int64_t)(hk * G + g_row) * p.mask_hstride +
+           (int64_t)s_row * p.mask_qstride;
+  const float scale = p.scale;
+  const float cap = p.softcap;
+  const float inv_cap = kCap ? 1.f / cap : 0.f;
+
+  float m = -INFINITY;
+  float lsum = 0.f;
+  mf_f32x4 o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int bpp = p.bpp;
+  const int nblk = npg * bpp;
+  const int nstage = (nblk + kChunkStage - 1) / kChunkStage;
+
+  // block bi's page view (uniform): valid tokens and the HELM token cursor
+  auto block_view = [&](int bi, int& ntok, int& tok0, const char*& kb, const char*& vb) {
+    const bool valid = bi < nblk;
+    const int pi = valid ? bi / bpp : 0;
+    const int sub = valid ? bi - pi * bpp : 0;
+    const PageView pv = lane_page_view(src, lanes, b, pg0 + pi, pi, hk);
+    const int tok_in = sub * kBlockTok;
+    ntok = valid ? sclamp(pv.used - tok_in, 0, kBlockTok) : 0;
+    tok0 = pv.tok_off + tok_in;
+    kb = pv.k + tok_in * kRow;
+    vb = pv.v + tok_in * kRow;
+  };
+
+  // additive mask of the lane's row for the four blocks of a stage (tokens
+  // 4r + q4 of each block), loaded a stage ahead like the K/V chunks
+  float mcur[kChunkStage][4], mnext[kChunkStage][4];
+  auto load_mask = [&](int st, float (&mk)[kChunkStage][4]) {
+    if constexpr (kMask) {
+#pragma unroll
+      for (int j = 0; j < kChunkStage; ++j) {
+        int ntok, tok0;
+        const char *kb, *vb;
+        block_view(st * kChunkStage + j, ntok, tok0, kb, vb);
+        const int last = max(ntok - 1, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          mk[j][r] = ntok > 0 ? mrow[tok0 + min(4 * r + q4, last)] : 0.f;
+      }
+    }
+  };
+
+  // this wave's share of a stage: block (stage * 4 + wave), 4 chunks of K and
+  // 4 of V per lane (chunk lane + 64 u of the block)
+  mf_u32x4 gk[4], gv[4];
+  auto load_stage = [&](int st) {
+    int ntok, tok0;
+    const char *kb, *vb;
+    block_view(st * kChunkStage + wave, ntok, tok0, kb, vb);
+    const auto rk = make_rsrc(kb, ntok * kRow);
+    const auto rv = make_rsrc(vb, ntok * kRow);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      gk[u] = buf_load16_nt(rk, (lane + 64 * u) * 16);
+      gv[u] = buf_load16_nt(rv, (lane + 64 * u) * 16);
+    }
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = lane + 64 * u;          // chunk index in the block
+      const int t = c >> 4;                 // token
+      const int slot = t * 16 + ((c & 15) ^ t);
+      lds[buf][0][wave][slot] = gk[u];
+      lds[buf][1][wave][slot] = gv[u];
+    }
+  };
+
+  const int tau = 4 * (n & 3) + (n >> 2);   // K token of this lane in a block
+  if (nstage > 0) {
+    load_stage(0);
+    if (wave_rows) load_mask(0, mcur);
+  }
+  for (int st = 0; st < nstage; ++st) {
+    const int buf = st & 1;
+    store_stage(buf);
+    if (st + 1 < nstage) {
+      load_stage(st + 1);
+      if (wave_rows) load_mask(st + 1, mnext);
+    }
+    __syncthreads();
+    if (wave_rows) {
+#pragma unroll
+      for (int j = 0; j < kChunkStage; ++j) {
+        int ntok, tok0;
+        const char *kb, *vb;
+        block_view(st * kChunkStage + j, ntok, tok0, kb, vb);
+        if (ntok == 0) continue;            // uniform: an empty or past-the-end block
+        mf_u32x4 k[4], v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) k[i] = lds[buf][0][j][tau * 16 + ((q4 + 4 * i) ^ tau)];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int t = q4 + 4 * jj;
+          v[jj] = lds[buf][1][j][t * 16 + (n ^ t)];
+        }
+        float mk[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (kMask) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mk[r] = mcur[j][r];
+        }
+        mfma_block_step<Ops, kMask, kCap, kCausal>(k, v, mk, ntok, tok0, qop, m, lsum, o, scale,
+                                                   cap, inv_cap, s_row, q4);
+      }
+    }
+    if constexpr (kMask) {
+#pragma unroll
+      for (int j = 0; j < kChunkStage; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mcur[j][r] = mnext[j][r];
+    }
+  }
+
+  // each wave's own partial (m, l, o[128]) per row, straight from registers
+  if (!wave_rows) return;
+  float lrow = lsum + __shfl_xor(lsum, 16, 64);
+  lrow += __shfl_xor(lrow, 32, 64);
+  const int64_t part = ((int64_t)tile * p.max_splits + split) * p.rows_per_tile;
+  if (q4 == 0 && n < nrows)
+    *reinterpret_cast<float2*>(&p.ws_ml[(part + n) * 2]) = make_float2(m, lrow);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 4 * q4 + r;
+    if (row < nrows) {
+      float* dst = &p.ws_o[(part + row) * 128 + 8 * n];
+      *reinterpret_cast<float4*>(dst) = make_float4(o[0][r], o[1][r], o[2][r], o[3][r]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4][r], o[5][r], o[6][r], o[7][r]);
+    }
+  }
 }
 
 }  // namespace helm

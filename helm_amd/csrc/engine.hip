@@ -160,6 +160,7 @@ void plan_shape(Plan& pl, int G, int q_len, int D, int max_tok_per_page) {
   // tile each over the same pages (K/V read once per workgroup from L2, not
   // once per tile); HELM_AMD_ROW_WAVES=0 keeps one tile per workgroup
   pl.row_waves = (pl.mfma && pl.n_qtiles >= 2 && env_int("HELM_AMD_ROW_WAVES", 1)) ? 1 : 0;
+  if (pl.row_waves) pl.nw = kChunkStage;  // chunk_mfma_kernel: four waves, one tile each
 }
 
 int max_pps_of(const Plan& pl) { return pl.mfma ? kMfmaMaxPps : kMaxPps; }
