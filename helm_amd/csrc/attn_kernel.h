@@ -41,6 +41,13 @@ constexpr int kMaxSplits = 256; // splits per (sequence, head, tile) merged
 constexpr int kMergeBatch = 8;  // split partials a merging thread loads at once
 constexpr float kRescaleSlack = 8.f;  // lazy online-softmax rescale threshold
 
+// Query row rr of a KV head's G * S rows is query position rr / G of group
+// head rr % G: the G heads that share a KV head and one position sit in
+// adjacent rows, so the rows of a tile read one mask row (and have one causal
+// limit) per position instead of one per row.  Decode (S = 1) has row = head.
+struct RowCoord { int g, s; };
+__device__ __forceinline__ RowCoord row_coord(int rr, int G) { return {rr % G, rr / G}; }
+
 // ---- element types ----------------------------------------------------------
 struct f16_t { uint16_t x; };
 struct bf16_t { uint16_t x; };
@@ -513,7 +520,8 @@ __device__ __forceinline__ void fused_merge_tail(Smem<NW, GM, DMAX>& sm,
       sm.redml[tid] = make_float2(M, L);
     } else {
       const int rr = r0 + g;
-      const int h = hk * G + rr / S, s = rr % S;
+      const RowCoord rc = row_coord(rr, G);
+      const int h = hk * G + rc.g, s = rc.s;
       char* orow = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * S + s) * D * QB;
       const float inv = 1.f / fmaxf(L, 1e-12f);
       const float a[4] = {acc.x, acc.y, acc.z, acc.w};
@@ -541,7 +549,8 @@ __device__ __forceinline__ void fused_merge_tail(Smem<NW, GM, DMAX>& sm,
       const int g = tid / (D / cw);
       const int d0 = (tid - g * (D / cw)) * cw;
       const int rr = r0 + g;
-      const int h = hk * G + rr / S, s = rr % S;
+      const RowCoord rc = row_coord(rr, G);
+      const int h = hk * G + rc.g, s = rc.s;
       char* orow = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * S + s) * D * QB;
       const float inv = 1.f / fmaxf(L, 1e-12f);
       const float a[4] = {acc.x, acc.y, acc.z, acc.w};
@@ -690,7 +699,8 @@ __device__ __forceinline__ void split_epilogue_d128(Smem<NW, GM, 128>& sm, const
         // one thread per item: write the output row chunk directly
         const float inv = 1.f / fmaxf(L, 1e-12f);
         const int rr = r0 + g;
-        const int h = hk * p.G + rr / p.S, sq = rr % p.S;
+        const RowCoord rc = row_coord(rr, p.G);
+        const int h = hk * p.G + rc.g, sq = rc.s;
         char* orow =
             reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * p.S + sq) * 128 * QB;
         store_elem<TQ>(orow + (d0 + 0) * QB, acc.x * inv);
@@ -723,7 +733,8 @@ __device__ __forceinline__ void split_epilogue_d128(Smem<NW, GM, 128>& sm, const
       const int g = i >> 5;
       const int d0 = (i & 31) * 4;
       const int rr = r0 + g;
-      const int h = hk * p.G + rr / p.S, sq = rr % p.S;
+      const RowCoord rc = row_coord(rr, p.G);
+      const int h = hk * p.G + rc.g, sq = rc.s;
       char* orow = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * p.S + sq) * 128 * QB;
       store_elem<TQ>(orow + (d0 + 0) * QB, o.x * inv);
       store_elem<TQ>(orow + (d0 + 1) * QB, o.y * inv);
@@ -762,7 +773,8 @@ __global__ __launch_bounds__(kThreads) void merge_splits_kernel(AttnParams p) {
   const int r0 = qt * RS;
   if (r0 + row >= G * S) return;
   const int rr = r0 + row;
-  const int h = hk * G + rr / S, s = rr % S;
+  const RowCoord rc = row_coord(rr, G);
+  const int h = hk * G + rc.g, s = rc.s;
   char* out_row = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * S + s) * D * QB;
   const int total = p.counts[tile];
 
@@ -951,7 +963,8 @@ __global__ __launch_bounds__(kThreads) void merge_splits_d128_kernel(AttnParams 
       o.w = fmaf(wgt, t.w, o.w);
     }
     const float inv = 1.f / fmaxf(Lx, 1e-12f);
-    const int h = hk * p.G + rr / p.S, sq = rr % p.S;
+    const RowCoord rc = row_coord(rr, p.G);
+    const int h = hk * p.G + rc.g, sq = rc.s;
     char* orow = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * p.S + sq) * 128 * QB;
     store_elem<TQ>(orow + (tid * 4 + 0) * QB, o.x * inv);
     store_elem<TQ>(orow + (tid * 4 + 1) * QB, o.y * inv);
@@ -1006,7 +1019,8 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
     if (p.fused && split_local == 0) {
       for (int idx = tid; idx < nrows * D; idx += kThreads) {
         const int rr = r0 + idx / D;
-        const int h = hk * G + rr / S, s = rr % S;
+        const RowCoord rc = row_coord(rr, G);
+        const int h = hk * G + rc.g, s = rc.s;
         const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * D + idx % D;
         store_elem<TQ>(reinterpret_cast<char*>(p.out) + o_off * QB, 0.f);
       }
@@ -1029,7 +1043,8 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
 #pragma unroll
   for (int g = 0; g < GM; ++g) {
     const int rr = r0 + (g < nrows ? g : 0);
-    const int gg = rr / S, s = rr % S;
+    const RowCoord rc = row_coord(rr, G);
+    const int gg = rc.g, s = rc.s;
     const int h = hk * G + gg;
     srow[g] = s;
     mrow[g] = (int64_t)b * p.mask_bstride + (int64_t)h * p.mask_hstride +

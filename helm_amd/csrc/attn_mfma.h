@@ -277,8 +277,9 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   // ---- query operand: row n of the tile at dim chunks 4i + q4 ---------------
   const bool row_ok = n < nrows;
   const int rr = r0 + (row_ok ? n : 0);
-  const int g_row = rr / S;
-  const int s_row = rr % S;
+  const RowCoord rc = row_coord(rr, G);
+  const int g_row = rc.g;
+  const int s_row = rc.s;
   mf_u32x4 qop[4];
   {
     const int h = hk * G + g_row;
@@ -306,7 +307,8 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
     if (total == 0 && p.fused && split_local == 0) {
       for (int idx = tid; idx < nrows * 128; idx += NT) {
         const int zr = r0 + idx / 128;
-        const int h = hk * G + zr / S, s = zr % S;
+        const RowCoord rc = row_coord(zr, G);
+        const int h = hk * G + rc.g, s = rc.s;
         const int64_t o_off = ((int64_t)(b * p.Hq + h) * S + s) * 128 + idx % 128;
         store_elem<T>(reinterpret_cast<char*>(p.out) + o_off * 2, 0.f);
       }
@@ -480,8 +482,9 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
       lane_pages(src, b, p.lo + split_local * p.pps, lane);
   const bool row_ok = n < nrows;
   const int rr = r0 + (row_ok ? n : 0);
-  const int g_row = rr / S;
-  const int s_row = rr % S;
+  const RowCoord rc = row_coord(rr, G);
+  const int g_row = rc.g;
+  const int s_row = rc.s;
   mf_u32x4 qop[4];
   {
     const int h = hk * G + g_row;

@@ -134,10 +134,12 @@ class LayerKVCache:
         self._dev = None                # device copy of the records (uint8 tensor)
         self._dev_dirty: List[int] = []  # records changed since the last upload
         self._dev_all = False           # every record needs an upload
+        self._gen = 0                   # bumped whenever the page list changes
 
     def _reset(self) -> None:
         """Drops every page (the list is emptied in place)."""
         self.pages.clear()
+        self._gen += 1
         self.tail_page = None
         self.total_tokens = 0
         self._rec_ok, self._rec_sig = True, None
@@ -149,6 +151,7 @@ class LayerKVCache:
 
     def append_page(self, page: KVPage):
         self.pages.append(page)
+        self._gen += 1
         self.tail_page = page
         n = len(self.pages)
         if n > self._rec.shape[0]:
@@ -208,6 +211,7 @@ class LayerKVCache:
         """Page `idx` moved tiers: `page` takes its place and record."""
         old = self.pages[idx]
         self.pages[idx] = page
+        self._gen += 1
         if self.tail_page is old:
             self.tail_page = page
         self._set_record(idx, page)
@@ -273,6 +277,44 @@ def _used_bytes(page: KVPage) -> int:
     if k.dim() != 4:
         return 0
     return page.used_tokens * k.size(0) * k.size(1) * k.size(3) * k.element_size() * 2
+
+
+class _LayerPages(list):
+    """What ``iterate_layer_pages`` returns: a shallow copy of a layer's page
+    list (kv_cache.py:173-177) that also remembers the layer and the layer's
+    page generation.  While the layer's pages are unchanged and the list has
+    not been modified, ``perform_streaming_attention`` attends through the
+    layer's records instead of reading every page in Python; any in-place
+    change to the list drops that link (the list is then an ordinary list)."""
+
+    __slots__ = ("_layer", "_gen")
+
+    def __init__(self, layer: LayerKVCache):
+        super().__init__(layer.pages)
+        self._layer = layer
+        self._gen = layer._gen
+
+    def _live_layer(self) -> Optional[LayerKVCache]:
+        layer = self._layer
+        if layer is None or layer._gen != self._gen or len(layer.pages) != len(self):
+            return None
+        return layer
+
+
+def _detaching(name):
+    base = getattr(list, name)
+
+    def method(self, *args, **kwargs):
+        self._layer = None
+        return base(self, *args, **kwargs)
+    method.__name__ = name
+    return method
+
+
+for _name in ("append", "extend", "insert", "pop", "remove", "clear", "sort", "reverse",
+              "__setitem__", "__delitem__", "__iadd__", "__imul__"):
+    setattr(_LayerPages, _name, _detaching(_name))
+del _name
 
 
 # ── token writes ───────────────────────────────────────────────────────────────
@@ -474,7 +516,7 @@ class KVCacheManager:
     def iterate_layer_pages(self, layer_id: int):
         if layer_id not in self.layers:
             return []
-        return list(self.layers[layer_id].pages)
+        return _LayerPages(self.layers[layer_id])
 
     def _evictable(self):
         """(layer, page) pairs HELM may evict: GPU-resident, full, not a tail
@@ -836,6 +878,10 @@ def perform_streaming_attention(
     device = query.device
     if scale is None:
         scale = 1.0 / math.sqrt(query.size(-1))
+    if type(pages) is _LayerPages and device.type == "cuda":
+        out = _attend_layer_pages(query, pages, scale, attention_mask, softcap)
+        if out is not None:
+            return out
     active_pages = [p for p in pages if p.used_tokens > 0 and p.state != 'DEAD']
     if not active_pages:
         return torch.zeros_like(query)
@@ -881,6 +927,37 @@ def perform_streaming_attention(
                 for i in range(B)], dim=0)
         seqs.append(segs)
     return _attend(query, seqs, Hkv, kv_dtype, scale, attention_mask, softcap, causal)
+
+
+def _attend_layer_pages(query: torch.Tensor, pages: _LayerPages, scale: float,
+                        attention_mask: Optional[torch.Tensor], softcap: Optional[float]):
+    """perform_streaming_attention over a layer's unchanged page list from
+    the layer's records: the same path choice, token order, masking and
+    prefetch counting as the page-by-page branch below, without reading each
+    page in Python.  None when the records cannot serve."""
+    layer = pages._live_layer()
+    if layer is None or query.size(0) != 1 or not _async_kv_prefetch_enabled():
+        return None
+    rec = layer.records()
+    n = len(pages)
+    sig = layer._rec_sig
+    if rec is None or n == 0 or layer._n_other or sig is None or sig[2] != query.size(-1):
+        return None
+    kv_dtype, Hkv = sig[0], sig[1]
+    t = int(rec["tok_off"][n - 1]) + int(rec["used"][n - 1])
+    if t == 0:
+        return torch.zeros_like(query)
+    host = layer._n_host > 0
+    if host:
+        _record_prefetch(layer._n_host, layer._host_bytes)
+    masked = attention_mask is not None or softcap is not None
+    # Path 1's top-left causal applies to all-device pages only (Path 3 is unmasked)
+    causal = (not masked) and (not host) and query.size(2) > 1
+    if not host:
+        return _attend_layers(query, [layer], [t], Hkv, kv_dtype, scale, attention_mask, softcap,
+                              causal)
+    return _attend_records(query, rec, np.array([0, n], dtype=np.int32), t, Hkv, kv_dtype, scale,
+                           attention_mask, softcap, causal)
 
 
 def _batch_view(page: KVPage, i: int) -> KVPage:

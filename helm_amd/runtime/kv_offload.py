@@ -193,7 +193,7 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
         _record_prefetch(layer._n_host, layer._host_bytes)
     if bsz <= _MAX_SEQ_ARGS and not any(layer._n_host for layer in layers):
         # every page on the device: the layers' device-resident records
-        return _attend_layers(q, layers, lens, Hkv, kv_dtype, scale, attention_mask, None,
+        return _attend_layers(q, layers, lens, Hkv, kv_dtype, scale, attention_mask, softcap,
                               False)
     if bsz == 1 or not any(layer._n_host for layer in layers):
         return _attend_records(q, arr, seq_off, max(lens), Hkv, kv_dtype, scale,

@@ -496,6 +496,38 @@ def test_decode_from_layer_records_matches_page_list_path(masked, evict, kernel,
         assert (x.float() - y.float()).abs().max().item() <= 1e-2
 
 
+@pytest.mark.parametrize("evict", [False, True])
+def test_decode_from_records_applies_softcap(evict):
+    """The records decode path with a logit softcap (Gemma-2's decode,
+    kv_cache.py:521-522): with every page resident (device-resident records)
+    and with host pages, the output is tanh-capped attention, not plain
+    attention."""
+    from helm_amd.runtime.kv_offload import _decode_from_records
+    Hq, kvh, D, P, cap = 8, 2, 128, 16, 2.0
+    lens = [150, 77]
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=torch.bfloat16)
+    wm = 2 * (2 * kvh * P * D * 2) if evict else 10 ** 12
+    kvcms = [KVCacheManager(a, gpu_high_watermark_bytes=wm) for _ in lens]
+    g = torch.Generator().manual_seed(5)
+    kv = [(torch.randn(1, kvh, n, D, generator=g).bfloat16(),
+           torch.randn(1, kvh, n, D, generator=g).bfloat16()) for n in lens]
+    for m, (k, v) in zip(kvcms, kv):
+        m.append_prefill(0, k.to(DEV), v.to(DEV))
+    assert any(L._n_host for m in kvcms for L in m.layers.values()) == evict
+    # scores of a few units, so that a cap of 2 changes them
+    q = (3 * torch.randn(len(lens), Hq, 1, D, generator=g)).bfloat16()
+    out = _decode_from_records(kvcms, q.to(DEV), 0, kvh, D, 1 / math.sqrt(D), None, cap)
+    assert out is not None
+    torch.cuda.synchronize()
+    for i, (k, v) in enumerate(kv):
+        ref = A.attention_fp64_batched(q[i].float(), k[0].float(), v[0].float(), softcap=cap)
+        plain = A.attention_fp64_batched(q[i].float(), k[0].float(), v[0].float())
+        assert (ref - plain).abs().max().item() > 0.05
+        assert (out[i].double().cpu() - ref).abs().max().item() <= 1e-2
+    for m in kvcms:
+        m.clear()
+
+
 @pytest.mark.parametrize("B,T,steps", [(4, 16384, 18), (17, 600, 3)])
 def test_decode_batched_many_pages_and_many_sequences(B, T, steps):
     """_decode_batched at scale: 4 sequences x 16k tokens (1,024 pages each,
@@ -604,9 +636,11 @@ def _tiny_model(arch: str):
         cfg, cls = tm.mistral.MistralConfig(**common), tm.mistral.MistralForCausalLM
     elif arch == "olmo2":
         cfg, cls = tm.olmo2.Olmo2Config(**common), tm.olmo2.Olmo2ForCausalLM
-    elif arch == "gemma2":
+    elif arch.startswith("gemma2"):
+        # "gemma2-cap1": a logit softcap of 1, so that the tanh changes every score
+        cap = 1.0 if arch == "gemma2-cap1" else 50.0
         cfg = tm.gemma2.Gemma2Config(head_dim=16, sliding_window=8, query_pre_attn_scalar=16,
-                                      attn_logit_softcapping=50.0, final_logit_softcapping=30.0,
+                                      attn_logit_softcapping=cap, final_logit_softcapping=30.0,
                                       **common)
         cls = tm.gemma2.Gemma2ForCausalLM
     else:
@@ -619,7 +653,8 @@ def _tiny_model(arch: str):
     return ref, model
 
 
-@pytest.mark.parametrize("arch", ["llama", "qwen2", "qwen3", "mistral", "olmo2", "gemma2"])
+@pytest.mark.parametrize("arch", ["llama", "qwen2", "qwen3", "mistral", "olmo2", "gemma2",
+                                  "gemma2-cap1"])
 def test_tiny_models_decode_logits_match_hf_with_eviction(arch):
     """Every architecture the paged forwards cover (kv_offload.py:291-651): a
     tiny random model prefills in two chunks and decodes through the paged,
@@ -703,3 +738,65 @@ def test_tiny_llama_greedy_matches_hf_with_eviction():
     mgr.restore()
     assert out_tokens == ref_tokens
     assert KC.get_paging_stats()["pages_evicted"] > 0
+
+
+@pytest.mark.parametrize("case", ["decode", "mask", "softcap", "chunk", "chunk-mask", "host",
+                                  "host-mask", "host-chunk"])
+def test_layer_page_list_attention_matches_page_by_page(case, monkeypatch):
+    """perform_streaming_attention over the list iterate_layer_pages returns
+    runs from the layer's records; a plain copy of the same list runs page by
+    page.  The two agree, count the same prefetches, and match the fp64
+    oracle: decode with and without a mask or softcap, a query chunk under
+    Path 1's top-left causal mask or an additive mask, and pages partly in
+    host memory (Path 3: unmasked, no causal)."""
+    taken = []
+    real = KC._attend_layer_pages
+
+    def spy(*args):
+        out = real(*args)
+        taken.append(out is not None)
+        return out
+    monkeypatch.setattr(KC, "_attend_layer_pages", spy)
+    Hq, kvh, D, P, T = 8, 2, 128, 16, 300
+    host = case.startswith("host")
+    S = 5 if "chunk" in case else 1
+    page_bytes = 2 * kvh * P * D * 2
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=torch.bfloat16)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=4 * page_bytes if host else 10 ** 12)
+    g = torch.Generator().manual_seed(21)
+    k = torch.randn(1, kvh, T, D, generator=g).bfloat16()
+    v = torch.randn(1, kvh, T, D, generator=g).bfloat16()
+    mgr.append_prefill(0, k.to(DEV), v.to(DEV))
+    assert (mgr.layers[0]._n_host > 0) == host
+    q = (2 * torch.randn(1, Hq, S, D, generator=g)).bfloat16()
+    mask = softcap = None
+    ref_mask = None
+    if "mask" in case:
+        mask = torch.zeros(1, 1, S, T)
+        mask[..., 3::5] = float("-inf")
+        mask[0, 0, :, T - 9:] = -2.5
+        ref_mask = mask[0].double()
+    elif case == "softcap":
+        softcap = 3.0
+    elif S > 1 and not host:
+        ref_mask = torch.zeros(1, S, T, dtype=torch.float64)
+        ref_mask[0][torch.arange(T)[None, :] > torch.arange(S)[:, None]] = float("-inf")
+    outs, stats = [], []
+    for linked in (True, False):
+        pages = mgr.iterate_layer_pages(0)
+        if not linked:
+            pages = list(pages)
+        KC.reset_paging_stats()
+        outs.append(perform_streaming_attention(
+            q.to(DEV), pages, attention_mask=mask.to(DEV) if mask is not None else None,
+            softcap=softcap).cpu())
+        stats.append(KC.get_paging_stats())
+    assert taken == [True]
+    assert stats[0] == stats[1] and (stats[0]["prefetch_calls"] == 1) == host
+    ref = A.attention_fp64_batched(q[0].float(), k[0].float(), v[0].float(), mask=ref_mask,
+                                   softcap=softcap)
+    for o in outs:
+        assert o.shape == q.shape and o.dtype == q.dtype
+        assert (o[0].double() - ref).abs().max().item() <= 1e-2
+    assert (outs[0].float() - outs[1].float()).abs().max().item() <= 1e-2
+    mgr.clear()

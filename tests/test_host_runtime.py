@@ -355,3 +355,46 @@ def test_external_layer_changes_rebuild_the_heap():
     assert mgr._ev_bytes == (2 + 2) * (2 * H * P * D * 4) + (2 * H * P * D * 4)
     mgr.clear()
     assert mgr._ev_bytes == 0 and mgr._evq == []
+
+
+def test_layer_page_list_link_follows_the_layer():
+    """iterate_layer_pages returns a plain list (kv_cache.py:173-177) that stays
+    linked to the layer's records only while it holds exactly the layer's
+    pages: a token written into the tail keeps the link; a new page, an
+    eviction, a clear or any in-place change of the list drops it."""
+    H, D, P = 2, 4, 4
+    page_bytes = 2 * H * P * D * 4
+    a = _CpuBackedGpuAllocator(1, H, D, page_size=P, dtype=torch.float32)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 9)
+    mgr.append_prefill(0, *_pos_kv(P + 2, 0, H, D))
+    pages = mgr.iterate_layer_pages(0)
+    assert isinstance(pages, list) and pages == mgr.layers[0].pages
+    assert pages is not mgr.layers[0].pages
+    layer = mgr.layers[0]
+    assert pages._live_layer() is layer
+    mgr.append_decode(0, *_pos_kv(1, P + 2, H, D))          # into the tail
+    assert pages._live_layer() is layer and pages[-1].used_tokens == 3
+    mgr.append_decode(0, *_pos_kv(1, P + 3, H, D))          # fills the tail
+    assert pages._live_layer() is layer
+    mgr.append_decode(0, *_pos_kv(1, P + 4, H, D))          # a new page
+    assert pages._live_layer() is None and len(pages) == 2
+    assert mgr.iterate_layer_pages(0)._live_layer() is layer
+    for change in (lambda l: l.append(l[0]), lambda l: l.pop(), lambda l: l.reverse(),
+                   lambda l: l.__setitem__(0, l[0]), lambda l: l.__delitem__(0),
+                   lambda l: l.extend([]), lambda l: l.sort(key=lambda p: 0),
+                   lambda l: l.insert(0, l[0]), lambda l: l.clear()):
+        fresh = mgr.iterate_layer_pages(0)
+        change(fresh)
+        assert fresh._live_layer() is None
+    fresh = mgr.iterate_layer_pages(0)
+    fresh += []
+    assert fresh._live_layer() is None
+    assert type(mgr.iterate_layer_pages(0)[:1]) is list     # slices are plain lists
+    # an eviction replaces a page object: older lists lose the link
+    fresh = mgr.iterate_layer_pages(0)
+    mgr.evict_pages(page_bytes)
+    assert fresh[0].state == "DEAD" and fresh._live_layer() is None
+    assert mgr.iterate_layer_pages(0)[0].state == "CPU"
+    fresh = mgr.iterate_layer_pages(0)
+    mgr.clear()
+    assert fresh._live_layer() is None and mgr.iterate_layer_pages(0) == []
