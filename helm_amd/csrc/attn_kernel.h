@@ -407,6 +407,7 @@ struct AttnParams {
   uint32_t* tickets;  // [tiles] arrivals (fused mode; zero between calls)
   int fused;          // 1: the last split of a tile merges in-kernel
   int row_waves;      // 1 (matrix-core kernel): each wave owns a 16-row tile
+  int direct_out;     // 1: the call has one split; the chunk kernel writes the output
 };
 
 // Per-workgroup LDS: per-wave online-softmax states of the tile's rows, and

@@ -60,12 +60,18 @@ template <> struct MfmaOps<bf16_t> {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(mf_bf16x8, a),
                                                    __builtin_bit_cast(mf_bf16x8, b), c, 0, 0, 0);
   }
-  // round to nearest even (finite, non-negative inputs: softmax weights)
-  __device__ static __forceinline__ uint32_t to16(float x) {
-    const uint32_t u = __float_as_uint(x);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  // Two weights as packed 16-bit hi and lo parts, hi = RNE(w), lo = RNE(w - hi)
+  // (v_cvt_pk_bf16_f32 rounds to nearest even); element 0 in the low half.
+  __device__ static __forceinline__ void split2(float w0, float w1, uint32_t& hi,
+                                                uint32_t& lo) {
+    hi = pk(w0, w1);
+    lo = pk(w0 - __uint_as_float(hi << 16), w1 - __uint_as_float(hi & 0xffff0000u));
   }
-  __device__ static __forceinline__ float from16(uint32_t h) { return __uint_as_float(h << 16); }
+  __device__ static __forceinline__ uint32_t pk(float a, float b) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, bf2));
+  }
 };
 
 template <> struct MfmaOps<f16_t> {
@@ -73,11 +79,21 @@ template <> struct MfmaOps<f16_t> {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(mf_f16x8, a),
                                                   __builtin_bit_cast(mf_f16x8, b), c, 0, 0, 0);
   }
-  __device__ static __forceinline__ uint32_t to16(float x) {
-    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+  __device__ static __forceinline__ uint32_t pk(float a, float b) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, h2));
   }
-  __device__ static __forceinline__ float from16(uint32_t h) {
-    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+  // hi = RNE(w), lo = RNE(w - hi) in fp16, packed two per word (v_cvt_pk_f16_f32)
+  __device__ static __forceinline__ void split2(float w0, float w1, uint32_t& hi,
+                                                uint32_t& lo) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const h2 h = __builtin_convertvector((f2){w0, w1}, h2);
+    hi = __builtin_bit_cast(uint32_t, h);
+    const f2 back = __builtin_convertvector(h, f2);
+    lo = __builtin_bit_cast(uint32_t,
+                            __builtin_convertvector((f2){w0 - back[0], w1 - back[1]}, h2));
   }
 };
 
@@ -212,16 +228,16 @@ __device__ __forceinline__ void mfma_block_step(const mf_u32x4 (&k)[4], const mf
     }
   }
   const float base = (m == -INFINITY) ? 0.f : m;
-  uint32_t h16[4], l16[4];
+  float wt[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const float w = fexp(x[r] - base);
-    lsum += w;
-    h16[r] = Ops::to16(w);
-    l16[r] = Ops::to16(w - Ops::from16(h16[r]));
+    wt[r] = fexp(x[r] - base);
+    lsum += wt[r];
   }
-  const mf_u32x4 pop = mf_u32x4{h16[0] | (h16[1] << 16), h16[2] | (h16[3] << 16),
-                                l16[0] | (l16[1] << 16), l16[2] | (l16[3] << 16)};
+  uint32_t h01, l01, h23, l23;
+  Ops::split2(wt[0], wt[1], h01, l01);
+  Ops::split2(wt[2], wt[3], h23, l23);
+  const mf_u32x4 pop = mf_u32x4{h01, h23, l01, l23};
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const uint32_t a01 = pack_lo(v[0][w], v[1][w]);
@@ -444,14 +460,17 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
 // V sit in LDS as 16-byte chunks with chunk c of token t at slot c ^ (t % 16),
 // so the operand reads of a wave (16 tokens x one chunk for K, one token x
 // 16 chunks for V) are free of bank conflicts.  The per-block arithmetic is
-// mfma_block_step, as in the decode kernel; each wave writes its own split
-// partial.  No in-kernel merge: merge_splits_d128_kernel follows.
+// mfma_block_step, as in the decode kernel.  A split may span any number of
+// pages: the page records sit one per lane in windows of 64 pages, the next
+// window loaded when the current one is entered.  Each wave writes its own
+// split partial (merged by merge_splits_d128_kernel), or, when the call has a
+// single split (p.direct_out), its normalized output rows.
 constexpr int kChunkStage = 4;        // blocks per stage = waves per workgroup
+constexpr int kRecWindow = 64;        // page records held per lane window
 
 template <typename T, class Src, int FEAT>
 __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) {
   using Ops = MfmaOps<T>;
-  constexpr int NW = kChunkStage;
   constexpr int kRow = 256;            // bytes per token row (128 dims x 2 B)
   constexpr int kBlk = kBlockTok * kRow;  // 4 KiB per block of K (or V)
   constexpr bool kMask = (FEAT & kFeatMask) != 0;
@@ -468,7 +487,7 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
 
   const int split_local = blockIdx.x;
   const int hk = blockIdx.y % p.Hkv;
-  const int qt_w = (blockIdx.y / p.Hkv) * NW + wave;
+  const int qt_w = (blockIdx.y / p.Hkv) * kChunkStage + wave;
   const bool wave_rows = qt_w < p.n_qtiles;
   const int qt = wave_rows ? qt_w : p.n_qtiles - 1;
   const int b = blockIdx.z;
@@ -478,8 +497,32 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
   const int r0 = qt * kMfmaRows;
   const int nrows = min(kMfmaRows, G * S - r0);
 
-  const typename LanesOf<Src>::type lanes =
-      lane_pages(src, b, p.lo + split_local * p.pps, lane);
+  // output row of this lane's accumulator row 4 q4 + r (direct output)
+  auto out_row = [&](int r) -> char* {
+    const RowCoord c = row_coord(r0 + 4 * q4 + r, G);
+    return reinterpret_cast<char*>(p.out) +
+           (((int64_t)(b * p.Hq + hk * G + c.g) * S + c.s) * 128 + 8 * n) * 2;
+  };
+
+  const int np = src.n_pages(b);
+  const int lo = min(p.lo, np);
+  const int hi = min(p.hi, np);
+  const int nsplit_launch = (hi - lo + p.pps - 1) / p.pps;
+  const int total = p.total_splits > 0 ? p.total_splits : nsplit_launch;
+  if (split_local == 0 && lane == 0 && wave_rows) p.counts[tile] = total;
+  if (!(total > 0 && split_local < nsplit_launch)) {      // uniform per workgroup
+    if (p.direct_out && total == 0 && split_local == 0 && wave_rows) {
+      // no keys: HELM's zeros
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (4 * q4 + r < nrows) *reinterpret_cast<uint4*>(out_row(r)) = make_uint4(0, 0, 0, 0);
+    }
+    return;
+  }
+  const int split = p.split_base + split_local;
+  const int pg0 = lo + split_local * p.pps;
+  const int npg = min(pg0 + p.pps, hi) - pg0;
+
   const bool row_ok = n < nrows;
   const int rr = r0 + (row_ok ? n : 0);
   const RowCoord rc = row_coord(rr, G);
@@ -496,17 +539,6 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
       qop[i] = row_ok ? mf_u32x4{v.x, v.y, v.z, v.w} : mf_u32x4{0u, 0u, 0u, 0u};
     }
   }
-  const int np = src.n_pages(b);
-  const int lo = min(p.lo, np);
-  const int hi = min(p.hi, np);
-  const int nsplit_launch = (hi - lo + p.pps - 1) / p.pps;
-  const int total = p.total_splits > 0 ? p.total_splits : nsplit_launch;
-  if (split_local == 0 && lane == 0 && wave_rows) p.counts[tile] = total;
-  if (!(total > 0 && split_local < nsplit_launch)) return;   // uniform per workgroup
-  const int split = p.split_base + split_local;
-  const int pg0 = lo + split_local * p.pps;
-  const int npg = min(pg0 + p.pps, hi) - pg0;
-
   const float* mrow = nullptr;
   if constexpr (kMask)
     mrow = p.mask + (int64_t)b * p.mask_bstride + (int64_t)(hk * G + g_row) * p.mask_hstride +
@@ -525,33 +557,56 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
   const int nblk = npg * bpp;
   const int nstage = (nblk + kChunkStage - 1) / kChunkStage;
 
-  // block bi's page view (uniform): valid tokens and the HELM token cursor
-  auto block_view = [&](int bi, int& ntok, int& tok0, const char*& kb, const char*& vb) {
-    const bool valid = bi < nblk;
-    const int pi = valid ? bi / bpp : 0;
-    const int sub = valid ? bi - pi * bpp : 0;
-    const PageView pv = lane_page_view(src, lanes, b, pg0 + pi, pi, hk);
-    const int tok_in = sub * kBlockTok;
-    ntok = valid ? sclamp(pv.used - tok_in, 0, kBlockTok) : 0;
-    tok0 = pv.tok_off + tok_in;
-    kb = pv.k + tok_in * kRow;
-    vb = pv.v + tok_in * kRow;
+  // page records: window [win, win + 64) of the split's pages, and the next
+  typename LanesOf<Src>::type lanes = lane_pages(src, b, pg0, lane);
+  typename LanesOf<Src>::type lanes_next = lane_pages(src, b, pg0 + kRecWindow, lane);
+  int win = 0;
+  // the page (relative to pg0) and sub-block of the next block to be viewed
+  int cur_pi = 0, cur_sub = 0;
+
+  // The four blocks of a stage, viewed once, in order: valid tokens and HELM
+  // token cursor of each (uniform), and this wave's own block's K / V bases.
+  struct StageView {
+    int ntok[kChunkStage], tok0[kChunkStage];
+    int own_ntok;
+    const char *kb, *vb;
+  };
+  auto view_stage = [&](int st, StageView& sv) {
+#pragma unroll
+    for (int j = 0; j < kChunkStage; ++j) {
+      if (cur_pi - win >= kRecWindow) {   // uniform: the page lies in the next window
+        lanes = lanes_next;
+        win += kRecWindow;
+        lanes_next = lane_pages(src, b, pg0 + win + kRecWindow, lane);
+      }
+      const PageView pv = lane_page_view(src, lanes, b, pg0 + cur_pi, cur_pi - win, hk);
+      const int tok_in = cur_sub * kBlockTok;
+      const int nt = st * kChunkStage + j < nblk ? sclamp(pv.used - tok_in, 0, kBlockTok) : 0;
+      sv.ntok[j] = nt;
+      sv.tok0[j] = pv.tok_off + tok_in;
+      if (j == wave) {
+        sv.own_ntok = nt;
+        sv.kb = pv.k + tok_in * kRow;
+        sv.vb = pv.v + tok_in * kRow;
+      }
+      if (++cur_sub == bpp) {
+        cur_sub = 0;
+        ++cur_pi;
+      }
+    }
   };
 
   // additive mask of the lane's row for the four blocks of a stage (tokens
   // 4r + q4 of each block), loaded a stage ahead like the K/V chunks
   float mcur[kChunkStage][4], mnext[kChunkStage][4];
-  auto load_mask = [&](int st, float (&mk)[kChunkStage][4]) {
+  auto load_mask = [&](const StageView& sv, float (&mk)[kChunkStage][4]) {
     if constexpr (kMask) {
 #pragma unroll
       for (int j = 0; j < kChunkStage; ++j) {
-        int ntok, tok0;
-        const char *kb, *vb;
-        block_view(st * kChunkStage + j, ntok, tok0, kb, vb);
-        const int last = max(ntok - 1, 0);
+        const int last = max(sv.ntok[j] - 1, 0);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          mk[j][r] = ntok > 0 ? mrow[tok0 + min(4 * r + q4, last)] : 0.f;
+          mk[j][r] = sv.ntok[j] > 0 ? mrow[sv.tok0[j] + min(4 * r + q4, last)] : 0.f;
       }
     }
   };
@@ -559,12 +614,9 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
   // this wave's share of a stage: block (stage * 4 + wave), 4 chunks of K and
   // 4 of V per lane (chunk lane + 64 u of the block)
   mf_u32x4 gk[4], gv[4];
-  auto load_stage = [&](int st) {
-    int ntok, tok0;
-    const char *kb, *vb;
-    block_view(st * kChunkStage + wave, ntok, tok0, kb, vb);
-    const auto rk = make_rsrc(kb, ntok * kRow);
-    const auto rv = make_rsrc(vb, ntok * kRow);
+  auto load_stage = [&](const StageView& sv) {
+    const auto rk = make_rsrc(sv.kb, sv.own_ntok * kRow);
+    const auto rv = make_rsrc(sv.vb, sv.own_ntok * kRow);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       gk[u] = buf_load16_nt(rk, (lane + 64 * u) * 16);
@@ -583,24 +635,25 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
   };
 
   const int tau = 4 * (n & 3) + (n >> 2);   // K token of this lane in a block
+  StageView sv_cur, sv_next;
   if (nstage > 0) {
-    load_stage(0);
-    if (wave_rows) load_mask(0, mcur);
+    view_stage(0, sv_cur);
+    load_stage(sv_cur);
+    if (wave_rows) load_mask(sv_cur, mcur);
   }
   for (int st = 0; st < nstage; ++st) {
     const int buf = st & 1;
     store_stage(buf);
     if (st + 1 < nstage) {
-      load_stage(st + 1);
-      if (wave_rows) load_mask(st + 1, mnext);
+      view_stage(st + 1, sv_next);
+      load_stage(sv_next);
+      if (wave_rows) load_mask(sv_next, mnext);
     }
     __syncthreads();
     if (wave_rows) {
 #pragma unroll
       for (int j = 0; j < kChunkStage; ++j) {
-        int ntok, tok0;
-        const char *kb, *vb;
-        block_view(st * kChunkStage + j, ntok, tok0, kb, vb);
+        const int ntok = sv_cur.ntok[j];
         if (ntok == 0) continue;            // uniform: an empty or past-the-end block
         mf_u32x4 k[4], v[4];
 #pragma unroll
@@ -615,10 +668,11 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
 #pragma unroll
           for (int r = 0; r < 4; ++r) mk[r] = mcur[j][r];
         }
-        mfma_block_step<Ops, kMask, kCap, kCausal>(k, v, mk, ntok, tok0, qop, m, lsum, o, scale,
-                                                   cap, inv_cap, s_row, q4);
+        mfma_block_step<Ops, kMask, kCap, kCausal>(k, v, mk, ntok, sv_cur.tok0[j], qop, m, lsum,
+                                                   o, scale, cap, inv_cap, s_row, q4);
       }
     }
+    sv_cur = sv_next;
     if constexpr (kMask) {
 #pragma unroll
       for (int j = 0; j < kChunkStage; ++j)
@@ -627,10 +681,24 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
     }
   }
 
-  // each wave's own partial (m, l, o[128]) per row, straight from registers
   if (!wave_rows) return;
   float lrow = lsum + __shfl_xor(lsum, 16, 64);
   lrow += __shfl_xor(lrow, 32, 64);
+  if (p.direct_out) {
+    // the call's only split: normalized rows straight to the output
+    // (HELM's final out / max(sum, 1e-12), kv_cache.py:554-555)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float l = __shfl(lrow, 4 * q4 + r, 64);   // lane 4 q4 + r holds that row's sum
+      const float inv = 1.f / fmaxf(l, 1e-12f);
+      if (4 * q4 + r < nrows)
+        *reinterpret_cast<uint4*>(out_row(r)) =
+            make_uint4(Ops::pk(o[0][r] * inv, o[1][r] * inv), Ops::pk(o[2][r] * inv, o[3][r] * inv),
+                       Ops::pk(o[4][r] * inv, o[5][r] * inv), Ops::pk(o[6][r] * inv, o[7][r] * inv));
+    }
+    return;
+  }
+  // the wave's own partial (m, l, o[128]) per row, straight from registers
   const int64_t part = ((int64_t)tile * p.max_splits + split) * p.rows_per_tile;
   if (q4 == 0 && n < nrows)
     *reinterpret_cast<float2*>(&p.ws_ml[(part + n) * 2]) = make_float2(m, lrow);

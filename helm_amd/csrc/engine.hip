@@ -80,6 +80,7 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 struct Plan {
   int mfma, fast, nw, fused, gm, rows, epl, n_qtiles, bpp, pps, max_splits;
   int row_waves;  // matrix-core kernel: one 16-row tile per wave (query chunks)
+  int direct;     // row-wave plan with one split: output written by the split kernel
   // workgroups per (sequence, KV head) along the query rows
   int qblocks() const { return row_waves ? (n_qtiles + nw - 1) / nw : n_qtiles; }
   size_t ticket_bytes, count_bytes, ml_bytes, o_bytes;
@@ -140,6 +141,7 @@ void settle_fused(Plan& pl, int B, int Hkv) {
   const size_t tiles = (size_t)B * Hkv * pl.n_qtiles;
   if (pl.o_bytes >= 0x7ffffff0u || tiles * 4 > kTicketRegionBytes || pl.row_waves)
     pl.fused = 0;
+  pl.direct = (pl.row_waves && pl.max_splits == 1) ? 1 : 0;
 }
 
 // Rows, tiles and the split limits of a kernel choice.
@@ -163,7 +165,11 @@ void plan_shape(Plan& pl, int G, int q_len, int D, int max_tok_per_page) {
   if (pl.row_waves) pl.nw = kChunkStage;  // chunk_mfma_kernel: four waves, one tile each
 }
 
-int max_pps_of(const Plan& pl) { return pl.mfma ? kMfmaMaxPps : kMaxPps; }
+// chunk_mfma_kernel reads its page records in windows: a split may be long
+constexpr int kChunkMaxPps = 1 << 20;
+int max_pps_of(const Plan& pl) {
+  return pl.row_waves ? kChunkMaxPps : pl.mfma ? kMfmaMaxPps : kMaxPps;
+}
 constexpr int kRaggedPps = 48;
 int max_splits_of(const Plan& pl) { return pl.mfma ? kMfmaMaxSplits : kMaxSplits; }
 
@@ -191,8 +197,9 @@ int make_plan(Plan& pl, int kv_dtype, int q_dtype, int B, int Hq, int Hkv,
   int pps = pps_req > 0 ? pps_req : env_int("HELM_AMD_PPS", 0);
   if (pps <= 0) {
     const double units = (double)B * Hkv * pl.qblocks();
-    // one workgroup per CU: longer splits mean fewer partials to merge
-    const int target = env_int("HELM_AMD_WG_PER_CU", 1) * device_cus();
+    // one workgroup per CU (two for the chunk kernel, whose 64 KiB of LDS and
+    // 2 waves per SIMD let two share a CU): longer splits mean fewer partials
+    const int target = env_int("HELM_AMD_WG_PER_CU", pl.row_waves ? 2 : 1) * device_cus();
     const double splits = std::max(1.0, target / units);
     pps = (int)std::ceil(std::max(1.0, avg_pages) / splits);
     pps = std::max(pps, min_pps(pl.bpp, pl.nw));
@@ -201,7 +208,7 @@ int make_plan(Plan& pl, int kv_dtype, int q_dtype, int B, int Hq, int Hkv,
     // tail of the longest sequences' splits; shorter splits shorten it
     // (Qwen3-14B B8, 4k-32k: 146.6 us at 64 pages per split, 123.6 at 48;
     // equal-length batches are best at 64)
-    if (pl.mfma && B > 1 && max_pages > 1.5 * avg_pages && pps > kRaggedPps &&
+    if (pl.mfma && !pl.row_waves && B > 1 && max_pages > 1.5 * avg_pages && pps > kRaggedPps &&
         units * std::ceil(avg_pages / pps) > 2.0 * device_cus())
       pps = kRaggedPps;
   }
@@ -250,6 +257,7 @@ void fill_params(AttnParams& a, const Plan& pl, const void* q, void* out,
   a.rows_per_tile = pl.rows;
   a.n_qtiles = pl.n_qtiles;
   a.row_waves = pl.row_waves;
+  a.direct_out = pl.direct;
   a.scale = scale;
   a.softcap = softcap;
   a.mask = mask;
@@ -284,7 +292,7 @@ hipError_t dispatch(const LaunchSpec& s, hipStream_t st) {
 // Combines the split partials of every tile into the output (after the
 // split kernels, on the same stream).
 hipError_t launch_merge(const LaunchSpec& s, int B, int Hkv, hipStream_t st) {
-  if (s.p.fused) return hipSuccess;
+  if (s.p.fused || s.p.direct_out) return hipSuccess;
   // column groups: spread each row's partial reads over several CUs
   const int chunks = (s.p.D % 4 == 0) ? s.p.D / 4 : s.p.D;
   const int groups = std::max(1, std::min(env_int("HELM_AMD_MERGE_GROUPS", 1), chunks));

@@ -749,12 +749,18 @@ def _attend(query: torch.Tensor, seqs: Sequence[Sequence[_Segment]], Hkv: int, k
     seq_off = np.zeros(B + 1, dtype=np.int32)
     i = 0
     t_max = 0
+    # top-left causal: query row s sees keys 0..s, so keys from q_len on are
+    # masked for every row and their pages need not be read
+    limit = query.size(2) if causal else None
     for b, segs in enumerate(seqs):
         tok = 0
         for sg in segs:
-            arr[i] = (sg.k, sg.v, sg.used, tok, sg.head_stride,
+            if limit is not None and tok >= limit:
+                break
+            used = sg.used if limit is None else min(sg.used, limit - tok)
+            arr[i] = (sg.k, sg.v, used, tok, sg.head_stride,
                       _native.HELM_PAGE_HOST if sg.host else 0)
-            tok += sg.used
+            tok += used
             i += 1
         seq_off[b + 1] = i
         t_max = max(t_max, tok)
@@ -831,6 +837,13 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
                     dtype=np.uint64)
     npages = np.array([len(layer.pages) for layer in layers], dtype=np.int32)
     tokens = np.array(lens, dtype=np.int32)
+    if causal:
+        # top-left causal: keys from S on are masked for every row; the pages
+        # holding only such keys are left out (records are in token order)
+        for b, layer in enumerate(layers):
+            if tokens[b] > S:
+                tokens[b] = S
+                npages[b] = int(np.searchsorted(layer._rec["tok_off"][:npages[b]], S, "left"))
     page_tokens = max(layer._page_tokens for layer in layers)
     aligned = all(layer._aligned16 for layer in layers)
     _native.call("helm_paged_attn_seqs", eng, q.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,

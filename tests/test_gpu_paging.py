@@ -800,3 +800,44 @@ def test_layer_page_list_attention_matches_page_by_page(case, monkeypatch):
         assert (o[0].double() - ref).abs().max().item() <= 1e-2
     assert (outs[0].float() - outs[1].float()).abs().max().item() <= 1e-2
     mgr.clear()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("S,B,pps", [(1024, 1, None), (512, 2, 300), (256, 1, None)])
+def test_chunk_kernel_long_splits(dtype, S, B, pps, monkeypatch):
+    """Query chunks over 257 pages (last one partial) where a split spans more
+    than the 64 page records one lane window holds.  S = 1024: enough
+    workgroups that every (KV head, tile block) takes all pages in one split
+    and the chunk kernel writes the output itself; S = 512 with a second,
+    empty sequence and 300 pages per split: the same, with zeros for the
+    empty sequence; S = 256: four splits of 65 pages, merged.  All match the
+    fp64 oracle under an additive chunk mask (checked on two KV heads)."""
+    if pps is not None:
+        monkeypatch.setenv("HELM_AMD_PPS", str(pps))
+    Hq, kvh, D, P, T = 32, 8, 128, 16, 4100
+    G = Hq // kvh
+    tol = 1e-2 if dtype == torch.bfloat16 else 2e-3
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=dtype)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    g = torch.Generator().manual_seed(23)
+    k = torch.randn(1, kvh, T, D, generator=g).to(dtype)
+    v = torch.randn(1, kvh, T, D, generator=g).to(dtype)
+    mgr.append_prefill(0, k.to(DEV), v.to(DEV))
+    q = torch.randn(B, Hq, S, D, generator=g).to(dtype)
+    mask = torch.zeros(1, 1, S, T)
+    lim = T - S + torch.arange(S)
+    mask[0, 0][torch.arange(T)[None, :] > lim[:, None]] = float("-inf")
+    mask[..., 5::11] = -1.75
+    rec = mgr.layers[0].records()
+    n = len(rec)
+    seq_off = np.array([0] + [n] * B, dtype=np.int32)
+    out = KC._attend_records(q.to(DEV), rec, seq_off, T, kvh, dtype, 1 / math.sqrt(D),
+                             mask.to(DEV), None, False).cpu()
+    for hk in (0, kvh - 1):
+        hs = slice(hk * G, (hk + 1) * G)
+        ref = A.attention_fp64_batched(q[0, hs].float(), k[0, hk:hk + 1].float(),
+                                       v[0, hk:hk + 1].float(), mask=mask[0].double())
+        assert (out[0, hs].double() - ref).abs().max().item() <= tol
+    if B > 1:
+        assert torch.count_nonzero(out[1]).item() == 0
+    mgr.clear()
