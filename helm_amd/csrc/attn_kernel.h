@@ -408,6 +408,7 @@ struct AttnParams {
   int fused;          // 1: the last split of a tile merges in-kernel
   int row_waves;      // 1 (matrix-core kernel): each wave owns a 16-row tile
   int direct_out;     // 1: the call has one split; the chunk kernel writes the output
+  int bpp_log2;       // log2 of bpp when bpp is a power of two, else -1
 };
 
 // Per-workgroup LDS: per-wave online-softmax states of the tile's rows, and
@@ -1102,7 +1103,7 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
   // iteration issues the same loads and waits stay exact.
   auto load_block = [&](int bi, Blk& B) {
     const bool valid = bi < nblk;
-    const int pi = valid ? bi / p.bpp : 0;
+    const int pi = valid ? (p.bpp_log2 >= 0 ? bi >> p.bpp_log2 : bi / p.bpp) : 0;
     const int sub = valid ? bi - pi * p.bpp : 0;
     const PageView pv = src.page(b, pg0 + pi, hk);
     const int used = valid ? pv.used : 0;

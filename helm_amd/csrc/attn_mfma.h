@@ -272,13 +272,9 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
 
   const int split_local = blockIdx.x;
   const int hk = blockIdx.y % p.Hkv;
-  // row-wave mode (query chunks): wave w owns 16-row tile qblk * NW + w and
-  // walks every block of the split; otherwise the waves share one tile and
-  // split its blocks
-  const int qblk = blockIdx.y / p.Hkv;
-  const int qt_w = p.row_waves ? qblk * NW + wave : qblk;
-  const bool wave_rows = qt_w < p.n_qtiles;
-  const int qt = wave_rows ? qt_w : p.n_qtiles - 1;
+  // the waves share one 16-row tile and split its blocks (query chunks with
+  // more tiles run in chunk_mfma_kernel)
+  const int qt = blockIdx.y / p.Hkv;
   const int b = blockIdx.z;
   const int tile = (b * p.Hkv + hk) * p.n_qtiles + qt;
   const int S = p.S;
@@ -316,8 +312,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   // split 0 publishes the tile's split count; a tile without pages gets
   // zeros (HELM kv_cache.py:441-442): from split 0 in fused mode, from
   // merge_splits_kernel otherwise
-  if (split_local == 0 && (p.row_waves ? (lane == 0 && wave_rows) : tid == 0))
-    p.counts[tile] = total;
+  if (split_local == 0 && tid == 0) p.counts[tile] = total;
   const bool active = total > 0 && split_local < nsplit_launch;
   if (!active) {
     if (total == 0 && p.fused && split_local == 0) {
@@ -351,7 +346,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   for (int e = 0; e < 8; ++e) o[e] = mf_f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int bpp = p.bpp;
-  const int nblk = wave_rows ? npg * bpp : 0;
+  const int nblk = npg * bpp;
   // lane offsets inside a block: K token tau(n) at chunk q4 (+64 B per i),
   // V token q4 at dims 8n (+1 KiB per j)
   const int voff_k = (4 * (n & 3) + (n >> 2)) * kRow + 16 * q4;
@@ -367,7 +362,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
 
   auto load_block = [&](int bi, Blk& B) {
     const bool valid = bi < nblk;
-    const int pi = valid ? bi / bpp : 0;
+    const int pi = valid ? (p.bpp_log2 >= 0 ? bi >> p.bpp_log2 : bi / bpp) : 0;
     const int sub = valid ? bi - pi * bpp : 0;
     const PageView pv = lane_page_view(src, lanes, b, pg0 + pi, pi, hk);
     const int tok_in = sub * kBlockTok;
@@ -398,40 +393,19 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   // blocks' loads in flight while one block is computed ----------------------
   {
     constexpr int NB = kMfmaBufs;
-    const int W = p.row_waves ? 1 : NW;     // block stride of this wave
-    const int w0 = p.row_waves ? 0 : wave;  // its first block
-    const int nmine = nblk > w0 ? (nblk - w0 + W - 1) / W : 0;
+    // this wave's blocks: wave, wave + NW, ...
+    const int nmine = nblk > wave ? (nblk - wave + NW - 1) / NW : 0;
     Blk buf[NB];
 #pragma unroll
-    for (int i = 0; i < NB - 1; ++i) load_block(w0 + i * W, buf[i]);
+    for (int i = 0; i < NB - 1; ++i) load_block(wave + i * NW, buf[i]);
     for (int k = 0; k < nmine; k += NB) {
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
         if (k + u >= nmine) break;
-        load_block(w0 + (k + u + NB - 1) * W, buf[(u + NB - 1) % NB]);
+        load_block(wave + (k + u + NB - 1) * NW, buf[(u + NB - 1) % NB]);
         compute_block(buf[u]);
       }
     }
-  }
-
-  if (p.row_waves) {
-    // each wave's own partial (m, l, o[128]) per row, straight from registers
-    if (!wave_rows) return;
-    float lrow = lsum + __shfl_xor(lsum, 16, 64);
-    lrow += __shfl_xor(lrow, 32, 64);
-    const int64_t part = ((int64_t)tile * p.max_splits + split) * p.rows_per_tile;
-    if (q4 == 0 && n < nrows)
-      *reinterpret_cast<float2*>(&p.ws_ml[(part + n) * 2]) = make_float2(m, lrow);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 4 * q4 + r;
-      if (row < nrows) {
-        float* dst = &p.ws_o[(part + row) * 128 + 8 * n];
-        *reinterpret_cast<float4*>(dst) = make_float4(o[0][r], o[1][r], o[2][r], o[3][r]);
-        *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4][r], o[5][r], o[6][r], o[7][r]);
-      }
-    }
-    return;
   }
 
   // ---- per-wave state to LDS ---------------------------------------------------

@@ -267,6 +267,9 @@ void fill_params(AttnParams& a, const Plan& pl, const void* q, void* out,
   a.causal = causal;
   a.pps = pl.pps;
   a.bpp = pl.bpp;
+  a.bpp_log2 = -1;
+  for (int k = 0; k < 31; ++k)
+    if (pl.bpp == (1 << k)) a.bpp_log2 = k;
   a.lo = 0;
   a.hi = 0x7fffffff;
   a.split_base = 0;
