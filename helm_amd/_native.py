@@ -64,6 +64,10 @@ SIGNATURES = {
                                                 _c_void_p]),
     "helm_page_append": (ctypes.c_int, [_c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, _c_void_p]),
+    "helm_decode_front": (ctypes.c_int, [
+        _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, ctypes.c_int, _f32,
+        _c_void_p, _c_void_p, _i64, ctypes.c_int, _c_void_p, _c_void_p, ctypes.c_int,
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
     "helm_evict_pages": (ctypes.c_int, [_c_void_p, ctypes.c_int, _c_void_p, _c_void_p,
                                         _c_void_p, ctypes.c_int, _c_void_p]),
     "helm_prefetch_pages": (ctypes.c_int, [_c_void_p, ctypes.c_int, _c_void_p, _c_void_p,

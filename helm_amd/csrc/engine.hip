@@ -13,6 +13,7 @@
 
 #include "attn_kernel.h"
 #include "attn_mfma.h"
+#include "front.h"
 #include "helm_amd.h"
 
 namespace helm {
@@ -1200,6 +1201,76 @@ int helm_page_append(const helm_append_seg* segs, int n_segs, int Hkv, int D,
     for (int i = 0; i < a.n_seg; ++i) a.seg[i] = segs[base + i];
     hipLaunchKernelGGL(page_append_kernel, dim3(a.n_seg, Hkv), dim3(256), 0,
                        st, a);
+    HELM_HIP(hipGetLastError());
+  }
+  return HELM_OK;
+}
+
+int helm_decode_front(const void* q_proj, const void* k_proj, const void* v_proj,
+                      int64_t q_stride, int64_t kv_stride, const void* q_norm_w,
+                      const void* k_norm_w, int norm_mode, float eps, const void* cos,
+                      const void* sin, int64_t cs_stride, int cs_dtype, void* q_out,
+                      const helm_append_seg* dst, int B, int Hq, int Hkv, int D, int dtype,
+                      void* stream) {
+  const int eb = elem_bytes(dtype);
+  if (!eb) return fail(HELM_E_INVALID, "unknown dtype");
+  if (cs_dtype != dtype && cs_dtype != HELM_F32)
+    return fail(HELM_E_UNSUPPORTED, "cos / sin must have the projection dtype or float32");
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || D < 2 || D % 2 != 0 || D > kFrontMaxD)
+    return fail(HELM_E_INVALID, "bad decode front shape (D even, at most 256)");
+  if (norm_mode < 0 || norm_mode > 2) return fail(HELM_E_INVALID, "norm_mode must be 0, 1 or 2");
+  if (B == 0) return HELM_OK;
+  if (!q_proj || !k_proj || !v_proj || !cos || !sin || !q_out || !dst ||
+      (norm_mode && (!q_norm_w || !k_norm_w)))
+    return fail(HELM_E_INVALID, "null pointer argument");
+  if (q_stride < (int64_t)Hq * D || kv_stride < (int64_t)Hkv * D || cs_stride < 0)
+    return fail(HELM_E_INVALID, "projection rows overlap");
+  for (int b = 0; b < B; ++b)
+    if (!dst[b].dst_k || !dst[b].dst_v || dst[b].dst_tok < 0 ||
+        dst[b].dst_head_stride < (dst[b].dst_tok + 1) * D)
+      return fail(HELM_E_INVALID, "bad destination " + std::to_string(b));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  for (int b0 = 0; b0 < B; b0 += kFrontMaxSeqs) {
+    FrontArgs a{};
+    const int nb = std::min(kFrontMaxSeqs, B - b0);
+    a.q = static_cast<const char*>(q_proj);
+    a.k = static_cast<const char*>(k_proj);
+    a.v = static_cast<const char*>(v_proj);
+    a.q_stride = q_stride;
+    a.kv_stride = kv_stride;
+    a.qw = static_cast<const char*>(q_norm_w);
+    a.kw = static_cast<const char*>(k_norm_w);
+    a.eps = eps;
+    a.norm = norm_mode;
+    a.cos = static_cast<const char*>(cos);
+    a.sin = static_cast<const char*>(sin);
+    a.cs_stride = cs_stride;
+    a.q_out = static_cast<char*>(q_out);
+    a.b0 = b0;
+    a.Hq = Hq;
+    a.Hkv = Hkv;
+    a.D = D;
+    for (int i = 0; i < nb; ++i) {
+      a.dst_k[i] = dst[b0 + i].dst_k;
+      a.dst_v[i] = dst[b0 + i].dst_v;
+      a.dst_head_stride[i] = dst[b0 + i].dst_head_stride;
+      a.dst_tok[i] = dst[b0 + i].dst_tok;
+    }
+    const dim3 grid(nb, Hq + Hkv);
+    const bool c32 = cs_dtype == HELM_F32;
+    switch (dtype) {
+      case HELM_BF16:
+        if (c32) hipLaunchKernelGGL((decode_front_kernel<bf16_t, float>), grid, dim3(64), 0, st, a);
+        else hipLaunchKernelGGL((decode_front_kernel<bf16_t, bf16_t>), grid, dim3(64), 0, st, a);
+        break;
+      case HELM_F16:
+        if (c32) hipLaunchKernelGGL((decode_front_kernel<f16_t, float>), grid, dim3(64), 0, st, a);
+        else hipLaunchKernelGGL((decode_front_kernel<f16_t, f16_t>), grid, dim3(64), 0, st, a);
+        break;
+      default:
+        hipLaunchKernelGGL((decode_front_kernel<float, float>), grid, dim3(64), 0, st, a);
+        break;
+    }
     HELM_HIP(hipGetLastError());
   }
   return HELM_OK;

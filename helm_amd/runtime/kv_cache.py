@@ -499,8 +499,14 @@ class KVCacheManager:
             self._enforce_residency_policy()
 
     def _append_decode_deferred(self, layer_id: int, K_new: torch.Tensor, V_new: torch.Tensor):
+        page, tok = self._decode_slot(layer_id, K_new.device)
+        _write_tokens(self._appends, page, tok, K_new, V_new)
+
+    def _decode_slot(self, layer_id: int, device: torch.device):
+        """The page and token index of one decoded token, with append_decode's
+        bookkeeping (a new page when the tail is missing or full, used and
+        total counts, kv_cache.py:145-171); the caller writes the token."""
         layer = self._layer(layer_id)
-        device = K_new.device
         if layer.tail_page is None or layer.tail_page.used_tokens == layer.tail_page.capacity_tokens:
             page = self.allocator.allocate(device)
             page.layer_id = layer_id
@@ -508,10 +514,11 @@ class KVCacheManager:
             page.used_tokens = 0
             self._add_page(layer, page)
         page = layer.tail_page
-        _write_tokens(self._appends, page, page.used_tokens, K_new, V_new)
+        tok = page.used_tokens
         page.used_tokens += 1
         layer.total_tokens += 1
         layer._tail_filled()
+        return page, tok
 
     def iterate_layer_pages(self, layer_id: int):
         if layer_id not in self.layers:

@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import importlib
 import math
+import os
 from dataclasses import dataclass
 from types import MethodType
 from typing import Optional
@@ -25,6 +26,8 @@ from typing import Optional
 import numpy as np
 import torch
 
+from helm_amd import _native
+from helm_amd.runtime import engine as _engine
 from helm_amd.runtime.kv_allocator import KVAllocator
 from helm_amd.runtime.kv_cache import (KVCacheManager, _async_kv_prefetch_enabled, _attend,
                                        _attend_layers, _attend_records, _contiguous_segments,
@@ -108,7 +111,15 @@ def _decode_batched(kvcms, q, k, v, layer_idx: int, scale: float,
         kvcms[i]._append_decode_deferred(layer_idx, k[i:i + 1], v[i:i + 1])
         kvcms[i]._enforce_residency_policy()
     _flush_appends([kvcm._appends for kvcm in kvcms])
+    return _decode_attend(kvcms, q, layer_idx, Hkv, scale, attention_mask)
 
+
+def _decode_attend(kvcms, q, layer_idx: int, Hkv: int, scale: float,
+                   attention_mask: Optional[torch.Tensor]):
+    """The attention of a decode step once every item's token is in its pages:
+    from the layers' records, else HELM's batched or per-item page-list path
+    (kv_offload.py:116-186)."""
+    bsz, D = q.shape[0], q.shape[-1]
     out = _decode_from_records(kvcms, q, layer_idx, Hkv, D, scale, attention_mask)
     if out is not None:
         return out
@@ -407,27 +418,123 @@ def _gemma2_decode_from_records(attn_self, kvcms, q, layer: int, scale: float, s
                                 scale, mask, softcap)
 
 
+_FRONT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+_FRONT_NORMS = {"head": ("Qwen3RMSNorm", 1), "proj": ("Olmo2RMSNorm", 2)}
+
+
+def _front_norm(attn_self, arch: _Arch, dtype, Hq: int, Hkv: int, D: int):
+    """(mode, q weight, k weight, eps) of the forward's q / k norm as
+    helm_decode_front computes it, or None for a norm it does not reproduce."""
+    if arch.qk_norm == "none":
+        return 0, None, None, 0.0
+    name, mode = _FRONT_NORMS[arch.qk_norm]
+    qn, kn = getattr(attn_self, "q_norm", None), getattr(attn_self, "k_norm", None)
+    if type(qn).__name__ != name or type(kn).__name__ != name:
+        return None
+    qw, kw = qn.weight, kn.weight
+    want = (D, D) if mode == 1 else (Hq * D, Hkv * D)
+    if (qw.dtype != dtype or kw.dtype != dtype or (qw.numel(), kw.numel()) != want
+            or not qw.is_contiguous() or not kw.is_contiguous()
+            or qn.variance_epsilon != kn.variance_epsilon):
+        return None
+    return mode, qw, kw, float(qn.variance_epsilon)
+
+
+def _page_dst_ok(page, device, dtype, Hkv: int, D: int) -> bool:
+    k, v = page.k_tensor, page.v_tensor
+    return (k.device == device and v.device == device and k.dtype == dtype and v.dtype == dtype
+            and k.dim() == 4 and k.shape[:2] == (1, Hkv) and k.size(3) == D
+            and v.shape == k.shape and k.stride(3) == 1 and v.stride(3) == 1
+            and k.stride(2) == D and v.stride(2) == D and k.stride(1) == v.stride(1))
+
+
+def _decode_front(kvcms, attn_self, arch: _Arch, qp, kp, vp, cos, sin, layer: int):
+    """The decode front end in one helm_decode_front launch: q / k norm,
+    rotary embedding, and each item's token written into its pages (then
+    the residency policy per item, as append_decode does).  Returns q
+    [B, Hq, 1, D], or None when the forward's torch ops must run instead."""
+    if os.environ.get("HELM_AMD_FRONT", "1") == "0":
+        return None
+    bsz = qp.shape[0]
+    D = attn_self.head_dim
+    dtype, device = qp.dtype, qp.device
+    if (device.type != "cuda" or dtype not in _FRONT_DTYPES or len(kvcms) < bsz
+            or any(getattr(c, "use_contiguous", False) for c in kvcms[:bsz])
+            or (torch.is_grad_enabled() and (qp.requires_grad or kp.requires_grad))):
+        return None
+    if (qp.dim() != 3 or qp.size(1) != 1 or kp.shape != vp.shape or kp.dtype != dtype
+            or vp.dtype != dtype or qp.size(2) % D or kp.size(2) % D or D % 2 or D > 256
+            or qp.stride(2) != 1 or kp.stride(2) != 1 or vp.stride(2) != 1
+            or kp.stride(0) != vp.stride(0)):
+        return None
+    Hq, Hkv = qp.size(2) // D, kp.size(2) // D
+    if (Hq % Hkv or cos.dim() != 3 or cos.shape != sin.shape or cos.shape[1:] != (1, D)
+            or cos.size(0) not in (1, bsz) or cos.dtype != sin.dtype
+            or cos.dtype not in (dtype, torch.float32) or cos.stride(2) != 1
+            or cos.stride() != sin.stride() or cos.device != device):
+        return None
+    norm = _front_norm(attn_self, arch, dtype, Hq, Hkv, D)
+    if norm is None:
+        return None
+    for c in kvcms[:bsz]:
+        lc = c.layers.get(layer)
+        tail = lc.tail_page if lc is not None else None
+        if (tail is not None and tail.used_tokens < tail.capacity_tokens
+                and not _page_dst_ok(tail, device, dtype, Hkv, D)):
+            return None
+    # the destination of each item's token (bookkeeping as append_decode's)
+    dst = np.zeros(bsz, dtype=_native.APPEND_DTYPE)
+    for i in range(bsz):
+        page, tok = kvcms[i]._decode_slot(layer, device)
+        if not _page_dst_ok(page, device, dtype, Hkv, D):
+            raise RuntimeError("decode front end: the tail page of layer %d is not a dense "
+                               "[1, Hkv, P, D] device page" % layer)
+        dst[i]["dst_k"] = page.k_tensor.data_ptr()
+        dst[i]["dst_v"] = page.v_tensor.data_ptr()
+        dst[i]["dst_head_stride"] = page.k_tensor.stride(1)
+        dst[i]["dst_tok"] = tok
+    mode, qw, kw, eps = norm
+    q_out = torch.empty(bsz, Hq, 1, D, dtype=dtype, device=device)
+    _native.call("helm_decode_front", qp.data_ptr(), kp.data_ptr(), vp.data_ptr(),
+                 qp.stride(0), kp.stride(0), qw.data_ptr() if qw is not None else None,
+                 kw.data_ptr() if kw is not None else None, mode, eps, cos.data_ptr(),
+                 sin.data_ptr(), cos.stride(0) if cos.size(0) > 1 else 0,
+                 _native.dtype_code(cos.dtype), q_out.data_ptr(), _native.ptr(dst), bsz, Hq,
+                 Hkv, D, _native.dtype_code(dtype), _engine.stream_ptr(device))
+    for i in range(bsz):
+        kvcms[i]._enforce_residency_policy()
+    return q_out
+
+
+def _gemma2_decode_attend(attn_self, kvcms, q, layer: int, scale: float, softcap,
+                          attention_mask, cache_position):
+    """Gemma-2 decode attention once every item's token is in its pages:
+    one call over the layers' records with per-item sliding-window masks,
+    else per-item streaming attention (kv_offload.py:577-613)."""
+    out = _gemma2_decode_from_records(attn_self, kvcms, q, layer, scale, softcap,
+                                      attention_mask, cache_position)
+    if out is not None:
+        return out
+    outs = []
+    for i in range(q.shape[0]):
+        pages = kvcms[i].iterate_layer_pages(layer)
+        key_length = sum(p.used_tokens for p in pages if p.used_tokens > 0 and p.state != "DEAD")
+        item_mask = (_gemma2_sliding_window_mask(
+            attn_self, attention_mask[i:i + 1] if attention_mask is not None else None,
+            cache_position, key_length, device=q.device, dtype=q.dtype)
+            if key_length > 0 else None)
+        outs.append(perform_streaming_attention(q[i:i + 1], pages, scale=scale,
+                                                attention_mask=item_mask, softcap=softcap))
+    return torch.cat(outs, dim=0)
+
+
 def _make_forward(kvcms, arch: _Arch):
     """Attention forward for `arch` bound to the per-item caches `kvcms`."""
 
     def forward(attn_self, hidden_states, position_embeddings, attention_mask=None,
                 past_key_values=None, cache_position=None, **kwargs):
-        rope = importlib.import_module(arch.rope_module).apply_rotary_pos_emb
         bsz, q_len, _ = hidden_states.shape
         shape = (bsz, q_len, -1, attn_self.head_dim)
-
-        q = attn_self.q_proj(hidden_states)
-        k = attn_self.k_proj(hidden_states)
-        v = attn_self.v_proj(hidden_states)
-        if arch.qk_norm == "proj":
-            q, k = attn_self.q_norm(q), attn_self.k_norm(k)
-        q, k, v = q.view(shape), k.view(shape), v.view(shape)
-        if arch.qk_norm == "head":
-            q, k = attn_self.q_norm(q), attn_self.k_norm(k)
-        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
-        cos, sin = position_embeddings
-        q, k = rope(q, k, cos, sin)
-
         if arch.gemma:
             scale = getattr(attn_self, "scaling", 1.0 / math.sqrt(attn_self.head_dim))
             softcap = getattr(attn_self, "attn_logit_softcapping", None)
@@ -435,6 +542,32 @@ def _make_forward(kvcms, arch: _Arch):
             scale = 1.0 / math.sqrt(attn_self.head_dim)
             softcap = None
         layer = attn_self.layer_idx
+        cos, sin = position_embeddings
+
+        q = attn_self.q_proj(hidden_states)
+        k = attn_self.k_proj(hidden_states)
+        v = attn_self.v_proj(hidden_states)
+        if q_len == 1:
+            # norm + rotary + page write in one launch where the kernel can
+            qf = _decode_front(kvcms, attn_self, arch, q, k, v, cos, sin, layer)
+            if qf is not None:
+                if arch.gemma:
+                    out = _gemma2_decode_attend(attn_self, kvcms, qf, layer, scale, softcap,
+                                                attention_mask, cache_position)
+                else:
+                    out = _decode_attend(kvcms, qf, layer, k.size(2) // attn_self.head_dim,
+                                         scale, attention_mask)
+                out = out.transpose(1, 2).contiguous().reshape(bsz, q_len, -1)
+                return attn_self.o_proj(out), None
+
+        rope = importlib.import_module(arch.rope_module).apply_rotary_pos_emb
+        if arch.qk_norm == "proj":
+            q, k = attn_self.q_norm(q), attn_self.k_norm(k)
+        q, k, v = q.view(shape), k.view(shape), v.view(shape)
+        if arch.qk_norm == "head":
+            q, k = attn_self.q_norm(q), attn_self.k_norm(k)
+        q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+        q, k = rope(q, k, cos, sin)
 
         if q_len > 1:
             past_lengths = _append_prefill_batched(kvcms, k, v, layer)
@@ -456,22 +589,8 @@ def _make_forward(kvcms, arch: _Arch):
                 kvcms[i]._append_decode_deferred(layer, k[i:i + 1], v[i:i + 1])
                 kvcms[i]._enforce_residency_policy()
             _flush_appends([c._appends for c in kvcms])
-            out = _gemma2_decode_from_records(attn_self, kvcms, q, layer, scale, softcap,
-                                              attention_mask, cache_position)
-            if out is None:
-                outs = []
-                for i in range(bsz):
-                    pages = kvcms[i].iterate_layer_pages(layer)
-                    key_length = sum(p.used_tokens for p in pages
-                                     if p.used_tokens > 0 and p.state != "DEAD")
-                    item_mask = (_gemma2_sliding_window_mask(
-                        attn_self, attention_mask[i:i + 1] if attention_mask is not None else None,
-                        cache_position, key_length, device=q.device, dtype=q.dtype)
-                        if key_length > 0 else None)
-                    outs.append(perform_streaming_attention(q[i:i + 1], pages, scale=scale,
-                                                            attention_mask=item_mask,
-                                                            softcap=softcap))
-                out = torch.cat(outs, dim=0)
+            out = _gemma2_decode_attend(attn_self, kvcms, q, layer, scale, softcap,
+                                        attention_mask, cache_position)
         else:
             out = _decode_batched(kvcms, q, k, v, layer, scale, attention_mask)
 

@@ -212,6 +212,28 @@ int helm_host_pages_in_place(helm_engine* eng, const helm_page* pages, int n,
 int helm_page_append(const helm_append_seg* segs, int n_segs, int Hkv, int D,
                      int dtype, void* stream);
 
+/* Decode front end, one launch for B sequences of one token each.  Row b of
+ * q_proj / k_proj / v_proj (q_stride / kv_stride elements apart, heads of D
+ * contiguous elements) gets, per head: RMSNorm with weights q_norm_w /
+ * k_norm_w and epsilon eps (norm_mode 1: per head, D weights, rounded before
+ * the weight multiply like Qwen3RMSNorm; 2: over the whole row, Hq*D or
+ * Hkv*D weights, rounded after it like Olmo2RMSNorm; 0: none), then the
+ * rotary embedding x*cos + rotate_half(x)*sin with cos / sin rows of D
+ * elements cs_stride apart (cs_dtype: dtype, every op rounded to dtype as
+ * eager torch does, or HELM_F32, computed in fp32 and rounded once).  q goes
+ * to q_out [B, Hq, D]; k and v (v unchanged) go to token dst[b].dst_tok of the
+ * page at dst[b].dst_k / dst_v (heads dst_head_stride elements apart; the
+ * src_* and n_tok fields are unused).  D even, <= 256.  Replaces the q_norm /
+ * k_norm / apply_rotary_pos_emb steps and the append_decode copy of the
+ * patched attention forwards (helm/runtime/kv_offload.py:365-373,
+ * helm/runtime/kv_cache.py:145-171). */
+int helm_decode_front(const void* q_proj, const void* k_proj, const void* v_proj,
+                      int64_t q_stride, int64_t kv_stride, const void* q_norm_w,
+                      const void* k_norm_w, int norm_mode, float eps, const void* cos,
+                      const void* sin, int64_t cs_stride, int cs_dtype, void* q_out,
+                      const helm_append_seg* dst, int B, int Hq, int Hkv, int D, int dtype,
+                      void* stream);
+
 /* Eviction copies: n regions of bytes[i] from device src[i] to pinned host
  * dst[i], issued with hipMemcpyAsync on `stream` after everything already
  * queued there; regions adjacent on both sides are merged into one copy.
