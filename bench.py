@@ -17,7 +17,10 @@ Also measured (extra keys of the one JSON line):
 * the full 40-layer Qwen3-14B decode step (batch 4 x 65,536 tokens, per layer
   token append + residency policy + attention through the runtime API), with
   the 64 GB device KV budget (nothing evicted) and with a 32 GB budget that
-  keeps about 25% of the pages in pinned host RAM.
+  keeps about 25% of the pages in pinned host RAM;
+* a prefill chunk: 512 query tokens over 32,768 cached tokens of one
+  Qwen3-8B-shaped layer under the chunk-causal mask, through the runtime's
+  prefill path (TFLOP/s against the matrix cores' dense bf16 peak).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -58,6 +61,7 @@ def parse():
     ap.add_argument("--pps", type=int, default=0, help="pages per split (0 = auto)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (PMC byte-count calibration)")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-chunk leg")
     ap.add_argument("--no-full-step", action="store_true",
                     help="skip the 40-layer Qwen3-14B B4 x 64k decode step (64 GB device KV "
                          "budget, and a 32 GB budget that forces eviction)")
@@ -311,6 +315,54 @@ def gpu_full_step(args, torch, W, budget_gb, steps, name="qwen3-14b-40l-b4-64k",
     return res
 
 
+def gpu_prefill(args, torch, T=32768, S=512, reps=20, seed=6):
+    """A prefill chunk through the runtime: Qwen3-8B attention shape (32 query /
+    8 KV heads, head_dim 128, bf16, pages of 16), an S-token chunk attending
+    over the T tokens of its layer's pages (the chunk's own K/V appended last)
+    under the additive chunk-causal mask HELM's pipeline passes
+    (pipeline_runtime.py:94-113), via ``_stream_prefill_batched``
+    (kv_offload.py:207-227).  Roofline: the matrix cores (4 Hq S T D flops)."""
+    from helm_amd.runtime.kv_allocator import KVAllocator
+    from helm_amd.runtime.kv_cache import KVCacheManager
+    from helm_amd.runtime.kv_offload import _stream_prefill_batched
+    from oracle.attention import attention_fp64_batched
+    Hq, Hkv, D, P = 32, 8, 128, 16
+    dev = torch.device("cuda:0")
+    a = KVAllocator(1, Hkv, D, page_size=P, dtype=torch.bfloat16)
+    m = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 13)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    k = torch.randn(1, Hkv, T, D, generator=g, device=dev).bfloat16()
+    v = torch.randn(1, Hkv, T, D, generator=g, device=dev).bfloat16()
+    m.append_prefill(0, k, v)
+    q = torch.randn(1, Hq, S, D, generator=g, device=dev).bfloat16()
+    mask = torch.zeros(1, 1, S, T, device=dev)
+    lim = T - S + torch.arange(S, device=dev)
+    mask[0, 0][torch.arange(T, device=dev)[None, :] > lim[:, None]] = torch.finfo(torch.float32).min
+    scale = 1.0 / math.sqrt(D)
+    run = lambda: _stream_prefill_batched([m], q, 0, scale, attention_mask=mask)
+    out = run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        out = run()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    flops = 4.0 * Hq * S * T * D
+    # spot check: KV head 0's four query heads at 64 chunk positions
+    rows = torch.arange(0, S, S // 64)
+    ref = attention_fp64_batched(q[0, :4, rows].cpu(), k[0, :1].cpu(), v[0, :1].cpu(),
+                                 mask=mask[0, :, rows].double().cpu())
+    err = (out[0, :4, rows].double().cpu() - ref).abs().max().item()
+    res = {"workload": f"qwen3-8b attention shape, 1 layer: {S}-token chunk over {T} cached "
+                       f"tokens (pages of {P}), bf16, additive chunk-causal mask [1,1,{S},{T}]",
+           "ms_per_call": dt * 1e3, "TFLOPs": flops / dt / 1e12,
+           "mfma_peak_TFLOPs": 2500.0, "frac_of_peak": flops / dt / 1e12 / 2500.0,
+           "calls": reps, "max_abs_err_vs_fp64": err}
+    del m, a, k, v, q, mask, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def all_configs(args, torch, W, paged):
     """Every decode-attention configuration of the benchmark set, one line
     each on stderr and all of them in gpurun_out/bench_all.json."""
@@ -410,6 +462,12 @@ def main():
             log(json.dumps(r))
             full[label] = r
 
+    pre = None
+    if not args.no_prefill:
+        log("prefill chunk: qwen3-8b shape, 512 tokens over 32k cached, chunk mask")
+        pre = gpu_prefill(args, torch)
+        log(f"prefill {pre['ms_per_call']:.3f} ms/call, {pre['TFLOPs']:.1f} TFLOP/s")
+
     off = None
     if not args.no_offload:
         log("offload: qwen3-8b-32k, oldest 50% in pinned host")
@@ -429,6 +487,13 @@ def main():
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
+    # the rocprofv3 kernel durations of the same call (decode + merge kernels),
+    # from the committed profile: the live call time above should agree
+    prof = None
+    ppath = os.path.join(ROOT, "profiles", "paged_decode_qwen3-8b-32k_kernel_times.json")
+    if os.path.exists(ppath):
+        with open(ppath) as f:
+            prof = json.load(f)
 
     line = {
         "metric": METRIC,
@@ -453,9 +518,13 @@ def main():
                      "traffic": traffic,
                      "alg_bytes_per_launch": h["alg_bytes"],
                      "avg_launch_us": round(h["per_call_s"] * 1e6, 3),
+                     "launch": "one helm_paged_decode_attn call = decode_mfma_kernel + "
+                               "merge_splits_d128_kernel, timed with HIP events on its stream",
+                     "rocprof_kernel_us": prof,
                      "host_issue_us_per_call": round(h["host_issue_us_per_call"], 2)},
         "offload50": off,
         "full_step_40l": full,
+        "prefill_chunk": pre,
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["path2_concat_sdpa"]["GBs"], 3), "unit": "GB/s",
             "cores": threads, "kind": "port",
