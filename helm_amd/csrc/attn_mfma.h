@@ -185,17 +185,21 @@ __device__ __forceinline__ PageView lane_page_view(const DescSrc& s, const DescL
 // lane's row for tokens 4r + q4, ntok the block's valid tokens, tok0 the
 // HELM token cursor of its first token.  Updates the row max m, this lane's
 // share of the row sum, and O (rows 4 q4 + r, dims 8n + e).
-template <class Ops, bool kMask, bool kCap, bool kCausal>
-__device__ __forceinline__ void mfma_block_step(const mf_u32x4 (&k)[4], const mf_u32x4 (&v)[4],
-                                                const float (&mk)[4], int ntok, int tok0,
-                                                const mf_u32x4 (&qop)[4], float& m, float& lsum,
-                                                mf_f32x4 (&o)[8], float scale, float cap,
-                                                float inv_cap, int s_row, int q4) {
-  // scores of row n for tokens 4r + q4
+// q . k of the lane's row n for tokens 4r + q4 of a block (K operand k).
+template <class Ops>
+__device__ __forceinline__ mf_f32x4 mfma_qk(const mf_u32x4 (&k)[4], const mf_u32x4 (&qop)[4]) {
   mf_f32x4 sc = mf_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < 4; ++i) sc = Ops::mma(k[i], qop[i], sc);
-  float x[4];
+  return sc;
+}
+
+// Logits of those four tokens: scale, soft-cap, additive mask, causal limit,
+// and -inf past the block's ntok valid tokens.
+template <bool kMask, bool kCap, bool kCausal>
+__device__ __forceinline__ void mfma_logits(mf_f32x4 sc, const float (&mk)[4], int ntok, int tok0,
+                                            float scale, float cap, float inv_cap, int s_row,
+                                            int q4, float (&x)[4]) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     float val = sc[r] * scale;
@@ -210,7 +214,13 @@ __device__ __forceinline__ void mfma_block_step(const mf_u32x4 (&k)[4], const mf
     for (int r = 0; r < 4; ++r)
       if (4 * r + q4 >= ntok) x[r] = -INFINITY;
   }
-  const float bm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+}
+
+// The lazy online-softmax reference update for a block max bm: when bm
+// exceeds the row max by more than the slack anywhere in the wave, the row
+// max is refreshed and l and the O rows rescaled.
+__device__ __forceinline__ void mfma_refresh_max(float bm, float& m, float& lsum,
+                                                 mf_f32x4 (&o)[8], int q4) {
   if (__builtin_amdgcn_ballot_w64(bm > m + kMfmaSlack)) {
     // refresh the row max (uniform across the row's four lanes)
     float rm = fmaxf(bm, __shfl_xor(bm, 16, 64));
@@ -227,6 +237,13 @@ __device__ __forceinline__ void mfma_block_step(const mf_u32x4 (&k)[4], const mf
       for (int e = 0; e < 8; ++e) o[e][r] *= ar;
     }
   }
+}
+
+// Weights exp(x - m) of the four tokens into l and, as hi + lo 16-bit parts,
+// P . V into O (V operand v: tokens q4 + 4j at dims 8n .. 8n + 7).
+template <class Ops>
+__device__ __forceinline__ void mfma_pv(const float (&x)[4], const mf_u32x4 (&v)[4], float m,
+                                        float& lsum, mf_f32x4 (&o)[8]) {
   const float base = (m == -INFINITY) ? 0.f : m;
   float wt[4];
 #pragma unroll
@@ -247,6 +264,20 @@ __device__ __forceinline__ void mfma_block_step(const mf_u32x4 (&k)[4], const mf
     o[2 * w] = Ops::mma(pop, mf_u32x4{a01, a23, a01, a23}, o[2 * w]);
     o[2 * w + 1] = Ops::mma(pop, mf_u32x4{b01, b23, b01, b23}, o[2 * w + 1]);
   }
+}
+
+// One 16-token block of the recurrence: q . k, logits, max refresh, P . V.
+template <class Ops, bool kMask, bool kCap, bool kCausal>
+__device__ __forceinline__ void mfma_block_step(const mf_u32x4 (&k)[4], const mf_u32x4 (&v)[4],
+                                                const float (&mk)[4], int ntok, int tok0,
+                                                const mf_u32x4 (&qop)[4], float& m, float& lsum,
+                                                mf_f32x4 (&o)[8], float scale, float cap,
+                                                float inv_cap, int s_row, int q4) {
+  float x[4];
+  mfma_logits<kMask, kCap, kCausal>(mfma_qk<Ops>(k, qop), mk, ntok, tok0, scale, cap, inv_cap,
+                                    s_row, q4, x);
+  mfma_refresh_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), m, lsum, o, q4);
+  mfma_pv<Ops>(x, v, m, lsum, o);
 }
 
 template <class Src> struct LanesOf;

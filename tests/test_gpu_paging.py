@@ -841,3 +841,52 @@ def test_chunk_kernel_long_splits(dtype, S, B, pps, monkeypatch):
     if B > 1:
         assert torch.count_nonzero(out[1]).item() == 0
     mgr.clear()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_page64_ragged_prefill_chunks_then_decode(dtype):
+    """HELM's default page size (64 tokens: four 16-token blocks per page)
+    with prefill chunks of odd lengths, so that several pages in the middle
+    of the sequence are partly filled (append_prefill starts a new page per
+    chunk, kv_cache.py:113-143): a later 300-token chunk under an additive
+    mask, and decode steps after it, match the fp64 oracle over the gathered
+    tokens, through the records path and HELM's page-list path alike."""
+    Hq, kvh, D, P = 16, 4, 128, 64
+    tol = 1e-2 if dtype == torch.bfloat16 else 2e-3
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=dtype)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    g = torch.Generator().manual_seed(29)
+    chunks = [1000, 777, 515, 300]
+    ks, vs = [], []
+    for n in chunks:
+        k = torch.randn(1, kvh, n, D, generator=g).to(dtype)
+        v = torch.randn(1, kvh, n, D, generator=g).to(dtype)
+        mgr.append_prefill(0, k.to(DEV), v.to(DEV))
+        ks.append(k)
+        vs.append(v)
+    used = [p.used_tokens for p in mgr.layers[0].pages]
+    assert any(u < P for u in used[:-1])              # partly filled pages mid-sequence
+    K, V = torch.cat(ks, 2), torch.cat(vs, 2)
+    T, S = K.size(2), chunks[-1]
+    q = torch.randn(1, Hq, S, D, generator=g).to(dtype)
+    mask = torch.zeros(1, 1, S, T)
+    mask[0, 0][torch.arange(T)[None, :] > (T - S + torch.arange(S))[:, None]] = float("-inf")
+    mask[..., 7::13] = -3.0
+    ref = A.attention_fp64_batched(q[0].float(), K[0].float(), V[0].float(),
+                                   mask=mask[0].double())
+    out = _stream_prefill_batched([mgr], q.to(DEV), 0, 1 / math.sqrt(D),
+                                  attention_mask=mask.to(DEV)).cpu()
+    assert (out[0].double() - ref).abs().max().item() <= tol
+    pl = perform_streaming_attention(q.to(DEV), list(mgr.iterate_layer_pages(0)),
+                                     attention_mask=mask.to(DEV)).cpu()
+    assert (pl[0].double() - ref).abs().max().item() <= tol
+    for step in range(70):                            # crosses into a new page
+        kd = torch.randn(1, kvh, 1, D, generator=g).to(dtype)
+        vd = torch.randn(1, kvh, 1, D, generator=g).to(dtype)
+        qd = torch.randn(1, Hq, 1, D, generator=g).to(dtype)
+        od = _decode_batched([mgr], qd.to(DEV), kd.to(DEV), vd.to(DEV), 0, 1 / math.sqrt(D))
+        K, V = torch.cat([K, kd], 2), torch.cat([V, vd], 2)
+        if step in (0, 69):
+            r = A.attention_fp64_batched(qd[0].float(), K[0].float(), V[0].float())
+            assert (od[0].double().cpu() - r).abs().max().item() <= tol
+    mgr.clear()
