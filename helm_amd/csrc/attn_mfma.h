@@ -103,6 +103,16 @@ __device__ __forceinline__ mf_u32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, int 
   return mf_u32x4{v[0], v[1], v[2], v[3]};
 }
 
+// LDS transpose read of 16-bit elements (ds_read_b64_tr_b16): within each
+// 16-lane group, lane c = 4a + b receives element b of the 8 bytes that
+// lanes a, a + 4, a + 8 and a + 12 address, in that order.
+__device__ __forceinline__ uint2 ld_tr16(const char* lds_addr) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)(lds_addr));
+  return __builtin_bit_cast(uint2, r);
+}
+
 // Low / high 16-bit halves of two words packed into one: (a.lo, b.lo), (a.hi, b.hi).
 __device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x05040100u);
@@ -506,7 +516,7 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
   auto out_row = [&](int r) -> char* {
     const RowCoord c = row_coord(r0 + 4 * q4 + r, G);
     return reinterpret_cast<char*>(p.out) +
-           (((int64_t)(b * p.Hq + hk * G + c.g) * S + c.s) * 128 + 8 * n) * 2;
+           (((int64_t)(b * p.Hq + hk * G + c.g) * S + c.s) * 128 + n) * 2;
   };
 
   const int np = src.n_pages(b);
@@ -520,7 +530,11 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
       // no keys: HELM's zeros
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        if (4 * q4 + r < nrows) *reinterpret_cast<uint4*>(out_row(r)) = make_uint4(0, 0, 0, 0);
+        if (4 * q4 + r < nrows) {
+          uint16_t* dst = reinterpret_cast<uint16_t*>(out_row(r));
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dst[16 * e] = 0;
+        }
     }
     return;
   }
@@ -639,6 +653,15 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
     }
   };
 
+  // LDS address this lane supplies to the transpose read of V dim group e of
+  // block j: token 4 (n >> 2) + q4, dims 16 e + 4 (n & 3) .. + 3 (8 bytes of
+  // the swizzled row); the read hands lane n dim 16 e + n of the four tokens
+  // 4r + q4 supplied by lanes n >> 2, + 4, + 8, + 12 of its 16-lane group
+  const int vt = 4 * (n >> 2) + q4;
+  auto vaddr = [&](int buf, int j, int e) -> const char* {
+    const int chunk = 2 * e + ((n & 3) >> 1);
+    return reinterpret_cast<const char*>(&lds[buf][1][j][vt * 16 + (chunk ^ vt)]) + 8 * (n & 1);
+  };
   const int tau = 4 * (n & 3) + (n >> 2);   // K token of this lane in a block
   StageView sv_cur, sv_next;
   if (nstage > 0) {
@@ -656,25 +679,60 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
     }
     __syncthreads();
     if (wave_rows) {
+      // blocks in pairs: one P . V MFMA takes 32 tokens (block jp's four of
+      // this lane in k 0-3, block jp + 1's in k 4-7), once with the hi parts
+      // of the weights and once with the lo parts, against the same V
+      // operand; an empty block of a pair holds zeros (bounded loads) and
+      // -inf logits, so it adds nothing
 #pragma unroll
-      for (int j = 0; j < kChunkStage; ++j) {
-        const int ntok = sv_cur.ntok[j];
-        if (ntok == 0) continue;            // uniform: an empty or past-the-end block
-        mf_u32x4 k[4], v[4];
+      for (int jp = 0; jp < kChunkStage; jp += 2) {
+        if (sv_cur.ntok[jp] == 0 && sv_cur.ntok[jp + 1] == 0) continue;   // uniform
+        float x[2][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) k[i] = lds[buf][0][j][tau * 16 + ((q4 + 4 * i) ^ tau)];
+        for (int h = 0; h < 2; ++h) {
+          const int j = jp + h;
+          mf_u32x4 k[4];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int t = q4 + 4 * jj;
-          v[jj] = lds[buf][1][j][t * 16 + (n ^ t)];
+          for (int i = 0; i < 4; ++i) k[i] = lds[buf][0][j][tau * 16 + ((q4 + 4 * i) ^ tau)];
+          float mk[4] = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (kMask) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mk[r] = mcur[j][r];
+          }
+          mfma_logits<kMask, kCap, kCausal>(mfma_qk<Ops>(k, qop), mk, sv_cur.ntok[j],
+                                            sv_cur.tok0[j], scale, cap, inv_cap, s_row, q4, x[h]);
         }
-        float mk[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (kMask) {
+        mfma_refresh_max(fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
+                               fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3]))),
+                         m, lsum, o, q4);
+        const float base = (m == -INFINITY) ? 0.f : m;
+        uint32_t hw[4], lw[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) mk[r] = mcur[j][r];
+        for (int h = 0; h < 2; ++h) {
+          float wt[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            wt[r] = fexp(x[h][r] - base);
+            lsum += wt[r];
+          }
+          Ops::split2(wt[0], wt[1], hw[2 * h], lw[2 * h]);
+          Ops::split2(wt[2], wt[3], hw[2 * h + 1], lw[2 * h + 1]);
         }
-        mfma_block_step<Ops, kMask, kCap, kCausal>(k, v, mk, ntok, sv_cur.tok0[j], qop, m, lsum,
-                                                   o, scale, cap, inv_cap, s_row, q4);
+        const mf_u32x4 phi = mf_u32x4{hw[0], hw[1], hw[2], hw[3]};
+        const mf_u32x4 plo = mf_u32x4{lw[0], lw[1], lw[2], lw[3]};
+        // V operand of dim group e: lane n gets dim 16 e + n of tokens
+        // 4r + q4 (r = 0..3) of each block, by the LDS transpose read
+        mf_u32x4 vop[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint2 a = ld_tr16(vaddr(buf, jp, e));
+          const uint2 c = ld_tr16(vaddr(buf, jp + 1, e));
+          vop[e] = mf_u32x4{a.x, a.y, c.x, c.y};
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = Ops::mma(phi, vop[e], o[e]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = Ops::mma(plo, vop[e], o[e]);
       }
     }
     sv_cur = sv_next;
@@ -696,10 +754,12 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
     for (int r = 0; r < 4; ++r) {
       const float l = __shfl(lrow, 4 * q4 + r, 64);   // lane 4 q4 + r holds that row's sum
       const float inv = 1.f / fmaxf(l, 1e-12f);
-      if (4 * q4 + r < nrows)
-        *reinterpret_cast<uint4*>(out_row(r)) =
-            make_uint4(Ops::pk(o[0][r] * inv, o[1][r] * inv), Ops::pk(o[2][r] * inv, o[3][r] * inv),
-                       Ops::pk(o[4][r] * inv, o[5][r] * inv), Ops::pk(o[6][r] * inv, o[7][r] * inv));
+      if (4 * q4 + r < nrows) {
+        uint16_t* dst = reinterpret_cast<uint16_t*>(out_row(r));
+#pragma unroll
+        for (int e = 0; e < 8; ++e)                              // dim 16 e + n
+          dst[16 * e] = static_cast<uint16_t>(Ops::pk(o[e][r] * inv, 0.f));
+      }
     }
     return;
   }
@@ -711,9 +771,9 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
   for (int r = 0; r < 4; ++r) {
     const int row = 4 * q4 + r;
     if (row < nrows) {
-      float* dst = &p.ws_o[(part + row) * 128 + 8 * n];
-      *reinterpret_cast<float4*>(dst) = make_float4(o[0][r], o[1][r], o[2][r], o[3][r]);
-      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4][r], o[5][r], o[6][r], o[7][r]);
+      float* dst = &p.ws_o[(part + row) * 128 + n];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[16 * e] = o[e][r];      // dim 16 e + n
     }
   }
 }
