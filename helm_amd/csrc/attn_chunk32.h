@@ -1,0 +1,385 @@
+// Query chunks on 32 x 32 matrix-core tiles (v_mfma_f32_32x32x16_{bf16,f16}).
+//
+// The same page walk and LDS staging as chunk_mfma_kernel (a workgroup of
+// four waves, stages of four 16-token blocks, one per wave, swizzled into LDS,
+// one barrier per stage; here the blocks go from memory straight into LDS by
+// buffer loads with the LDS destination), but each wave owns 32 query rows (two
+// 16-row tiles of the partial layout) and computes 32 tokens (two blocks) per
+// step, so the softmax of a step covers 1024 scores instead of 256 and its
+// fixed costs (max refresh check, weight split, scalar bookkeeping) are shared
+// by four times the matrix work.
+//
+// Lane l = 32 hh + j (j = l % 32):
+//   q . k   S^T = K Q^T: A = K (row m = token tau(m), dims 16i + 8hh .. + 7),
+//           B = Q^T (column j = query row j), eight MFMAs over the 128 dims.
+//           The result gives lane l, for its query row j, register
+//           r = 4g + t <-> output row m = 8g + 4hh + t, and with
+//           tau(8g + 4h + t) = 16 (g >> 1) + 8h + 4 (g & 1) + t register r holds
+//           token 8hh + (r & 7) of block r >> 3 of the step.
+//   P . V   O += P V: A = the weights of row j for tokens 8hh .. 8hh + 7 of a
+//           block (exactly registers 8u .. 8u + 7 above), split into 16-bit hi
+//           and lo parts (two MFMAs); B = V of those tokens at dim 32e + j,
+//           fetched by LDS transpose reads; O register 4g + t of dim group e
+//           is row 8g + 4hh + t, dim 32e + j.
+// Online softmax per query row with the lazy rescale of the decode kernel.
+#pragma once
+
+#include "attn_mfma.h"
+
+namespace helm {
+
+typedef float mf_f32x16 __attribute__((ext_vector_type(16)));
+
+template <typename T> struct Mfma32;
+template <> struct Mfma32<bf16_t> {
+  __device__ static __forceinline__ mf_f32x16 mma(mf_u32x4 a, mf_u32x4 b, mf_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mf_bf16x8, a),
+                                                   __builtin_bit_cast(mf_bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma32<f16_t> {
+  __device__ static __forceinline__ mf_f32x16 mma(mf_u32x4 a, mf_u32x4 b, mf_f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mf_f16x8, a),
+                                                  __builtin_bit_cast(mf_f16x8, b), c, 0, 0, 0);
+  }
+};
+
+constexpr int kChunk32Rows = 32;   // query rows per wave
+
+// 16 bytes per lane from a buffer straight into LDS: lane i writes
+// lds_dst + 16 i (the address must be the same in every lane); loads past the
+// buffer's size write zeros
+__device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, void* lds_dst, int off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_dst, 16,
+                                           off, 0, 0, 0);
+}
+
+template <typename T, class Src, int FEAT>
+__global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src) {
+  using Ops = MfmaOps<T>;
+  using M32 = Mfma32<T>;
+  constexpr int kRow = 256;                // bytes per token row (128 dims x 2 B)
+  constexpr int kBlk = kBlockTok * kRow;   // 4 KiB per 16-token block of K (or V)
+  constexpr bool kMask = (FEAT & kFeatMask) != 0;
+  constexpr bool kCap = (FEAT & kFeatCap) != 0;
+  constexpr bool kCausal = (FEAT & kFeatCausal) != 0;
+  // two stage buffers as two objects, so that the compiler sees that the
+  // loads filling one never touch the reads of the other:
+  // [K, V][block of the stage][16-byte chunk], chunk c of token t at slot
+  // t * 16 + (c ^ t)
+  typedef mf_u32x4 StageBuf[2][kChunkStage][kBlk / 16];
+  __shared__ StageBuf lds0, lds1;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int jr = lane & 31;
+  const int hh = lane >> 5;
+
+  const int split_local = blockIdx.x;
+  const int hk = blockIdx.y % p.Hkv;
+  const int n32 = (p.n_qtiles + 1) / 2;                 // 32-row groups of the head
+  const int wt = (blockIdx.y / p.Hkv) * kChunkStage + wave;
+  const bool wave_rows = wt < n32;
+  const int wtc = wave_rows ? wt : n32 - 1;
+  const int b = blockIdx.z;
+  const int S = p.S;
+  const int G = p.G;
+  const int rbase = wtc * kChunk32Rows;
+  const int nrows = min(kChunk32Rows, G * S - rbase);
+  const int tile0 = (b * p.Hkv + hk) * p.n_qtiles + 2 * wtc;   // this wave's first 16-row tile
+  const bool two_tiles = 2 * wtc + 1 < p.n_qtiles;
+
+  // output element of O register 4g + t of dim group e
+  auto out_elem = [&](int g, int t, int e) -> uint16_t* {
+    const RowCoord c = row_coord(rbase + 8 * g + 4 * hh + t, G);
+    return reinterpret_cast<uint16_t*>(p.out) +
+           ((int64_t)(b * p.Hq + hk * G + c.g) * S + c.s) * 128 + 32 * e + jr;
+  };
+
+  const int np = src.n_pages(b);
+  const int lo = min(p.lo, np);
+  const int hi = min(p.hi, np);
+  const int nsplit_launch = (hi - lo + p.pps - 1) / p.pps;
+  const int total = p.total_splits > 0 ? p.total_splits : nsplit_launch;
+  if (split_local == 0 && lane == 0 && wave_rows) {
+    p.counts[tile0] = total;
+    if (two_tiles) p.counts[tile0 + 1] = total;
+  }
+  if (!(total > 0 && split_local < nsplit_launch)) {        // uniform per workgroup
+    if (p.direct_out && total == 0 && split_local == 0 && wave_rows) {
+      // no keys: HELM's zeros
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (8 * g + 4 * hh + t < nrows)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) *out_elem(g, t, e) = 0;
+    }
+    return;
+  }
+  const int split = p.split_base + split_local;
+  const int pg0 = lo + split_local * p.pps;
+  const int npg = min(pg0 + p.pps, hi) - pg0;
+
+  // ---- query operand: row jr of the wave, dims 16i + 8hh .. + 7 ----------------
+  const bool row_ok = jr < nrows;
+  const RowCoord rc = row_coord(rbase + (row_ok ? jr : 0), G);
+  const int s_row = rc.s;
+  mf_u32x4 qop[8];
+  {
+    const char* qp = reinterpret_cast<const char*>(p.q) +
+                     ((int64_t)(b * p.Hq + hk * G + rc.g) * S + s_row) * kRow;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qp + 16 * (2 * i + hh));
+      qop[i] = row_ok ? mf_u32x4{v.x, v.y, v.z, v.w} : mf_u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  const float* mrow = nullptr;
+  if constexpr (kMask)
+    mrow = p.mask + (int64_t)b * p.mask_bstride + (int64_t)(hk * G + rc.g) * p.mask_hstride +
+           (int64_t)s_row * p.mask_qstride;
+  const float scale = p.scale;
+  const float cap = p.softcap;
+  const float inv_cap = kCap ? 1.f / cap : 0.f;
+
+  float m = -INFINITY;   // running max of row jr (same in both halves)
+  float lsum = 0.f;      // this lane's share of the row's weight sum
+  mf_f32x16 o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[e][r] = 0.f;
+
+  const int bpp = p.bpp;
+  const int nblk = npg * bpp;
+  const int nstage = (nblk + kChunkStage - 1) / kChunkStage;
+
+  // page records: window [win, win + 64) of the split's pages (the next
+  // window is read when the walk enters it, once per 64 pages)
+  typename LanesOf<Src>::type lanes = lane_pages(src, b, pg0, lane);
+  int win = 0;
+  int cur_pi = 0, cur_sub = 0;   // page (relative to pg0) and sub-block of the next view
+
+  struct StageView {
+    int ntok[kChunkStage], tok0[kChunkStage];
+    int own_ntok;
+    const char *kb, *vb;
+  };
+  auto view_stage = [&](int st, StageView& sv) {
+#pragma unroll
+    for (int j = 0; j < kChunkStage; ++j) {
+      if (cur_pi - win >= kRecWindow) {   // uniform: the page lies in the next window
+        win += kRecWindow;
+        lanes = lane_pages(src, b, pg0 + win, lane);
+      }
+      const PageView pv = lane_page_view(src, lanes, b, pg0 + cur_pi, cur_pi - win, hk);
+      const int tok_in = cur_sub * kBlockTok;
+      const int nt = st * kChunkStage + j < nblk ? sclamp(pv.used - tok_in, 0, kBlockTok) : 0;
+      sv.ntok[j] = nt;
+      sv.tok0[j] = pv.tok_off + tok_in;
+      if (j == wave) {
+        sv.own_ntok = nt;
+        sv.kb = pv.k + tok_in * kRow;
+        sv.vb = pv.v + tok_in * kRow;
+      }
+      if (++cur_sub == bpp) {
+        cur_sub = 0;
+        ++cur_pi;
+      }
+    }
+  };
+
+  // a stage's block of this wave straight from memory into LDS (no VGPRs):
+  // instruction u writes slots 64u .. 64u + 63, lane i slot 64u + i, which
+  // holds chunk (i & 15) ^ t of token t = 4u + (i >> 4) (the swizzle), so
+  // each lane fetches that chunk; loads past the block's tokens write zeros
+  auto dma_stage = [&](const StageView& sv, StageBuf& dst) {
+    const auto rk = make_rsrc(sv.kb, sv.own_ntok * kRow);
+    const auto rv = make_rsrc(sv.vb, sv.own_ntok * kRow);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = 4 * u + (lane >> 4);
+      const int off = t * kRow + 16 * ((lane & 15) ^ t);
+      buf_load16_lds(rk, &dst[0][wave][64 * u], off);
+      buf_load16_lds(rv, &dst[1][wave][64 * u], off);
+    }
+  };
+
+  // K row this lane supplies to the q . k MFMAs: token tau(jr) of the step
+  const int g_a = jr >> 3, h_a = (jr >> 2) & 1, t_a = jr & 3;
+  const int tau = 16 * (g_a >> 1) + 8 * h_a + 4 * (g_a & 1) + t_a;
+  const int kblk = tau >> 4, ktok = tau & 15;
+  // transpose-read address of V: token 8hh + 4z + (n >> 2) of a block, dims
+  // 32e + 16 (jr >> 4) + 4 (n & 3) .. + 3, with n = lane % 16
+  const int nl = lane & 15;
+  auto vaddr = [&](const StageBuf& cur, int blk, int z, int e) -> const char* {
+    const int vtok = 8 * hh + 4 * z + (nl >> 2);
+    const int chunk = 4 * e + 2 * (jr >> 4) + ((nl & 3) >> 1);
+    return reinterpret_cast<const char*>(&cur[1][blk][vtok * 16 + (chunk ^ vtok)]) +
+           8 * (nl & 1);
+  };
+
+  // additive mask of row jr for the step of blocks bp, bp + 1 of a stage:
+  // tokens 8hh .. 8hh + 7 of each block, bounded by its valid tokens
+  float mk_next[16];
+  auto load_step_mask = [&](const StageView& sv, int bp) {
+    if constexpr (kMask) {
+      // (plain loads: the row differs between lanes; past the block's last
+      // valid token the index is clamped to it)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int nt = sv.ntok[bp + u];
+        const int last = max(nt - 1, 0);
+        const float* mb = mrow + sv.tok0[bp + u];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mk_next[8 * u + i] = nt > 0 ? mb[min(8 * hh + i, last)] : 0.f;
+      }
+    }
+  };
+
+  StageView sv_cur, sv_next;
+  if (nstage > 0) {
+    view_stage(0, sv_cur);
+    dma_stage(sv_cur, lds0);
+    if (wave_rows) load_step_mask(sv_cur, 0);
+  }
+  // stage st computes from `cur` while stage st + 1 loads into `nxt`
+  auto stage = [&](int st, const StageBuf& cur, StageBuf& nxt) {
+    // stage st is in LDS (this wave's loads done, then everyone's), and every
+    // wave is done with the other buffer, which the next stage's loads fill
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    if (st + 1 < nstage) {
+      view_stage(st + 1, sv_next);
+      dma_stage(sv_next, nxt);
+    }
+    if (wave_rows) {
+#pragma unroll
+      for (int bp = 0; bp < kChunkStage; bp += 2) {     // the step's blocks bp, bp + 1
+        const int nt0 = sv_cur.ntok[bp], nt1 = sv_cur.ntok[bp + 1];
+        // the mask of the next step is loaded now, one step ahead of its use
+        float mk[16];
+        if constexpr (kMask) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mk[r] = mk_next[r];
+          if (bp == 0)
+            load_step_mask(sv_cur, 2);
+          else if (st + 1 < nstage)
+            load_step_mask(sv_next, 0);
+        }
+        if (nt0 == 0 && nt1 == 0) continue;   // uniform; an empty block of a step
+                                               // holds zeros and -inf logits
+        mf_f32x16 sc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const mf_u32x4 ka = cur[0][bp + kblk][ktok * 16 + ((2 * i + hh) ^ ktok)];
+          sc = M32::mma(ka, qop[i], sc);
+        }
+        float x[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int u = r >> 3;
+          const int tk = 8 * hh + (r & 7);
+          float val = sc[r] * scale;
+          if constexpr (kCap) val = tanhf(val * inv_cap) * cap;
+          if constexpr (kMask) val += mk[r];
+          if constexpr (kCausal)
+            if (sv_cur.tok0[bp + u] + tk > s_row) val = -INFINITY;
+          if (tk >= (u ? nt1 : nt0)) val = -INFINITY;
+          x[r] = val;
+        }
+        float bm = x[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) bm = fmaxf(bm, x[r]);
+        if (__builtin_amdgcn_ballot_w64(bm > m + kMfmaSlack)) {
+          // refresh the row max (both halves of the row agree)
+          const float mn = fmaxf(m, fmaxf(bm, __shfl_xor(bm, 32, 64)));
+          const float a = fexp(m - ((mn == -INFINITY) ? 0.f : mn));
+          lsum *= a;
+          m = mn;
+          // O register 4g + t is row 8g + 4hh + t: that row's factor
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              const float ar = __shfl(a, 8 * g + 4 * hh + t, 64);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) o[e][4 * g + t] *= ar;
+            }
+        }
+        const float base = (m == -INFINITY) ? 0.f : m;
+        uint32_t hw[8], lw[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float w0 = fexp(x[2 * q] - base), w1 = fexp(x[2 * q + 1] - base);
+          lsum += w0 + w1;
+          Ops::split2(w0, w1, hw[q], lw[q]);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const mf_u32x4 phi = mf_u32x4{hw[4 * u], hw[4 * u + 1], hw[4 * u + 2], hw[4 * u + 3]};
+          const mf_u32x4 plo = mf_u32x4{lw[4 * u], lw[4 * u + 1], lw[4 * u + 2], lw[4 * u + 3]};
+          mf_u32x4 vop[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint2 a0 = ld_tr16(vaddr(cur, bp + u, 0, e));
+            const uint2 a1 = ld_tr16(vaddr(cur, bp + u, 1, e));
+            vop[e] = mf_u32x4{a0.x, a0.y, a1.x, a1.y};
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = M32::mma(phi, vop[e], o[e]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = M32::mma(plo, vop[e], o[e]);
+        }
+      }
+    }
+    sv_cur = sv_next;
+  };
+  for (int st = 0; st < nstage; st += 2) {
+    stage(st, lds0, lds1);
+    if (st + 1 < nstage) stage(st + 1, lds1, lds0);
+  }
+
+  if (!wave_rows) return;
+  const float lrow = lsum + __shfl_xor(lsum, 32, 64);     // row jr's sum
+  if (p.direct_out) {
+    // the call's only split: normalized rows straight to the output
+    // (HELM's final out / max(sum, 1e-12), kv_cache.py:554-555)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int i = 8 * g + 4 * hh + t;
+        const float inv = 1.f / fmaxf(__shfl(lrow, i, 64), 1e-12f);
+        if (i < nrows)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            *out_elem(g, t, e) = static_cast<uint16_t>(Ops::pk(o[e][4 * g + t] * inv, 0.f));
+      }
+    return;
+  }
+  // partials (m, l, o[128]) of the wave's rows in their 16-row tiles
+  auto part_row = [&](int i) -> int64_t {
+    return ((int64_t)(tile0 + (i >> 4)) * p.max_splits + split) * p.rows_per_tile + (i & 15);
+  };
+  if (hh == 0 && jr < nrows)
+    *reinterpret_cast<float2*>(&p.ws_ml[part_row(jr) * 2]) = make_float2(m, lrow);
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int i = 8 * g + 4 * hh + t;
+      if (i < nrows) {
+        float* dst = &p.ws_o[part_row(i) * 128 + jr];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[32 * e] = o[e][4 * g + t];
+      }
+    }
+}
+
+}  // namespace helm

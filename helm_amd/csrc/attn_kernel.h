@@ -406,7 +406,7 @@ struct AttnParams {
   int* counts;        // [tiles] splits of each tile (merge-kernel mode)
   uint32_t* tickets;  // [tiles] arrivals (fused mode; zero between calls)
   int fused;          // 1: the last split of a tile merges in-kernel
-  int row_waves;      // 1 (matrix-core kernel): each wave owns a 16-row tile
+  int row_waves;      // query chunks: 16-row tiles per wave (1 or 2; 0: decode kernel)
   int direct_out;     // 1: the call has one split; the chunk kernel writes the output
   int bpp_log2;       // log2 of bpp when bpp is a power of two, else -1
 };

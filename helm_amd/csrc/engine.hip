@@ -80,10 +80,12 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 // matrix cores; generic: the element-wise kernel only).
 struct Plan {
   int mfma, fast, nw, fused, gm, rows, epl, n_qtiles, bpp, pps, max_splits;
-  int row_waves;  // matrix-core kernel: one 16-row tile per wave (query chunks)
+  int row_waves;  // query chunks: 16-row tiles per wave (1: chunk_mfma_kernel, 2: chunk32)
   int direct;     // row-wave plan with one split: output written by the split kernel
   // workgroups per (sequence, KV head) along the query rows
-  int qblocks() const { return row_waves ? (n_qtiles + nw - 1) / nw : n_qtiles; }
+  int qblocks() const {
+    return row_waves ? (n_qtiles + nw * row_waves - 1) / (nw * row_waves) : n_qtiles;
+  }
   size_t ticket_bytes, count_bytes, ml_bytes, o_bytes;
   size_t total() const { return ticket_bytes + count_bytes + ml_bytes + o_bytes; }
 };
@@ -162,8 +164,11 @@ void plan_shape(Plan& pl, int G, int q_len, int D, int max_tok_per_page) {
   // query chunks of several 16-row tiles: the waves of a workgroup take one
   // tile each over the same pages (K/V read once per workgroup from L2, not
   // once per tile); HELM_AMD_ROW_WAVES=0 keeps one tile per workgroup
-  pl.row_waves = (pl.mfma && pl.n_qtiles >= 2 && env_int("HELM_AMD_ROW_WAVES", 1)) ? 1 : 0;
-  if (pl.row_waves) pl.nw = kChunkStage;  // chunk_mfma_kernel: four waves, one tile each
+  // (HELM_AMD_CHUNK=16 keeps 16-row waves: chunk_mfma_kernel)
+  pl.row_waves = (pl.mfma && pl.n_qtiles >= 2 && env_int("HELM_AMD_ROW_WAVES", 1))
+                     ? (env_int("HELM_AMD_CHUNK", 32) == 16 ? 1 : 2)
+                     : 0;
+  if (pl.row_waves) pl.nw = kChunkStage;  // four waves per workgroup
 }
 
 // chunk_mfma_kernel reads its page records in windows: a split may be long

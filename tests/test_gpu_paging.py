@@ -802,9 +802,10 @@ def test_layer_page_list_attention_matches_page_by_page(case, monkeypatch):
     mgr.clear()
 
 
+@pytest.mark.parametrize("chunk", ["32", "16"])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("S,B,pps", [(1024, 1, None), (512, 2, 300), (256, 1, None)])
-def test_chunk_kernel_long_splits(dtype, S, B, pps, monkeypatch):
+def test_chunk_kernel_long_splits(dtype, S, B, pps, chunk, monkeypatch):
     """Query chunks over 257 pages (last one partial) where a split spans more
     than the 64 page records one lane window holds.  S = 1024: enough
     workgroups that every (KV head, tile block) takes all pages in one split
@@ -812,6 +813,7 @@ def test_chunk_kernel_long_splits(dtype, S, B, pps, monkeypatch):
     empty sequence and 300 pages per split: the same, with zeros for the
     empty sequence; S = 256: four splits of 65 pages, merged.  All match the
     fp64 oracle under an additive chunk mask (checked on two KV heads)."""
+    monkeypatch.setenv("HELM_AMD_CHUNK", chunk)
     if pps is not None:
         monkeypatch.setenv("HELM_AMD_PPS", str(pps))
     Hq, kvh, D, P, T = 32, 8, 128, 16, 4100
@@ -889,4 +891,36 @@ def test_page64_ragged_prefill_chunks_then_decode(dtype):
         if step in (0, 69):
             r = A.attention_fp64_batched(qd[0].float(), K[0].float(), V[0].float())
             assert (od[0].double().cpu() - r).abs().max().item() <= tol
+    mgr.clear()
+
+
+@pytest.mark.parametrize("chunk", ["32", "16"])
+@pytest.mark.parametrize("S", [5, 9, 12, 17, 33])
+def test_chunk_kernels_row_counts(chunk, S, monkeypatch):
+    """Both query-chunk kernels (32-row waves on 32x32 MFMA tiles, the
+    default; 16-row waves with HELM_AMD_CHUNK=16) at query-row counts that
+    leave a wave with one 16-row tile, a partial tile or both (G = 4:
+    20 .. 132 rows), under an additive mask and under HELM's top-left
+    causal, against the fp64 oracle."""
+    monkeypatch.setenv("HELM_AMD_CHUNK", chunk)
+    Hq, kvh, D, P, T = 16, 4, 128, 16, 301
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=torch.bfloat16)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    g = torch.Generator().manual_seed(31 + S)
+    k = torch.randn(1, kvh, T, D, generator=g).bfloat16()
+    v = torch.randn(1, kvh, T, D, generator=g).bfloat16()
+    mgr.append_prefill(0, k.to(DEV), v.to(DEV))
+    q = torch.randn(1, Hq, S, D, generator=g).bfloat16()
+    mask = torch.zeros(1, 1, S, T)
+    mask[0, 0][torch.arange(T)[None, :] > (T - S + torch.arange(S))[:, None]] = float("-inf")
+    mask[..., 2::9] = -1.5
+    out = _stream_prefill_batched([mgr], q.to(DEV), 0, 1 / math.sqrt(D),
+                                  attention_mask=mask.to(DEV)).cpu()
+    ref = A.attention_fp64_batched(q[0].float(), k[0].float(), v[0].float(), mask=mask[0].double())
+    assert (out[0].double() - ref).abs().max().item() <= 1e-2
+    causal = _stream_prefill_batched([mgr], q.to(DEV), 0, 1 / math.sqrt(D)).cpu()
+    cm = torch.zeros(1, S, T, dtype=torch.float64)
+    cm[0][torch.arange(T)[None, :] > torch.arange(S)[:, None]] = float("-inf")
+    ref = A.attention_fp64_batched(q[0].float(), k[0].float(), v[0].float(), mask=cm)
+    assert (causal[0].double() - ref).abs().max().item() <= 1e-2
     mgr.clear()
