@@ -924,3 +924,34 @@ def test_chunk_kernels_row_counts(chunk, S, monkeypatch):
     ref = A.attention_fp64_batched(q[0].float(), k[0].float(), v[0].float(), mask=cm)
     assert (causal[0].double() - ref).abs().max().item() <= 1e-2
     mgr.clear()
+
+
+@pytest.mark.parametrize("chunk", ["32", "16"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_chunk_kernels_softcap_and_window_mask(chunk, dtype, monkeypatch):
+    """Gemma-2's prefill over cached pages on the matrix-core chunk kernels:
+    a logit soft-cap together with a sliding-window additive mask (every
+    feature at once), 40 query rows per KV head, host pages included (the
+    watermark keeps four pages on the device), against the fp64 oracle."""
+    monkeypatch.setenv("HELM_AMD_CHUNK", chunk)
+    Hq, kvh, D, P, T, S, cap = 8, 2, 128, 16, 420, 10, 5.0
+    tol = 1e-2 if dtype == torch.bfloat16 else 2e-3
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=dtype)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=4 * (2 * kvh * P * D * 2))
+    g = torch.Generator().manual_seed(37)
+    k = torch.randn(1, kvh, T, D, generator=g).to(dtype)
+    v = torch.randn(1, kvh, T, D, generator=g).to(dtype)
+    mgr.append_prefill(0, k.to(DEV), v.to(DEV))
+    assert mgr.layers[0]._n_host > 0
+    q = (2 * torch.randn(1, Hq, S, D, generator=g)).to(dtype)
+    pos = T - S + torch.arange(S)
+    key = torch.arange(T)
+    mask = torch.zeros(1, 1, S, T)
+    mask[0, 0][(key[None, :] > pos[:, None]) | (key[None, :] <= pos[:, None] - 64)] = \
+        torch.finfo(torch.float32).min
+    out = _stream_prefill_batched([mgr], q.to(DEV), 0, 0.1, attention_mask=mask.to(DEV),
+                                  softcap=cap).cpu()
+    ref = A.attention_fp64_batched(q[0].float(), k[0].float(), v[0].float(), scale=0.1,
+                                   mask=mask[0].double(), softcap=cap)
+    assert (out[0].double() - ref).abs().max().item() <= tol
+    mgr.clear()
