@@ -176,3 +176,53 @@ def test_patched_decode_uses_front_and_matches_torch_ops(arch, monkeypatch):
     n_steps = (ids.shape[1] - 24) * cfg.num_hidden_layers
     assert served[:n_steps] == [True] * n_steps and served[n_steps:] == [False] * n_steps
     assert (runs["1"] - runs["0"]).abs().max().item() <= 5e-2
+
+
+def test_bf16_model_d128_matrix_core_paths_match_hf():
+    """A bf16 Qwen3-shaped model with head_dim 128, so that every attention
+    call runs on the matrix-core kernels: the first prompt chunk on the chunk
+    kernel over its own K/V, the second over the cached pages (32x32 tiles,
+    chunk mask), then decode steps through the fused front end and the decode
+    kernel, with eviction to pinned host pages along the way.  Logits stay
+    within bf16 rounding of HF's own eager forward over the same tokens."""
+    import transformers.models.qwen3 as q3
+    from helm_amd.runtime import kv_cache as KC
+    from helm_amd.runtime.kv_offload import KVOffloadConfig, KVOffloadManager
+    cfg = q3.Qwen3Config(vocab_size=97, hidden_size=512, intermediate_size=512,
+                         num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=4,
+                         head_dim=128, max_position_embeddings=1024)
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(1)
+    ref_model = q3.Qwen3ForCausalLM(cfg).eval().to(DEV, torch.bfloat16)
+    model = q3.Qwen3ForCausalLM(cfg).eval().to(DEV, torch.bfloat16)
+    model.load_state_dict(ref_model.state_dict())
+    conf = KVOffloadConfig.from_model(model, page_size=16, gpu_watermark_bytes=64 * 1024)
+    mgr = KVOffloadManager(model, conf, batch_size=1)
+    g = torch.Generator().manual_seed(4)
+    S, c1, steps = 200, 120, 24
+    ids = torch.randint(0, 97, (1, S + steps), generator=g).to(DEV)
+    KC.reset_paging_stats()
+    diffs = []
+    with torch.no_grad():
+        lg = model(ids[:, :c1], position_ids=torch.arange(c1, device=DEV)[None],
+                   use_cache=False).logits
+        ref = ref_model(ids[:, :S], use_cache=False).logits
+        diffs.append((lg.float() - ref[:, :c1].float()).abs())
+        n2 = S - c1
+        cm = torch.zeros(1, 1, n2, S, device=DEV)
+        cm[0, 0][torch.arange(S, device=DEV)[None, :] >
+                 (c1 + torch.arange(n2, device=DEV))[:, None]] = torch.finfo(torch.float32).min
+        lg = model(ids[:, c1:S], position_ids=torch.arange(c1, S, device=DEV)[None],
+                   attention_mask=cm, use_cache=False,
+                   cache_position=torch.arange(c1, S, device=DEV)).logits
+        diffs.append((lg.float() - ref[:, c1:S].float()).abs())
+        for t in range(steps):
+            pos = S + t
+            lg = model(ids[:, pos:pos + 1], position_ids=torch.tensor([[pos]], device=DEV),
+                       use_cache=False, cache_position=torch.tensor([pos], device=DEV)).logits
+            r = ref_model(ids[:, :pos + 1], use_cache=False).logits[:, -1:]
+            diffs.append((lg.float() - r.float()).abs())
+    mgr.restore()
+    d = torch.cat([x.flatten() for x in diffs])
+    assert KC.get_paging_stats()["pages_evicted"] > 0
+    assert d.max().item() <= 0.25 and d.mean().item() <= 0.02, (d.max().item(), d.mean().item())
