@@ -127,6 +127,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   const bool row_ok = jr < nrows;
   const RowCoord rc = row_coord(rbase + (row_ok ? jr : 0), G);
   const int s_row = rc.s;
+  const int s_last = (rbase + nrows - 1) / G;   // the wave's last query position
   mf_u32x4 qop[8];
   {
     const char* qp = reinterpret_cast<const char*>(p.q) +
@@ -272,6 +273,21 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
         }
         if (nt0 == 0 && nt1 == 0) continue;   // uniform; an empty block of a step
                                                // holds zeros and -inf logits
+        // steps that add exactly nothing for any row of the wave are skipped:
+        // causal, every token past the wave's last query position (-inf
+        // logits); masked, every mask value <= -1e30 while every row's max is
+        // already above -1e20 (each weight underflows to 0 and the max stays)
+        if constexpr (kCausal) {
+          if (sv_cur.tok0[bp] > s_last) continue;
+        }
+        if constexpr (kMask) {
+          float mm = mk[0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r) mm = fmaxf(mm, mk[r]);
+          if (!__builtin_amdgcn_ballot_w64(mm > -1e30f) &&
+              !__builtin_amdgcn_ballot_w64(m <= -1e20f))
+            continue;
+        }
         mf_f32x16 sc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] = 0.f;

@@ -955,3 +955,41 @@ def test_chunk_kernels_softcap_and_window_mask(chunk, dtype, monkeypatch):
                                    mask=mask[0].double(), softcap=cap)
     assert (out[0].double() - ref).abs().max().item() <= tol
     mgr.clear()
+
+
+@pytest.mark.parametrize("masked", [True, False])
+def test_chunk32_skips_only_steps_that_add_nothing(masked):
+    """A first prompt chunk over its own 600 tokens (S = T) under HF's
+    causal mask (finfo.min, as the pipeline's masks are) or HELM's top-left
+    causal: the 32x32 kernel skips the steps past each wave's last query
+    position, and the result still equals the fp64 oracle; a second case puts
+    finite mask values among finfo.min ones so that only all-masked steps
+    can be skipped."""
+    Hq, kvh, D, P, T = 16, 4, 128, 16, 600
+    S = T
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=torch.bfloat16)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    g = torch.Generator().manual_seed(41)
+    k = torch.randn(1, kvh, T, D, generator=g).bfloat16()
+    v = torch.randn(1, kvh, T, D, generator=g).bfloat16()
+    mgr.append_prefill(0, k.to(DEV), v.to(DEV))
+    q = torch.randn(1, Hq, S, D, generator=g).bfloat16()
+    fut = torch.arange(T)[None, :] > torch.arange(S)[:, None]
+    for variant in (0, 1):
+        mask = None
+        ref_mask = torch.zeros(1, S, T, dtype=torch.float64)
+        if masked:
+            mask = torch.zeros(1, 1, S, T)
+            mask[0, 0][fut] = torch.finfo(torch.float32).min
+            if variant == 1:
+                mask[0, 0, :, 500:520] = -2.0          # visible again, with a bias
+            ref_mask = mask[0].double()
+        else:
+            ref_mask[0][fut] = float("-inf")
+            if variant == 1:
+                break
+        out = _stream_prefill_batched([mgr], q.to(DEV), 0, 1 / math.sqrt(D),
+                                      attention_mask=mask.to(DEV) if masked else None).cpu()
+        ref = A.attention_fp64_batched(q[0].float(), k[0].float(), v[0].float(), mask=ref_mask)
+        assert (out[0].double() - ref).abs().max().item() <= 1e-2
+    mgr.clear()
