@@ -247,8 +247,21 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
     dma_stage(sv_cur, lds0);
     if (wave_rows) load_step_mask(sv_cur, 0);
   }
+  // causal: the workgroup's last query position; stages starting past it
+  // add nothing for any of its rows (tokens only grow along the walk), so the
+  // walk ends there (uniform across the workgroup)
+  const int qrow_end = min(G * S, (int)(blockIdx.y / p.Hkv + 1) * kChunkStage * kChunk32Rows);
+  const int s_last_wg = (qrow_end - 1) / G;
+  bool done = false;
   // stage st computes from `cur` while stage st + 1 loads into `nxt`
   auto stage = [&](int st, const StageBuf& cur, StageBuf& nxt) {
+    if constexpr (kCausal) {
+      if (sv_cur.tok0[0] > s_last_wg) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // this stage's loads land before the exit
+        done = true;
+        return;
+      }
+    }
     // stage st is in LDS (this wave's loads done, then everyone's), and every
     // wave is done with the other buffer, which the next stage's loads fill
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
@@ -356,9 +369,9 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
     }
     sv_cur = sv_next;
   };
-  for (int st = 0; st < nstage; st += 2) {
+  for (int st = 0; st < nstage && !done; st += 2) {
     stage(st, lds0, lds1);
-    if (st + 1 < nstage) stage(st + 1, lds1, lds0);
+    if (st + 1 < nstage && !done) stage(st + 1, lds1, lds0);
   }
 
   if (!wave_rows) return;
