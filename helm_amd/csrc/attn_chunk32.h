@@ -128,6 +128,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   const RowCoord rc = row_coord(rbase + (row_ok ? jr : 0), G);
   const int s_row = rc.s;
   const int s_last = (rbase + nrows - 1) / G;   // the wave's last query position
+  const int s_first = rbase / G;                // and its first
   mf_u32x4 qop[8];
   {
     const char* qp = reinterpret_cast<const char*>(p.q) +
@@ -312,15 +313,25 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
         float x[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int u = r >> 3;
-          const int tk = 8 * hh + (r & 7);
           float val = sc[r] * scale;
           if constexpr (kCap) val = tanhf(val * inv_cap) * cap;
           if constexpr (kMask) val += mk[r];
-          if constexpr (kCausal)
-            if (sv_cur.tok0[bp + u] + tk > s_row) val = -INFINITY;
-          if (tk >= (u ? nt1 : nt0)) val = -INFINITY;
           x[r] = val;
+        }
+        // the per-token limits, only where a step reaches them (uniform tests):
+        // the causal limit when its last token is past the wave's first query
+        // position, the valid-token limit when a block is partial
+        if constexpr (kCausal) {
+          if (sv_cur.tok0[bp + 1] + kBlockTok - 1 > s_first) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (sv_cur.tok0[bp + (r >> 3)] + 8 * hh + (r & 7) > s_row) x[r] = -INFINITY;
+          }
+        }
+        if (nt0 < kBlockTok || nt1 < kBlockTok) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (8 * hh + (r & 7) >= ((r >> 3) ? nt1 : nt0)) x[r] = -INFINITY;
         }
         float bm = x[0];
 #pragma unroll
