@@ -312,9 +312,36 @@ def _prefill_from_records(kvcms, q, layer_idx: int, scale: float,
     return torch.cat(outs, dim=0)
 
 
+_CAUSAL_MASKS: dict = {}   # (address, shape, strides, dtype, version) -> bool
+
+
+def _is_causal_mask(mask: Optional[torch.Tensor], S: int, T: int) -> bool:
+    """Whether an additive [B, H, S, S] mask is exactly the causal pattern: 0
+    on and below the diagonal, <= -1e4 above it (HF's finfo.min masks in fp32,
+    bf16 or fp16).  Attending under such a mask equals attending with causal
+    masking: every row sees at least its own key, so each masked weight
+    exp(logit + mask - max) underflows to exactly 0, as with -inf.  The answer
+    is remembered per tensor version (the forward passes one mask to every
+    layer), so the check runs once per forward."""
+    if (mask is None or S != T or S < 2 or mask.dim() != 4 or tuple(mask.shape[-2:]) != (S, T)
+            or mask.dtype not in (torch.float32, torch.bfloat16, torch.float16)):
+        return False
+    key = (mask.data_ptr(), tuple(mask.shape), tuple(mask.stride()), mask.dtype, mask._version)
+    hit = _CAUSAL_MASKS.get(key)
+    if hit is None:
+        upper = torch.ones(S, T, dtype=torch.bool, device=mask.device).triu_(1)
+        hit = bool(torch.where(upper, mask <= -1e4, mask == 0).all())
+        if len(_CAUSAL_MASKS) > 64:
+            _CAUSAL_MASKS.clear()
+        _CAUSAL_MASKS[key] = hit
+    return hit
+
+
 def _local_attention(q, k, v, scale, attention_mask, softcap=None):
     """First prefill chunk: attention over the chunk's own K/V (no pages yet),
-    the SDPA / eager call of kv_offload.py:330-338, :605-613."""
+    the SDPA / eager call of kv_offload.py:330-338, :605-613.  A mask that is
+    exactly causal runs as causal masking (same result; the kernel then skips
+    the keys past each row instead of reading the mask)."""
     _require_hip(q, "prefill attention")
     if attention_mask is not None and attention_mask.dtype == torch.bool:
         attention_mask = torch.zeros(attention_mask.shape, dtype=torch.float32,
@@ -323,6 +350,8 @@ def _local_attention(q, k, v, scale, attention_mask, softcap=None):
     if k.stride(3) != 1 or k.stride(2) != k.size(3) or v.stride() != k.stride():
         k, v = k.contiguous(), v.contiguous()
     seqs = [_contiguous_segments(k, v, b) for b in range(q.shape[0])]
+    if _is_causal_mask(attention_mask, q.shape[2], k.shape[2]):
+        return _attend(q, seqs, k.shape[1], k.dtype, scale, None, softcap, True)
     return _attend(q, seqs, k.shape[1], k.dtype, scale, attention_mask, softcap, False)
 
 

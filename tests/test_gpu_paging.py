@@ -993,3 +993,35 @@ def test_chunk32_skips_only_steps_that_add_nothing(masked):
         ref = A.attention_fp64_batched(q[0].float(), k[0].float(), v[0].float(), mask=ref_mask)
         assert (out[0].double() - ref).abs().max().item() <= 1e-2
     mgr.clear()
+
+
+@pytest.mark.parametrize("mdtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_first_chunk_causal_mask_shortcut_is_exact(mdtype, monkeypatch):
+    """The first prompt chunk under HF's causal mask (finfo.min of the mask's
+    dtype above the diagonal) runs as causal masking, with exactly the output
+    of the masked call; a mask that differs anywhere (a padded first key) is
+    not taken for causal, and an in-place change of a mask is noticed."""
+    from helm_amd.runtime import kv_offload as KO
+    B, Hq, kvh, D, S = 2, 8, 2, 128, 300
+    g = torch.Generator().manual_seed(43)
+    q = torch.randn(B, Hq, S, D, generator=g).bfloat16().to(DEV)
+    k = torch.randn(B, kvh, S, D, generator=g).bfloat16().to(DEV)
+    v = torch.randn(B, kvh, S, D, generator=g).bfloat16().to(DEV)
+    mask = torch.zeros(B, 1, S, S, dtype=mdtype)
+    mask[:, 0][:, torch.ones(S, S, dtype=torch.bool).triu(1)] = torch.finfo(mdtype).min
+    mask = mask.to(DEV)
+    fast = KO._local_attention(q, k, v, 1 / math.sqrt(D), mask)
+    assert KO._is_causal_mask(mask, S, S)
+    monkeypatch.setattr(KO, "_is_causal_mask", lambda *a: False)
+    slow = KO._local_attention(q, k, v, 1 / math.sqrt(D), mask)
+    monkeypatch.undo()
+    assert torch.equal(fast, slow)
+    ref = A.attention_fp64_batched(q[1].float().cpu(), k[1].float().cpu(), v[1].float().cpu(),
+                                   mask=mask[1].double().cpu())
+    assert (fast[1].double().cpu() - ref).abs().max().item() <= 1e-2
+    mask[1, 0, 5:, 0] = torch.finfo(mdtype).min       # item 1: key 0 padded away
+    assert not KO._is_causal_mask(mask, S, S)
+    out = KO._local_attention(q, k, v, 1 / math.sqrt(D), mask)
+    ref = A.attention_fp64_batched(q[1].float().cpu(), k[1].float().cpu(), v[1].float().cpu(),
+                                   mask=mask[1].double().cpu())
+    assert (out[1].double().cpu()[:, 5:] - ref[:, 5:]).abs().max().item() <= 1e-2
