@@ -127,8 +127,11 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   const bool row_ok = jr < nrows;
   const RowCoord rc = row_coord(rbase + (row_ok ? jr : 0), G);
   const int s_row = rc.s;
-  const int s_last = (rbase + nrows - 1) / G;   // the wave's last query position
-  const int s_first = rbase / G;                // and its first
+  // causal: query position s sees tokens 0 .. s + coff (coff = causal - 1)
+  const int coff = kCausal ? p.causal - 1 : 0;
+  const int s_vis = s_row + coff;                      // row jr's last visible token
+  const int s_last = (rbase + nrows - 1) / G + coff;   // the wave's last visible token
+  const int s_first = rbase / G + coff;                // and its first row's
   mf_u32x4 qop[8];
   {
     const char* qp = reinterpret_cast<const char*>(p.q) +
@@ -252,7 +255,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   // add nothing for any of its rows (tokens only grow along the walk), so the
   // walk ends there (uniform across the workgroup)
   const int qrow_end = min(G * S, (int)(blockIdx.y / p.Hkv + 1) * kChunkStage * kChunk32Rows);
-  const int s_last_wg = (qrow_end - 1) / G;
+  const int s_last_wg = (qrow_end - 1) / G + coff;
   bool done = false;
   // stage st computes from `cur` while stage st + 1 loads into `nxt`
   auto stage = [&](int st, const StageBuf& cur, StageBuf& nxt) {
@@ -325,7 +328,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
           if (sv_cur.tok0[bp + 1] + kBlockTok - 1 > s_first) {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-              if (sv_cur.tok0[bp + (r >> 3)] + 8 * hh + (r & 7) > s_row) x[r] = -INFINITY;
+              if (sv_cur.tok0[bp + (r >> 3)] + 8 * hh + (r & 7) > s_vis) x[r] = -INFINITY;
           }
         }
         if (nt0 < kBlockTok || nt1 < kBlockTok) {

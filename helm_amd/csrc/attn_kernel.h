@@ -393,7 +393,8 @@ struct AttnParams {
   float softcap;      // <= 0: off
   const float* mask;  // may be null
   int64_t mask_bstride, mask_hstride, mask_qstride;
-  int causal;         // top-left causal over key positions
+  int causal;         // 0: off; c > 0: position s sees tokens 0 .. s + c - 1
+                      // (1: top-left causal)
   int pps;            // pages per split
   int bpp;            // 16-token blocks per page
   int lo, hi;         // page range of this launch within every sequence
@@ -1210,7 +1211,7 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
       for (int g = 0; g < GM; ++g)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          if (tok_base + B.tok0 + 4 * j + row > srow[g]) sc[g][j] = -INFINITY;
+          if (tok_base + B.tok0 + 4 * j + row > srow[g] + p.causal - 1) sc[g][j] = -INFINITY;
     }
     // online-softmax update; sc becomes the probabilities.  The reference
     // max m is refreshed only when a block max exceeds it by more than

@@ -204,11 +204,12 @@ __device__ __forceinline__ mf_f32x4 mfma_qk(const mf_u32x4 (&k)[4], const mf_u32
   return sc;
 }
 
-// Logits of those four tokens: scale, soft-cap, additive mask, causal limit,
-// and -inf past the block's ntok valid tokens.
+// Logits of those four tokens: scale, soft-cap, additive mask, causal limit
+// (tokens past s_vis, the row's last visible token), and -inf past the
+// block's ntok valid tokens.
 template <bool kMask, bool kCap, bool kCausal>
 __device__ __forceinline__ void mfma_logits(mf_f32x4 sc, const float (&mk)[4], int ntok, int tok0,
-                                            float scale, float cap, float inv_cap, int s_row,
+                                            float scale, float cap, float inv_cap, int s_vis,
                                             int q4, float (&x)[4]) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -216,7 +217,7 @@ __device__ __forceinline__ void mfma_logits(mf_f32x4 sc, const float (&mk)[4], i
     if constexpr (kCap) val = tanhf(val * inv_cap) * cap;
     if constexpr (kMask) val += mk[r];
     if constexpr (kCausal)
-      if (tok0 + 4 * r + q4 > s_row) val = -INFINITY;
+      if (tok0 + 4 * r + q4 > s_vis) val = -INFINITY;
     x[r] = val;
   }
   if (ntok < kBlockTok) {
@@ -282,10 +283,10 @@ __device__ __forceinline__ void mfma_block_step(const mf_u32x4 (&k)[4], const mf
                                                 const float (&mk)[4], int ntok, int tok0,
                                                 const mf_u32x4 (&qop)[4], float& m, float& lsum,
                                                 mf_f32x4 (&o)[8], float scale, float cap,
-                                                float inv_cap, int s_row, int q4) {
+                                                float inv_cap, int s_vis, int q4) {
   float x[4];
   mfma_logits<kMask, kCap, kCausal>(mfma_qk<Ops>(k, qop), mk, ntok, tok0, scale, cap, inv_cap,
-                                    s_row, q4, x);
+                                    s_vis, q4, x);
   mfma_refresh_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), m, lsum, o, q4);
   mfma_pv<Ops>(x, v, m, lsum, o);
 }
@@ -333,6 +334,8 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   const RowCoord rc = row_coord(rr, G);
   const int g_row = rc.g;
   const int s_row = rc.s;
+  // causal: query position s sees tokens 0 .. s + causal - 1
+  const int s_vis = s_row + (kCausal ? p.causal - 1 : 0);
   mf_u32x4 qop[4];
   {
     const int h = hk * G + g_row;
@@ -427,7 +430,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
 
   auto compute_block = [&](const Blk& B) {
     mfma_block_step<Ops, kMask, kCap, kCausal>(B.k, B.v, B.mk, B.ntok, B.tok0, qop, m, lsum, o,
-                                               scale, cap, inv_cap, s_row, q4);
+                                               scale, cap, inv_cap, s_vis, q4);
   };
 
   // ---- main loop: a ring of kMfmaBufs register buffers, kMfmaBufs - 1
@@ -547,6 +550,8 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
   const RowCoord rc = row_coord(rr, G);
   const int g_row = rc.g;
   const int s_row = rc.s;
+  // causal: query position s sees tokens 0 .. s + causal - 1
+  const int s_vis = s_row + (kCausal ? p.causal - 1 : 0);
   mf_u32x4 qop[4];
   {
     const int h = hk * G + g_row;
@@ -700,7 +705,7 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
             for (int r = 0; r < 4; ++r) mk[r] = mcur[j][r];
           }
           mfma_logits<kMask, kCap, kCausal>(mfma_qk<Ops>(k, qop), mk, sv_cur.ntok[j],
-                                            sv_cur.tok0[j], scale, cap, inv_cap, s_row, q4, x[h]);
+                                            sv_cur.tok0[j], scale, cap, inv_cap, s_vis, q4, x[h]);
         }
         mfma_refresh_max(fmaxf(fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3])),
                                fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3]))),

@@ -834,6 +834,7 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
     return fail(HELM_E_INVALID, "null pointer argument");
   if (B <= 0) return fail(HELM_E_INVALID, "B must be positive");
   if (Hkv <= 0 || D <= 0) return fail(HELM_E_INVALID, "bad Hkv / D");
+  if (causal < 0) return fail(HELM_E_INVALID, "causal must be >= 0");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int eb = elem_bytes(kv_dtype);
   const int qb = elem_bytes(q_dtype);
@@ -1088,6 +1089,7 @@ int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
     return fail(HELM_E_INVALID, "null pointer argument");
   if (B <= 0 || Hkv <= 0 || D <= 0 || page_tokens <= 0)
     return fail(HELM_E_INVALID, "bad shape");
+  if (causal < 0) return fail(HELM_E_INVALID, "causal must be >= 0");
   if (B > kSeqArgs)
     return fail(HELM_E_UNSUPPORTED,
                 "more than " + std::to_string(kSeqArgs) + " sequences per call");

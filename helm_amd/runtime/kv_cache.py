@@ -748,17 +748,18 @@ def _contiguous_segments(K: torch.Tensor, V: torch.Tensor, b: int, block: int = 
 
 def _attend(query: torch.Tensor, seqs: Sequence[Sequence[_Segment]], Hkv: int, kv_dtype,
             scale: float, attention_mask: Optional[torch.Tensor], softcap: Optional[float],
-            causal: bool) -> torch.Tensor:
-    """One helm_stream_attn call: query [B,Hq,S,D], seqs[b] = ordered segments."""
+            causal: int) -> torch.Tensor:
+    """One helm_stream_attn call: query [B,Hq,S,D], seqs[b] = ordered segments.
+    causal = c > 0: query position s sees keys 0 .. s + c - 1 (c = 1: top-left)."""
     B = query.size(0)
     n = sum(len(s) for s in seqs)
     arr = np.zeros(n, dtype=_native.PAGE_DTYPE)
     seq_off = np.zeros(B + 1, dtype=np.int32)
     i = 0
     t_max = 0
-    # top-left causal: query row s sees keys 0..s, so keys from q_len on are
-    # masked for every row and their pages need not be read
-    limit = query.size(2) if causal else None
+    # causal: keys from q_len + c - 1 on are masked for every row and their
+    # pages need not be read
+    limit = query.size(2) + int(causal) - 1 if causal else None
     for b, segs in enumerate(seqs):
         tok = 0
         for sg in segs:
@@ -813,7 +814,7 @@ def _query_and_mask(query: torch.Tensor, Hkv: int, kv_dtype, t_max: int,
 
 def _attend_records(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarray, t_max: int,
                     Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
-                    softcap: Optional[float], causal: bool) -> torch.Tensor:
+                    softcap: Optional[float], causal: int) -> torch.Tensor:
     """One helm_stream_attn call over prepared ``helm_page`` records: sequence
     b owns records seq_off[b]:seq_off[b+1] (token offsets per sequence), the
     longest sequence holds t_max tokens."""
@@ -824,14 +825,14 @@ def _attend_records(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarray, t
     _native.call("helm_stream_attn", _engine.get_engine(device), q.data_ptr(), out.data_ptr(),
                  B, Hq, Hkv, S, D, _native.ptr(arr) if n else None, _native.ptr(seq_off),
                  float(scale), float(softcap) if softcap is not None else 0.0, *margs,
-                 1 if causal else 0, _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype),
+                 int(causal), _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype),
                  _engine.stream_ptr(device))
     return out if out.dtype == query.dtype else out.to(query.dtype)
 
 
 def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Sequence[int],
                    Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
-                   softcap: Optional[float], causal: bool) -> torch.Tensor:
+                   softcap: Optional[float], causal: int) -> torch.Tensor:
     """One helm_paged_attn_seqs call: sequence b is layers[b]'s pages, read
     through the layer's device-resident records (uploaded only where they
     changed); lens[b] tokens.  Every page must be device-resident."""
@@ -845,18 +846,20 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
     npages = np.array([len(layer.pages) for layer in layers], dtype=np.int32)
     tokens = np.array(lens, dtype=np.int32)
     if causal:
-        # top-left causal: keys from S on are masked for every row; the pages
+        # causal c: keys from S + c - 1 on are masked for every row; the pages
         # holding only such keys are left out (records are in token order)
+        limit = S + int(causal) - 1
         for b, layer in enumerate(layers):
-            if tokens[b] > S:
-                tokens[b] = S
-                npages[b] = int(np.searchsorted(layer._rec["tok_off"][:npages[b]], S, "left"))
+            if tokens[b] > limit:
+                tokens[b] = limit
+                npages[b] = int(np.searchsorted(layer._rec["tok_off"][:npages[b]], limit,
+                                                "left"))
     page_tokens = max(layer._page_tokens for layer in layers)
     aligned = all(layer._aligned16 for layer in layers)
     _native.call("helm_paged_attn_seqs", eng, q.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
                  _native.ptr(ptrs), _native.ptr(npages), _native.ptr(tokens), page_tokens,
                  1 if aligned else 0, float(scale),
-                 float(softcap) if softcap is not None else 0.0, *margs, 1 if causal else 0,
+                 float(softcap) if softcap is not None else 0.0, *margs, int(causal),
                  _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype), stream)
     return out if out.dtype == query.dtype else out.to(query.dtype)
 

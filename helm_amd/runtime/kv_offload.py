@@ -19,6 +19,7 @@ from __future__ import annotations
 import importlib
 import math
 import os
+import weakref
 from dataclasses import dataclass
 from types import MethodType
 from typing import Optional
@@ -266,7 +267,8 @@ def _prefill_from_records(kvcms, q, layer_idx: int, scale: float,
                           attention_mask: Optional[torch.Tensor], softcap: Optional[float]):
     """What per-item perform_streaming_attention gives for a prefill chunk
     (every active page in token order; top-left causal when unmasked and all
-    pages are on the device, kv_cache.py:562-568), from the layers' records;
+    pages are on the device, kv_cache.py:562-568; an exactly causal chunk mask
+    as causal masking at its offset), from the layers' records;
     None when they cannot serve (the page-list path then runs)."""
     if q.device.type != "cuda" or not _async_kv_prefetch_enabled():
         return None
@@ -283,14 +285,23 @@ def _prefill_from_records(kvcms, q, layer_idx: int, scale: float,
     kv_dtype, Hkv = layers[0]._rec_sig[0], layers[0]._rec_sig[1]
     if any(layer._rec_sig != (kv_dtype, Hkv, D) for layer in layers):
         return None
-    masked = attention_mask is not None or softcap is not None
+    lens = [int(r["tok_off"][-1]) + int(r["used"][-1]) for r in recs]
+    # a chunk mask that is exactly causal after `past` tokens runs as causal
+    # masking at that offset (same result, no mask reads; see
+    # _causal_mask_offset); it covers every cached token, as the mask must
+    causal_mask = 0
+    if attention_mask is not None and attention_mask.shape[-1] >= max(lens):
+        past = _causal_mask_offset(attention_mask, S)
+        if past is not None:
+            attention_mask, causal_mask = None, 1 + past
+    masked = attention_mask is not None or softcap is not None or causal_mask > 0
     host = [layer._n_host > 0 for layer in layers]
     if not masked and any(host) and not all(host):
         return None         # causal differs between items: the page-list path
-    causal = (not masked) and S > 1 and not any(host)
+    # unmasked with every page on the device: Path 1's top-left causal
+    causal = causal_mask or int((not masked) and S > 1 and not any(host))
     for layer in layers:
         _record_prefetch(layer._n_host, layer._host_bytes)
-    lens = [int(r["tok_off"][-1]) + int(r["used"][-1]) for r in recs]
     if B <= _MAX_SEQ_ARGS and not any(host):
         return _attend_layers(q, layers, lens, Hkv, kv_dtype, scale, attention_mask, softcap,
                               causal)
@@ -312,29 +323,38 @@ def _prefill_from_records(kvcms, q, layer_idx: int, scale: float,
     return torch.cat(outs, dim=0)
 
 
-_CAUSAL_MASKS: dict = {}   # (address, shape, strides, dtype, version) -> bool
+_CAUSAL_MASKS: dict = {}   # id(mask) -> (weak reference, signature, past or None)
 
 
-def _is_causal_mask(mask: Optional[torch.Tensor], S: int, T: int) -> bool:
-    """Whether an additive [B, H, S, S] mask is exactly the causal pattern: 0
-    on and below the diagonal, <= -1e4 above it (HF's finfo.min masks in fp32,
-    bf16 or fp16).  Attending under such a mask equals attending with causal
-    masking: every row sees at least its own key, so each masked weight
-    exp(logit + mask - max) underflows to exactly 0, as with -inf.  The answer
-    is remembered per tensor version (the forward passes one mask to every
-    layer), so the check runs once per forward."""
-    if (mask is None or S != T or S < 2 or mask.dim() != 4 or tuple(mask.shape[-2:]) != (S, T)
+def _causal_mask_offset(mask: Optional[torch.Tensor], S: int) -> Optional[int]:
+    """past = T - S when an additive [B, H, S, T] mask is exactly the causal
+    pattern of a prompt chunk after `past` cached tokens: 0 where key
+    j <= past + i, <= -1e4 elsewhere (HF's and HELM's finfo.min masks in fp32,
+    bf16 or fp16, helm/runtime/pipeline_runtime.py:94-113); None otherwise.
+    Attending under such a mask equals attending with causal masking at that
+    offset: every row sees key 0 .. past + i, which come before its masked
+    keys in token order, so each masked weight exp(logit + mask - max)
+    underflows to exactly 0, as with -inf.  The answer is remembered per
+    tensor object and version (the forward passes one mask object to every
+    layer), so the check runs once per forward and chunk.  The entry holds a
+    weak reference: a later mask that reuses a freed mask's memory (same
+    address, shape and a fresh version counter) is a different object and is
+    checked anew."""
+    if (mask is None or S < 2 or mask.dim() != 4 or mask.shape[-2] != S
+            or mask.shape[-1] < S
             or mask.dtype not in (torch.float32, torch.bfloat16, torch.float16)):
-        return False
-    key = (mask.data_ptr(), tuple(mask.shape), tuple(mask.stride()), mask.dtype, mask._version)
-    hit = _CAUSAL_MASKS.get(key)
-    if hit is None:
-        upper = torch.ones(S, T, dtype=torch.bool, device=mask.device).triu_(1)
-        hit = bool(torch.where(upper, mask <= -1e4, mask == 0).all())
-        if len(_CAUSAL_MASKS) > 64:
-            _CAUSAL_MASKS.clear()
-        _CAUSAL_MASKS[key] = hit
-    return hit
+        return None
+    T = mask.shape[-1]
+    sig = (mask.data_ptr(), tuple(mask.shape), tuple(mask.stride()), mask.dtype, mask._version)
+    ent = _CAUSAL_MASKS.get(id(mask))
+    if ent is not None and ent[0]() is mask and ent[1] == sig:
+        return ent[2]
+    upper = torch.ones(S, T, dtype=torch.bool, device=mask.device).triu_(1 + T - S)
+    past = T - S if bool(torch.where(upper, mask <= -1e4, mask == 0).all()) else None
+    if len(_CAUSAL_MASKS) > 64:
+        _CAUSAL_MASKS.clear()
+    _CAUSAL_MASKS[id(mask)] = (weakref.ref(mask), sig, past)
+    return past
 
 
 def _local_attention(q, k, v, scale, attention_mask, softcap=None):
@@ -350,9 +370,11 @@ def _local_attention(q, k, v, scale, attention_mask, softcap=None):
     if k.stride(3) != 1 or k.stride(2) != k.size(3) or v.stride() != k.stride():
         k, v = k.contiguous(), v.contiguous()
     seqs = [_contiguous_segments(k, v, b) for b in range(q.shape[0])]
-    if _is_causal_mask(attention_mask, q.shape[2], k.shape[2]):
-        return _attend(q, seqs, k.shape[1], k.dtype, scale, None, softcap, True)
-    return _attend(q, seqs, k.shape[1], k.dtype, scale, attention_mask, softcap, False)
+    if (attention_mask is not None and attention_mask.shape[-1] == k.shape[2]
+            and _causal_mask_offset(attention_mask, q.shape[2]) == k.shape[2] - q.shape[2]):
+        return _attend(q, seqs, k.shape[1], k.dtype, scale, None, softcap,
+                       1 + k.shape[2] - q.shape[2])
+    return _attend(q, seqs, k.shape[1], k.dtype, scale, attention_mask, softcap, 0)
 
 
 def _apply_softcap(attn_weights: torch.Tensor, softcap: Optional[float]) -> torch.Tensor:

@@ -149,8 +149,12 @@ int helm_paged_decode_attn(const void* q, void* out,
  * `stream` (runs of adjacent host pages become one copy, up to chunk_bytes
  * per chunk), each chunk's attention launch queued right behind its copy,
  * after the launch over the resident pages; the split merge follows, all on
- * `stream`.  causal != 0 applies a top-left causal mask (key t visible to
- * query row s iff t <= s), HELM's is_causal=q_len>1 of Path 1.  A sequence
+ * `stream`.  causal = c > 0 applies a causal mask with offset c - 1 (key t
+ * visible to query position s iff t <= s + c - 1): c = 1 is the top-left
+ * causal mask of HELM's is_causal=q_len>1 (Path 1); c = 1 + past is the
+ * chunk mask of a prefill chunk after `past` cached tokens
+ * (helm/runtime/pipeline_runtime.py:94-113) without reading it; causal < 0
+ * is HELM_E_INVALID.  A sequence
  * with no pages yields zeros.  Staged host pages require B == 1
  * (HELM_E_UNSUPPORTED otherwise).  Environment HELM_AMD_HOST_READ=copy stages
  * every host page, =direct reads every readable one in place. */

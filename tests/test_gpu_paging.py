@@ -1011,8 +1011,8 @@ def test_first_chunk_causal_mask_shortcut_is_exact(mdtype, monkeypatch):
     mask[:, 0][:, torch.ones(S, S, dtype=torch.bool).triu(1)] = torch.finfo(mdtype).min
     mask = mask.to(DEV)
     fast = KO._local_attention(q, k, v, 1 / math.sqrt(D), mask)
-    assert KO._is_causal_mask(mask, S, S)
-    monkeypatch.setattr(KO, "_is_causal_mask", lambda *a: False)
+    assert KO._causal_mask_offset(mask, S) == 0
+    monkeypatch.setattr(KO, "_causal_mask_offset", lambda *a: None)
     slow = KO._local_attention(q, k, v, 1 / math.sqrt(D), mask)
     monkeypatch.undo()
     assert torch.equal(fast, slow)
@@ -1020,8 +1020,93 @@ def test_first_chunk_causal_mask_shortcut_is_exact(mdtype, monkeypatch):
                                    mask=mask[1].double().cpu())
     assert (fast[1].double().cpu() - ref).abs().max().item() <= 1e-2
     mask[1, 0, 5:, 0] = torch.finfo(mdtype).min       # item 1: key 0 padded away
-    assert not KO._is_causal_mask(mask, S, S)
+    assert KO._causal_mask_offset(mask, S) is None
     out = KO._local_attention(q, k, v, 1 / math.sqrt(D), mask)
     ref = A.attention_fp64_batched(q[1].float().cpu(), k[1].float().cpu(), v[1].float().cpu(),
                                    mask=mask[1].double().cpu())
     assert (out[1].double().cpu()[:, 5:] - ref[:, 5:]).abs().max().item() <= 1e-2
+
+
+def _chunk_mask(past, S, dtype, B=1):
+    """HELM's prefill chunk mask (helm/runtime/pipeline_runtime.py:94-113):
+    queries at past .. past + S - 1 see keys 0 .. their own position; finfo.min
+    of the mask's dtype elsewhere."""
+    T = past + S
+    allowed = torch.arange(T)[None, :] <= past + torch.arange(S)[:, None]
+    m = torch.where(allowed, torch.zeros((), dtype=dtype),
+                    torch.full((), torch.finfo(dtype).min, dtype=dtype))
+    return m[None, None].expand(B, 1, S, T).contiguous()
+
+
+@pytest.mark.parametrize("mdtype,cap,evict", [(torch.float32, None, False),
+                                              (torch.bfloat16, None, True),
+                                              (torch.float16, 30.0, False)])
+def test_later_chunk_causal_mask_shortcut_is_exact(mdtype, cap, evict, monkeypatch):
+    """A later prompt chunk (300 queries after 1,037 cached tokens, pages of
+    16, two sequences) under HELM's chunk mask runs as causal masking at
+    offset `past`, with exactly the output of the masked call (soft-cap and
+    host pages too), within tolerance of the fp64 oracle; a mask with one
+    entry changed is not taken for causal."""
+    from helm_amd.runtime import kv_offload as KO
+    B, Hq, kvh, D, P, past, S = 2, 8, 2, 128, 16, 1037, 300
+    T = past + S
+    g = torch.Generator().manual_seed(47)
+    k = torch.randn(B, kvh, T, D, generator=g).bfloat16()
+    v = torch.randn(B, kvh, T, D, generator=g).bfloat16()
+    q = torch.randn(B, Hq, S, D, generator=g).bfloat16()
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=torch.bfloat16)
+    budget = 8 * (2 * kvh * P * D * 2) if evict else 10 ** 12
+    mgrs = [KVCacheManager(a, gpu_high_watermark_bytes=budget) for _ in range(B)]
+    for b in range(B):
+        mgrs[b].append_prefill(0, k[b:b + 1].to(DEV), v[b:b + 1].to(DEV))
+        assert (mgrs[b].layers[0]._n_host > 0) == evict
+    mask = _chunk_mask(past, S, mdtype, B).to(DEV)
+    assert KO._causal_mask_offset(mask, S) == past
+    fast = _stream_prefill_batched(mgrs, q.to(DEV), 0, 1 / math.sqrt(D), attention_mask=mask,
+                                   softcap=cap)
+    monkeypatch.setattr(KO, "_causal_mask_offset", lambda *a: None)
+    slow = _stream_prefill_batched(mgrs, q.to(DEV), 0, 1 / math.sqrt(D), attention_mask=mask,
+                                   softcap=cap)
+    monkeypatch.undo()
+    assert torch.equal(fast, slow)
+    for b in range(B):
+        ref = A.attention_fp64_batched(q[b].float(), k[b].float(), v[b].float(),
+                                       mask=mask[b].double().cpu(), softcap=cap)
+        assert (fast[b].double().cpu() - ref).abs().max().item() <= 1e-2
+    mask[1, 0, 7, past + 8] = 0.0                   # row 7 sees one future key
+    assert KO._causal_mask_offset(mask, S) is None
+    out = _stream_prefill_batched(mgrs, q.to(DEV), 0, 1 / math.sqrt(D), attention_mask=mask,
+                                  softcap=cap)
+    ref = A.attention_fp64_batched(q[1].float(), k[1].float(), v[1].float(),
+                                   mask=mask[1].double().cpu(), softcap=cap)
+    assert (out[1].double().cpu() - ref).abs().max().item() <= 1e-2
+    for m in mgrs:
+        m.clear()
+
+
+@pytest.mark.parametrize("kernel,chunk,S", [("mfma", "32", 4), ("mfma", "32", 40),
+                                            ("mfma", "16", 40), ("valu", "32", 40),
+                                            ("generic", "32", 9)])
+def test_causal_offset_through_the_abi_matches_oracle(kernel, chunk, S, monkeypatch):
+    """helm_stream_attn with causal = 1 + past over a contiguous K/V (query
+    position s sees keys 0 .. s + past) equals the fp64 oracle under the
+    matching additive mask, for an offset that ends inside a page, on every
+    kernel that takes the flag (decode tile: G * S <= 16 rows; the 32- and
+    16-row chunk kernels; the vector-ALU kernels)."""
+    from helm_amd.runtime.kv_cache import _attend, _contiguous_segments
+    monkeypatch.setenv("HELM_AMD_KERNEL", kernel)
+    monkeypatch.setenv("HELM_AMD_CHUNK", chunk)
+    Hq, kvh, D, past = 12, 4, 128, 77
+    T = past + S + 5                                  # 5 keys past every row's limit
+    g = torch.Generator().manual_seed(53)
+    q = torch.randn(1, Hq, S, D, generator=g).half()
+    k = torch.randn(1, kvh, T, D, generator=g).half()
+    v = torch.randn(1, kvh, T, D, generator=g).half()
+    kd, vd = k.to(DEV), v.to(DEV)
+    out = _attend(q.to(DEV), [_contiguous_segments(kd, vd, 0)], kvh, torch.float16, 0.125,
+                  None, None, 1 + past).cpu()
+    allowed = torch.arange(T)[None, :] <= past + torch.arange(S)[:, None]
+    mask = torch.zeros(1, S, T, dtype=torch.float64).masked_fill(~allowed, float("-inf"))
+    ref = A.attention_fp64_batched(q[0].float(), k[0].float(), v[0].float(), scale=0.125,
+                                   mask=mask)
+    assert (out[0].double() - ref).abs().max().item() <= 2e-3

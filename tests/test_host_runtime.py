@@ -398,3 +398,65 @@ def test_layer_page_list_link_follows_the_layer():
     fresh = mgr.iterate_layer_pages(0)
     mgr.clear()
     assert fresh._live_layer() is None and mgr.iterate_layer_pages(0) == []
+
+
+@pytest.mark.parametrize("mdtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_causal_mask_offset_recognises_only_exact_chunk_masks(mdtype):
+    """HELM's chunk mask after `past` cached tokens (pipeline_runtime.py:94-113:
+    key j visible to chunk row i iff j <= past + i, finfo.min elsewhere) is
+    recognised with its offset; first chunks give 0; a diagonal off by one, a
+    finite bias, a padded key, a mask narrower than the chunk and decode
+    (one row) are not taken for causal; an in-place change is noticed."""
+    from helm_amd.runtime.kv_offload import _causal_mask_offset
+    neg = torch.finfo(mdtype).min
+
+    def chunk_mask(past, S, shift=0):
+        T = past + S
+        allowed = torch.arange(T)[None, :] <= past + shift + torch.arange(S)[:, None]
+        return torch.where(allowed, torch.zeros((), dtype=mdtype),
+                           torch.full((), neg, dtype=mdtype))[None, None].contiguous()
+
+    for past, S in [(0, 5), (0, 64), (3, 2), (1037, 300), (4096, 17)]:
+        assert _causal_mask_offset(chunk_mask(past, S), S) == past
+        assert _causal_mask_offset(chunk_mask(past, S).expand(3, 2, S, past + S), S) == past
+    assert _causal_mask_offset(chunk_mask(10, 6, shift=1), 6) is None
+    assert _causal_mask_offset(chunk_mask(10, 6, shift=-1), 6) is None
+    m = chunk_mask(10, 6)
+    m[0, 0, 2, 3] = -1.0                              # a finite bias on a visible key
+    assert _causal_mask_offset(m, 6) is None
+    m = chunk_mask(10, 6)
+    m[0, 0, :, 0] = neg                               # key 0 padded away
+    assert _causal_mask_offset(m, 6) is None
+    assert _causal_mask_offset(torch.zeros(1, 1, 1, 40, dtype=mdtype), 1) is None
+    assert _causal_mask_offset(torch.zeros(1, 1, 6, 4, dtype=mdtype), 6) is None
+    assert _causal_mask_offset(chunk_mask(10, 6)[0], 6) is None      # not 4-D
+    assert _causal_mask_offset(torch.zeros(1, 1, 6, 16, dtype=torch.bool), 6) is None
+    m = chunk_mask(10, 6)
+    assert _causal_mask_offset(m, 6) == 10
+    m[0, 0, 5, 15] = neg                              # in place: the cached answer is dropped
+    assert _causal_mask_offset(m, 6) is None
+
+
+def test_causal_mask_offset_cache_follows_the_tensor_object():
+    """The recognition is cached per mask object: a new mask whose memory and
+    signature match a freed one's (address reuse, fresh version counter) is
+    checked anew, and a view of a recognised mask is checked on its own."""
+    from helm_amd.runtime import kv_offload as KO
+    S, past = 8, 24
+    T = past + S
+    allowed = torch.arange(T)[None, :] <= past + torch.arange(S)[:, None]
+    causal = torch.zeros(1, 1, S, T).masked_fill(~allowed, torch.finfo(torch.float32).min)
+    assert KO._causal_mask_offset(causal, S) == past
+    ptr = causal.data_ptr()
+    buf = causal.view(-1)
+    other = buf.view(1, 1, S, T)                   # same memory, shape and version
+    assert KO._causal_mask_offset(other, S) == past
+    del causal, other
+    # the memory rewritten without a torch version bump, then a new tensor
+    # over it: address, shape, strides, dtype and version (0) all equal the
+    # freed mask's, as with a reused allocation
+    arr = buf.numpy()
+    arr[T - 1] = 0.0                               # row 0 sees the last key
+    fresh = torch.from_numpy(arr).view(1, 1, S, T)
+    assert fresh.data_ptr() == ptr and fresh._version == 0
+    assert KO._causal_mask_offset(fresh, S) is None
