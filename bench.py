@@ -20,7 +20,10 @@ Also measured (extra keys of the one JSON line):
   keeps about 25% of the pages in pinned host RAM;
 * a prefill chunk: 512 query tokens over 32,768 cached tokens of one
   Qwen3-8B-shaped layer under the chunk-causal mask, through the runtime's
-  prefill path (TFLOP/s against the matrix cores' dense bf16 peak).
+  prefill path (TFLOP/s against the matrix cores' dense bf16 peak);
+* HELM's CPU-stage fp16 linear (helm/kernels): one Qwen3-8B layer's
+  decode-step GEMVs on this host's cores, the native GEMV beside HELM's own
+  AVX2 kernel built from its source and HELM's float32 fallback.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -62,6 +65,8 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (PMC byte-count calibration)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill-chunk leg")
+    ap.add_argument("--no-gemv", action="store_true",
+                    help="skip the host-CPU fp16 GEMV leg (HELM's CPU-stage linears)")
     ap.add_argument("--no-full-step", action="store_true",
                     help="skip the 40-layer Qwen3-14B B4 x 64k decode step (64 GB device KV "
                          "budget, and a 32 GB budget that forces eviction)")
@@ -390,6 +395,70 @@ def all_configs(args, torch, W, paged):
     return rows
 
 
+# Qwen3-8B decode-step linears of one layer (out x in): q, k, v, o, gate, up, down
+GEMV_SHAPES = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (12288, 4096),
+               (12288, 4096), (4096, 12288)]
+
+
+def cpu_gemv(args, torch, reps=10, layers=2, seed=7):
+    """HELM's CPU-stage linear (helm/kernels): the decode step's fp16 GEMVs of
+    one Qwen3-8B layer (q/k/v/o/gate/up/down, 386 MB of fp16 weights), two
+    layers' weights rotated so the host caches cannot hold them, on this
+    host's cores.  Timed: the native GEMV here (libhelm_cpu.so); HELM's own
+    AVX2 kernel built from its source (oracle/_ref, when present: the CPU
+    baseline); HELM's fallback when its kernel is unavailable (F.linear in
+    float32, the weight widened every call).  Bound: host DRAM bandwidth
+    (bytes = the weights; x and y are cache resident)."""
+    from helm_amd import kernels
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(seed)
+    Ws = [[(0.02 * torch.randn(n, k, generator=g)).half() for n, k in GEMV_SHAPES]
+          for _ in range(layers)]
+    xs = {k: torch.randn(1, 1, k, generator=g).half() for _, k in GEMV_SHAPES}
+    wbytes = sum(2 * n * k for n, k in GEMV_SHAPES)
+    res = {"workload": "qwen3-8b decode-step linears of one layer: q/k/v/o/gate/up/down, "
+                       f"fp16 weights {wbytes / 1e6:.0f} MB, batch 1, {layers} layers rotated",
+           "threads": threads, "cpu_isa": kernels.isa(), "weight_bytes_per_layer": wbytes}
+
+    def timed(fn, reps):
+        for li in range(layers):
+            fn(Ws[li])
+        t0 = time.perf_counter()
+        for r in range(reps):
+            fn(Ws[r % layers])
+        return (time.perf_counter() - t0) / reps
+
+    if kernels.is_available():
+        dt = timed(lambda ws: [kernels.gemv_fp16(xs[w.shape[1]], w, threads=threads)
+                               for w in ws], reps)
+        res["native"] = {"ms_per_layer": dt * 1e3, "GBs": wbytes / dt / 1e9}
+        # parity spot check on the last layer's down projection
+        from oracle import gemv as O
+        w = Ws[0][-1]
+        x = xs[w.shape[1]]
+        y = kernels.gemv_fp16(x, w, threads=threads).double().numpy()
+        ex = O.gemv_fp64(x.reshape(-1).numpy(), w.numpy())
+        res["native"]["within_oracle_bound"] = bool(
+            (np.abs(y - ex) <= O.error_bound(x.reshape(-1).numpy(), w.numpy())).all())
+    else:
+        res["native"] = {"unavailable": kernels.load_error()}
+    try:
+        from oracle import build_ref
+        ref = build_ref.load()
+    except Exception as e:          # a module built for another torch: say so
+        ref, res["reference_error"] = None, str(e)
+    if ref is not None:
+        os.environ.setdefault("OMP_NUM_THREADS", str(threads))
+        dt = timed(lambda ws: [ref.helm_fp16_linear(xs[w.shape[1]], w) for w in ws], reps)
+        res["reference_kernel"] = {"ms_per_layer": dt * 1e3, "GBs": wbytes / dt / 1e9}
+    dt = timed(lambda ws: [torch.nn.functional.linear(xs[w.shape[1]].float(), w.float()).half()
+                           for w in ws], 2)
+    res["torch_fp32_fallback"] = {"ms_per_layer": dt * 1e3, "GBs": wbytes / dt / 1e9}
+    del Ws
+    return res
+
+
 def cpu_baseline(args, torch, W):
     """The oracle's restatement of HELM's CPU streaming attention (torch CPU)
     on the headline shape; bounded to about args.cpu_seconds."""
@@ -476,6 +545,12 @@ def main():
         log(f"offload {off['ms_per_call']:.3f} ms/call, host link {off['host_link_GBs']:.1f} GB/s "
             f"({off['frac_of_measured_h2d'] * 100:.1f}% of measured {off['measured_h2d_GBs']:.1f})")
 
+    gemv = None
+    if not args.no_gemv:
+        log("cpu gemv: qwen3-8b decode-step linears on host cores (HELM's CPU stages)")
+        gemv = cpu_gemv(args, torch)
+        log(json.dumps(gemv))
+
     cpu = None
     threads = 0
     if not args.no_cpu:
@@ -526,6 +601,7 @@ def main():
         "offload50": off,
         "full_step_40l": full,
         "prefill_chunk": pre,
+        "cpu_gemv": gemv,
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["path2_concat_sdpa"]["GBs"], 3), "unit": "GB/s",
             "cores": threads, "kind": "port",

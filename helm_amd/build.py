@@ -64,8 +64,36 @@ def _compile(hipcc: str, src: Path, obj: Path) -> None:
         print(err, file=sys.stderr)
 
 
+CPU_SRC = PKG / "cpu" / "gemv.cpp"
+CPU_LIB = PKG / "libhelm_cpu.so"
+# host code only: no -march (the library runs on another machine's CPU); the
+# AVX2 / AVX-512 paths carry their own target attributes and are chosen at run
+# time from CPUID
+CPU_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-Wall",
+             f"-I{ROOT / 'include'}"]
+
+
+def build_cpu(verbose: bool = True) -> Path:
+    """Compiles the host-CPU fp16 GEMV (helm_amd/cpu/gemv.cpp) into
+    libhelm_cpu.so with g++; returns its path."""
+    gxx = shutil.which("g++") or shutil.which("c++")
+    if not gxx:
+        raise RuntimeError("g++ not found: needed for libhelm_cpu.so")
+    tmp = CPU_LIB.with_suffix(".so.tmp")
+    res = subprocess.run([gxx, *CPU_FLAGS, str(CPU_SRC), "-o", str(tmp)],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"g++ failed for {CPU_SRC.name}:\n{res.stderr}")
+    os.replace(tmp, CPU_LIB)
+    if verbose:
+        print(f"[helm_amd.build] wrote {CPU_LIB}", flush=True)
+    return CPU_LIB
+
+
 def build(incremental: bool = False, jobs: int | None = None, verbose: bool = True) -> Path:
-    """Compiles every HIP source and links libhelm_amd.so; returns its path."""
+    """Compiles every HIP source and links libhelm_amd.so, and builds
+    libhelm_cpu.so; returns the path of libhelm_amd.so."""
+    build_cpu(verbose=verbose)
     hipcc = _hipcc()
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))

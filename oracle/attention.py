@@ -3,7 +3,7 @@
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
 import this module, and only as the checker (or, in bench.py, as the timed
 CPU baseline).  The product (helm_amd) never imports it and has no CPU
-compute path.
+attention path.
 
 Three independent statements of the same arithmetic:
 
