@@ -1110,3 +1110,38 @@ def test_causal_offset_through_the_abi_matches_oracle(kernel, chunk, S, monkeypa
     ref = A.attention_fp64_batched(q[0].float(), k[0].float(), v[0].float(), scale=0.125,
                                    mask=mask)
     assert (out[0].double() - ref).abs().max().item() <= 2e-3
+
+
+def test_chunk32_rows_that_start_fully_masked_follow_helms_loop():
+    """A 40-row chunk (32-row waves) over 300 cached tokens under a mask whose
+    rows 0-4 are finfo.min everywhere (HELM's loop weighs such a row's keys
+    uniformly: the mean of V) and rows 5-9 finfo.min over their first 100
+    keys (weights of those keys are wiped by the first refresh), the rest
+    chunk-causal: every row matches HELM's loop restated by the oracle."""
+    Hq, kvh, D, P, T, S = 8, 2, 128, 16, 300, 40
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=torch.bfloat16)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    g = torch.Generator().manual_seed(59)
+    k = torch.randn(1, kvh, T, D, generator=g).bfloat16()
+    v = torch.randn(1, kvh, T, D, generator=g).bfloat16()
+    mgr.append_prefill(0, k.to(DEV), v.to(DEV))
+    q = torch.randn(1, Hq, S, D, generator=g).bfloat16()
+    mn = torch.finfo(torch.float32).min
+    pos = T - S + torch.arange(S)
+    mask = torch.where(torch.arange(T)[None, :] <= pos[:, None], torch.zeros(()),
+                       torch.full((), mn))
+    mask[0:5] = mn
+    mask[5:10, :100] = mn
+    mask = mask[None, None]
+    out = _stream_prefill_batched([mgr], q.to(DEV), 0, 1 / math.sqrt(D),
+                                  attention_mask=mask.to(DEV)).cpu()
+    pages = [(k[:, :, t:t + P], v[:, :, t:t + P]) for t in range(0, T, P)]
+    helm = A.online_softmax_pages(q.float(), [(kp.float(), vp.float()) for kp, vp in pages],
+                                  scale=1 / math.sqrt(D), attention_mask=mask)
+    assert (out.float() - helm.float()).abs().max().item() <= 1e-2
+    vmean = v[0].float().mean(1).repeat_interleave(Hq // kvh, 0)       # [Hq, D]
+    assert (out[0, :, 0:5].float() - vmean[:, None]).abs().max().item() <= 1e-2
+    ref = A.attention_fp64_batched(q[0, :, 5:].float(), k[0].float(), v[0].float(),
+                                   mask=mask[0, :, 5:].double(), scale=1 / math.sqrt(D))
+    assert (out[0, :, 5:].double() - ref).abs().max().item() <= 1e-2
+    mgr.clear()
