@@ -441,6 +441,11 @@ def cpu_gemv(args, torch, reps=10, layers=2, seed=7):
         ex = O.gemv_fp64(x.reshape(-1).numpy(), w.numpy())
         res["native"]["within_oracle_bound"] = bool(
             (np.abs(y - ex) <= O.error_bound(x.reshape(-1).numpy(), w.numpy())).all())
+        # a batched decode step of 8 tokens: W read once (HELM: float32 F.linear)
+        x8 = {k: torch.randn(8, k, generator=g).half() for _, k in GEMV_SHAPES}
+        dt = timed(lambda ws: [kernels.gemv_fp16(x8[w.shape[1]], w, threads=threads)
+                               for w in ws], reps)
+        res["native_8_tokens"] = {"ms_per_layer": dt * 1e3, "GBs": wbytes / dt / 1e9}
     else:
         res["native"] = {"unavailable": kernels.load_error()}
     try:

@@ -1,10 +1,10 @@
 """helm_amd.kernels — the fp16 linear of HELM's CPU stages (helm/kernels/__init__.py).
 
 Same surface as HELM's module: ``fp16_linear(input, weight, bias=None)``,
-``patch_cpu_linears(module)``, ``is_available()``, ``load_error()``.  The decode
-step's GEMV (one token: every leading dim 1) runs in libhelm_cpu.so
-(helm_amd/cpu/gemv.cpp: AVX-512 or AVX2 + F16C, fp32 accumulation, bias in
-fp32, one rounding to fp16); more tokens take HELM's float32 GEMM branch,
+``patch_cpu_linears(module)``, ``is_available()``, ``load_error()``.  A decode
+step's GEMV (up to 8 tokens) runs in libhelm_cpu.so (helm_amd/cpu/gemv.cpp:
+AVX-512 or AVX2 + F16C, fp32 accumulation, bias in fp32, one rounding to
+fp16, the weight read once); more tokens take HELM's float32 GEMM branch,
 ``F.linear`` in fp32 then fp16 (helm/kernels/__init__.py:78-82).  As in HELM,
 when the native library cannot be used (not built, or a CPU without AVX2 +
 F16C + FMA) ``is_available()`` is False and every call takes ``F.linear`` —
@@ -49,6 +49,11 @@ def _load():
         lib.helm_cpu_fp16_gemv.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                            ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
                                            ctypes.c_int64, ctypes.c_int]
+        lib.helm_cpu_fp16_gemv_batch.restype = ctypes.c_int
+        lib.helm_cpu_fp16_gemv_batch.argtypes = [ctypes.c_void_p, ctypes.c_void_p,
+                                                 ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                                 ctypes.c_int, ctypes.c_int64, ctypes.c_int64,
+                                                 ctypes.c_int]
         if lib.helm_cpu_isa() == 0:
             _load_error = "this CPU lacks AVX2 + F16C + FMA"
             return
@@ -75,20 +80,27 @@ def isa() -> str:
     return ISA_NAMES[_lib.helm_cpu_isa()] if _lib is not None else "none"
 
 
+MAX_BATCH = 8      # vectors per native call (HELM_CPU_GEMV_MAX_BATCH)
+
+
 def gemv_fp16(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
               threads: int = 0) -> torch.Tensor:
-    """y = fp16(weight @ x + bias) through libhelm_cpu.so: x [K] fp16, weight
-    [N, K] fp16 contiguous, bias [N] fp16 / fp32 or None; returns [N] fp16."""
+    """y = fp16(weight @ x + bias) through libhelm_cpu.so: x [K] or [M, K]
+    fp16 (M <= 8 vectors, W read once), weight [N, K] fp16, bias [N] fp16 /
+    fp32 or None; returns [N] (or [M, N]) fp16."""
     _load()
     if _lib is None:
         raise RuntimeError(f"native fp16 GEMV unavailable: {_load_error}")
     if weight.dim() != 2 or weight.dtype != torch.float16 or weight.device.type != "cpu":
         raise ValueError("weight must be a 2-D fp16 CPU tensor")
     N, K = weight.shape
-    if x.numel() != K or x.dtype != torch.float16 or x.device.type != "cpu":
-        raise ValueError(f"x must be {K} fp16 values on the CPU")
+    if x.dtype != torch.float16 or x.device.type != "cpu" or x.numel() % K or x.numel() == 0:
+        raise ValueError(f"x must hold a multiple of {K} fp16 values on the CPU")
+    M = x.numel() // K
+    if M > MAX_BATCH:
+        raise ValueError(f"at most {MAX_BATCH} vectors per call, got {M}")
     w = weight.contiguous()
-    xv = x.reshape(K).contiguous()
+    xv = x.reshape(M, K).contiguous()
     bdt, bptr, b = 0, None, None
     if bias is not None:
         if bias.numel() != N or bias.device.type != "cpu":
@@ -99,31 +111,33 @@ def gemv_fp16(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor
         else:
             b, bdt = b.float(), 2
         bptr = b.data_ptr()
-    y = torch.empty(N, dtype=torch.float16)
-    rc = _lib.helm_cpu_fp16_gemv(xv.data_ptr(), w.data_ptr(), bptr, bdt, y.data_ptr(), N, K,
-                                 int(threads))
+    y = torch.empty(M, N, dtype=torch.float16)
+    rc = _lib.helm_cpu_fp16_gemv_batch(xv.data_ptr(), w.data_ptr(), bptr, bdt, y.data_ptr(), M,
+                                       N, K, int(threads))
     if rc != 0:
-        raise RuntimeError(f"helm_cpu_fp16_gemv: {_lib.helm_cpu_last_error().decode()}")
-    return y
+        raise RuntimeError(f"helm_cpu_fp16_gemv_batch: {_lib.helm_cpu_last_error().decode()}")
+    return y if x.dim() > 1 else y.reshape(N)
 
 
 def fp16_linear(input: torch.Tensor, weight: torch.Tensor,
                 bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """F.linear for fp16 weights on the CPU (helm/kernels/__init__.py:58-89):
-    one token (all leading dims multiply to 1) runs the native GEMV; more
-    tokens run F.linear in float32 and cast to fp16; anything else (non-fp16,
-    not on the CPU) is plain F.linear."""
+    a decode step (up to 8 tokens: all leading dims multiply to <= 8) runs the
+    native GEMV, W read once; more tokens run F.linear in float32 and cast to
+    fp16 (HELM's branch for every count above 1: the same float32 sums and
+    one rounding, with W widened to float32 each call); anything else
+    (non-fp16, not on the CPU) is plain F.linear."""
     _load()
     if (weight.dtype == torch.float16 and weight.device.type == "cpu"
             and input.dtype == torch.float16):
         b = 1
         for s in input.shape[:-1]:
             b *= s
-        if b == 1 and _lib is not None and not os.environ.get("HELM_DISABLE_AVX"):
+        if b <= MAX_BATCH and _lib is not None and not os.environ.get("HELM_DISABLE_AVX"):
             if input.shape[-1] != weight.shape[1]:
                 raise RuntimeError(f"fp16_linear: input last dim ({input.shape[-1]}) != "
                                    f"weight K ({weight.shape[1]})")
-            y = gemv_fp16(input, weight, bias)
+            y = gemv_fp16(input.reshape(b, -1), weight, bias)
             return y.reshape(*input.shape[:-1], weight.shape[0])
         bias_f32 = bias.float() if bias is not None else None
         return F.linear(input.float(), weight.float(), bias_f32).half()

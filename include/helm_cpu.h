@@ -40,6 +40,19 @@ int helm_cpu_fp16_gemv(const uint16_t* x, const uint16_t* W, const void* bias,
                        int bias_dtype, uint16_t* y, int64_t N, int64_t K,
                        int threads);
 
+/* Up to HELM_CPU_GEMV_MAX_BATCH vectors per call: y[m*N + i] =
+ * fp16( sum_j W[i*K + j] * x[m*K + j]  +  bias[i] ), m in [0, M) — a decode
+ * step of M tokens, each vector rounded exactly as helm_cpu_fp16_gemv rounds it
+ * (the same summation order: a batch equals M single calls bit for bit),
+ * with W read from memory once.  HELM runs more than one token through
+ * F.linear in float32 (helm/kernels/__init__.py:78-82): the same arithmetic
+ * (float32 sums, one rounding), its weight widened to float32 every call.
+ * M outside [1, HELM_CPU_GEMV_MAX_BATCH] is HELM_CPU_E_INVALID. */
+#define HELM_CPU_GEMV_MAX_BATCH 8
+int helm_cpu_fp16_gemv_batch(const uint16_t* x, const uint16_t* W, const void* bias,
+                             int bias_dtype, uint16_t* y, int M, int64_t N, int64_t K,
+                             int threads);
+
 /* Message of the last failed call on this thread. */
 const char* helm_cpu_last_error(void);
 

@@ -200,7 +200,7 @@ def test_patch_cpu_linears():
     assert isinstance(m[2][1], nn.Linear)
     x = torch.randn(1, 1, 64, dtype=torch.float16)
     y = m[0](x)
-    assert torch.equal(y.reshape(-1), kernels.gemv_fp16(x, m[0].weight, m[0].bias))
+    assert torch.equal(y.reshape(-1), kernels.gemv_fp16(x, m[0].weight, m[0].bias).reshape(-1))
     assert "avx=True" in repr(m[0])
 
 
@@ -231,3 +231,43 @@ def test_reference_kernel_within_oracle_bound_and_beside_ours(N, K, bias):
         d = (y.float() - yr.float()).abs()
         ulp = torch.finfo(torch.float16).eps * yr.float().abs().clamp_min(2.0 ** -14)
         assert (d <= ulp).all()
+
+
+# ---- up to 8 tokens per call (a batched decode step) ------------------------------------
+
+@needs_kernel
+@pytest.mark.parametrize("isa", ["auto", "avx2"])
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 7, 8])
+def test_batch_equals_single_calls_and_oracle(M, isa, monkeypatch):
+    """M vectors in one call (W read once): each output row equals the
+    single-vector call on that vector bit for bit (same summation order), and
+    lies within the oracle's bound; odd N and K exercise every tail."""
+    if isa == "avx2":
+        monkeypatch.setenv("HELM_CPU_ISA", "avx2")
+    N, K = 203, 517
+    x, W, b = _rand((M, K), 70 + M), _rand((N, K), 71), _rand((N,), 72)
+    y = kernels.gemv_fp16(x, W, b)
+    assert y.shape == (M, N)
+    for m in range(M):
+        assert torch.equal(y[m], kernels.gemv_fp16(x[m], W, b))
+        _check(y[m], x[m], W, b)
+
+
+@needs_kernel
+def test_fp16_linear_small_batches_native_larger_fp32():
+    """2..8 tokens (any leading shape) take the native GEMV, within the
+    oracle's bound of HELM's float32 branch; 9 tokens take HELM's float32
+    branch exactly."""
+    w, b = _rand((96, 160), 80), _rand((96,), 81)
+    for shape in [(2, 1, 160), (1, 8, 160), (2, 2, 2, 160)]:
+        x = _rand(shape, 82)
+        out = kernels.fp16_linear(x, w, b)
+        assert out.shape == shape[:-1] + (96,)
+        flat = x.reshape(-1, 160)
+        for m in range(flat.shape[0]):
+            _check(out.reshape(-1, 96)[m], flat[m], w, b)
+        assert torch.allclose(out.float(), _ref(x, w, b).float(), atol=2e-2, rtol=1e-2)
+    x9 = _rand((9, 160), 83)
+    assert torch.equal(kernels.fp16_linear(x9, w, b), _ref(x9, w, b))
+    with pytest.raises(ValueError):
+        kernels.gemv_fp16(x9, w)
