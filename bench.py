@@ -429,25 +429,6 @@ def cpu_gemv(args, torch, reps=10, layers=2, seed=7):
             fn(Ws[r % layers])
         return (time.perf_counter() - t0) / reps
 
-    if kernels.is_available():
-        dt = timed(lambda ws: [kernels.gemv_fp16(xs[w.shape[1]], w, threads=threads)
-                               for w in ws], reps)
-        res["native"] = {"ms_per_layer": dt * 1e3, "GBs": wbytes / dt / 1e9}
-        # parity spot check on the last layer's down projection
-        from oracle import gemv as O
-        w = Ws[0][-1]
-        x = xs[w.shape[1]]
-        y = kernels.gemv_fp16(x, w, threads=threads).double().numpy()
-        ex = O.gemv_fp64(x.reshape(-1).numpy(), w.numpy())
-        res["native"]["within_oracle_bound"] = bool(
-            (np.abs(y - ex) <= O.error_bound(x.reshape(-1).numpy(), w.numpy())).all())
-        # a batched decode step of 8 tokens: W read once (HELM: float32 F.linear)
-        x8 = {k: torch.randn(8, k, generator=g).half() for _, k in GEMV_SHAPES}
-        dt = timed(lambda ws: [kernels.gemv_fp16(x8[w.shape[1]], w, threads=threads)
-                               for w in ws], reps)
-        res["native_8_tokens"] = {"ms_per_layer": dt * 1e3, "GBs": wbytes / dt / 1e9}
-    else:
-        res["native"] = {"unavailable": kernels.load_error()}
     try:
         from oracle import build_ref
         ref = build_ref.load()
@@ -455,8 +436,35 @@ def cpu_gemv(args, torch, reps=10, layers=2, seed=7):
         ref, res["reference_error"] = None, str(e)
     if ref is not None:
         os.environ.setdefault("OMP_NUM_THREADS", str(threads))
-        dt = timed(lambda ws: [ref.helm_fp16_linear(xs[w.shape[1]], w) for w in ws], reps)
-        res["reference_kernel"] = {"ms_per_layer": dt * 1e3, "GBs": wbytes / dt / 1e9}
+    # the native GEMV and HELM's kernel timed in turn, three rounds, best of
+    # each (the host is shared: one back-to-back pair can differ by 1.5x)
+    legs = {}
+    if kernels.is_available():
+        x8 = {k: torch.randn(8, k, generator=g).half() for _, k in GEMV_SHAPES}
+        legs["native"] = lambda ws: [kernels.gemv_fp16(xs[w.shape[1]], w, threads=threads)
+                                     for w in ws]
+        legs["native_8_tokens"] = lambda ws: [kernels.gemv_fp16(x8[w.shape[1]], w,
+                                                                threads=threads) for w in ws]
+    else:
+        res["native"] = {"unavailable": kernels.load_error()}
+    if ref is not None:
+        legs["reference_kernel"] = lambda ws: [ref.helm_fp16_linear(xs[w.shape[1]], w)
+                                               for w in ws]
+    best = {}
+    for _ in range(3):
+        for name, fn in legs.items():
+            best[name] = min(best.get(name, float("inf")), timed(fn, reps))
+    for name, dt in best.items():
+        res[name] = {"ms_per_layer": dt * 1e3, "GBs": wbytes / dt / 1e9, "rounds": 3}
+    if kernels.is_available():
+        # parity spot check on the down projection
+        from oracle import gemv as O
+        w = Ws[0][-1]
+        x = xs[w.shape[1]]
+        y = kernels.gemv_fp16(x, w, threads=threads).double().numpy()
+        ex = O.gemv_fp64(x.reshape(-1).numpy(), w.numpy())
+        res["native"]["within_oracle_bound"] = bool(
+            (np.abs(y - ex) <= O.error_bound(x.reshape(-1).numpy(), w.numpy())).all())
     dt = timed(lambda ws: [torch.nn.functional.linear(xs[w.shape[1]].float(), w.float()).half()
                            for w in ws], 2)
     res["torch_fp32_fallback"] = {"ms_per_layer": dt * 1e3, "GBs": wbytes / dt / 1e9}
