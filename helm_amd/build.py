@@ -64,7 +64,7 @@ def _compile(hipcc: str, src: Path, obj: Path) -> None:
         print(err, file=sys.stderr)
 
 
-CPU_SRC = PKG / "cpu" / "gemv.cpp"
+CPU_SRCS = [PKG / "cpu" / "gemv.cpp", PKG / "cpu" / "attn.cpp"]
 CPU_LIB = PKG / "libhelm_cpu.so"
 # host code only: no -march (the library runs on another machine's CPU); the
 # AVX2 / AVX-512 paths carry their own target attributes and are chosen at run
@@ -74,16 +74,17 @@ CPU_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-Wall",
 
 
 def build_cpu(verbose: bool = True) -> Path:
-    """Compiles the host-CPU fp16 GEMV (helm_amd/cpu/gemv.cpp) into
-    libhelm_cpu.so with g++; returns its path."""
+    """Compiles the host-CPU sources (helm_amd/cpu: the fp16 GEMV and the
+    streaming attention of HELM's CPU stages) into libhelm_cpu.so with g++;
+    returns its path."""
     gxx = shutil.which("g++") or shutil.which("c++")
     if not gxx:
         raise RuntimeError("g++ not found: needed for libhelm_cpu.so")
     tmp = CPU_LIB.with_suffix(".so.tmp")
-    res = subprocess.run([gxx, *CPU_FLAGS, str(CPU_SRC), "-o", str(tmp)],
+    res = subprocess.run([gxx, *CPU_FLAGS, *map(str, CPU_SRCS), "-o", str(tmp)],
                          capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"g++ failed for {CPU_SRC.name}:\n{res.stderr}")
+        raise RuntimeError(f"g++ failed for libhelm_cpu.so:\n{res.stderr}")
     os.replace(tmp, CPU_LIB)
     if verbose:
         print(f"[helm_amd.build] wrote {CPU_LIB}", flush=True)

@@ -21,6 +21,7 @@
 // The operation is bound by DRAM bandwidth: N*K*2 bytes of W per call against
 // N*K FMAs.
 #include "helm_cpu.h"
+#include "common.h"
 
 #include <immintrin.h>
 #include <omp.h>
@@ -30,14 +31,38 @@
 #include <string>
 #include <vector>
 
-namespace {
+namespace helm_cpu_internal {
 
+namespace {
 thread_local std::string g_err;
+}  // namespace
 
 int fail(int code, const std::string& msg) {
   g_err = msg;
   return code;
 }
+
+const char* last_error() { return g_err.c_str(); }
+
+int detect_isa() {
+  __builtin_cpu_init();
+  if (!__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma") ||
+      !__builtin_cpu_supports("f16c"))
+    return HELM_CPU_ISA_NONE;
+  const char* cap = std::getenv("HELM_CPU_ISA");
+  if (cap && !std::strcmp(cap, "avx2")) return HELM_CPU_ISA_AVX2;
+  return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+                 __builtin_cpu_supports("avx512vl")
+             ? HELM_CPU_ISA_AVX512
+             : HELM_CPU_ISA_AVX2;
+}
+
+}  // namespace helm_cpu_internal
+
+namespace {
+
+using helm_cpu_internal::detect_isa;
+using helm_cpu_internal::fail;
 
 constexpr int kRows = 4;   // rows per thread-block granule
 
@@ -178,23 +203,13 @@ __attribute__((target("avx2,f16c,fma"))) void finish(const float* acc, const voi
   }
 }
 
-int detect_isa() {
-  __builtin_cpu_init();
-  if (!__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma") ||
-      !__builtin_cpu_supports("f16c"))
-    return HELM_CPU_ISA_NONE;
-  const char* cap = std::getenv("HELM_CPU_ISA");
-  if (cap && !std::strcmp(cap, "avx2")) return HELM_CPU_ISA_AVX2;
-  return __builtin_cpu_supports("avx512f") ? HELM_CPU_ISA_AVX512 : HELM_CPU_ISA_AVX2;
-}
-
 }  // namespace
 
 extern "C" {
 
 int helm_cpu_isa(void) { return detect_isa(); }
 
-const char* helm_cpu_last_error(void) { return g_err.c_str(); }
+const char* helm_cpu_last_error(void) { return helm_cpu_internal::last_error(); }
 
 int helm_cpu_fp16_gemv(const uint16_t* x, const uint16_t* W, const void* bias, int bias_dtype,
                        uint16_t* y, int64_t N, int64_t K, int threads) {

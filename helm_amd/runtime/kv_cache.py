@@ -12,9 +12,11 @@ watermark, oldest-first eviction, contiguous fast path) and
 * attention is ``helm_stream_attn``: split-K HIP kernels over the page list,
   with host pages prefetched through a device staging ring by hipMemcpyAsync
   on the caller's stream, each staged chunk attended right behind its copy
-  (kv_cache.py:405-662).
-
-There is no CPU compute path: a query that is not on a HIP device raises.
+  (kv_cache.py:405-662);
+* a query on the CPU (the attention of HELM's CPU-stage layers) runs
+  ``helm_cpu_stream_attn`` of libhelm_cpu.so, a native host-CPU kernel over
+  the same page records (HELM's masked loop and Path 2 on the CPU,
+  kv_cache.py:531-555, :573-577).  Neither library has a torch fallback.
 """
 from __future__ import annotations
 
@@ -27,7 +29,7 @@ from typing import List, Optional, Sequence
 import numpy as np
 import torch
 
-from helm_amd import _native
+from helm_amd import _cpu_native, _native
 from helm_amd.runtime import engine as _engine
 from helm_amd.runtime.page import KVPage
 
@@ -819,6 +821,9 @@ def _attend_records(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarray, t
     b owns records seq_off[b]:seq_off[b+1] (token offsets per sequence), the
     longest sequence holds t_max tokens."""
     device = query.device
+    if device.type != "cuda":
+        return _attend_records_cpu(query, arr, seq_off, t_max, Hkv, kv_dtype, scale,
+                                   attention_mask, softcap, causal)
     B, Hq, S, D = query.shape
     q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, t_max, attention_mask)
     n = int(seq_off[B])
@@ -827,6 +832,23 @@ def _attend_records(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarray, t
                  float(scale), float(softcap) if softcap is not None else 0.0, *margs,
                  int(causal), _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype),
                  _engine.stream_ptr(device))
+    return out if out.dtype == query.dtype else out.to(query.dtype)
+
+
+def _attend_records_cpu(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarray, t_max: int,
+                        Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
+                        softcap: Optional[float], causal: int) -> torch.Tensor:
+    """``_attend_records`` for a query on the CPU: one helm_cpu_stream_attn
+    call (libhelm_cpu.so) over records whose pages are in host memory, on
+    torch's intra-op thread count."""
+    B, Hq, S, D = query.shape
+    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, t_max, attention_mask)
+    n = int(seq_off[B])
+    _cpu_native.call("helm_cpu_stream_attn", q.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
+                     _native.ptr(arr) if n else None, _native.ptr(seq_off), float(scale),
+                     float(softcap) if softcap is not None else 0.0, *margs, int(causal),
+                     _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype),
+                     torch.get_num_threads())
     return out if out.dtype == query.dtype else out.to(query.dtype)
 
 
@@ -896,12 +918,14 @@ def perform_streaming_attention(
     use top-left causal masking when q_len > 1 (Path 1, :562-568) and mixed
     residency attends all pages unmasked (Path 3, :584-662).  Host pages are
     prefetched through the engine's staging ring, overlapped with the device
-    pages.  The output has the query's shape and dtype.
+    pages.  A query on the CPU runs the host-CPU kernel (Path 2 and the CPU
+    branch of the loop, :531-555, :573-577).  The output has the query's
+    shape and dtype.
     """
     device = query.device
     if scale is None:
         scale = 1.0 / math.sqrt(query.size(-1))
-    if type(pages) is _LayerPages and device.type == "cuda":
+    if type(pages) is _LayerPages:
         out = _attend_layer_pages(query, pages, scale, attention_mask, softcap)
         if out is not None:
             return out
@@ -918,9 +942,8 @@ def perform_streaming_attention(
         _record_prefetch(len(cpu_pages), _cpu_bytes)
 
     if device.type != "cuda":
-        raise RuntimeError(
-            "perform_streaming_attention: the query must be on a HIP device; this library "
-            "implements the GPU attention path only (CPU-stage attention stays HELM's own)")
+        return _cpu_query_attention(query, active_pages, gpu_pages, cpu_pages, scale,
+                                    attention_mask, softcap)
 
     masked = attention_mask is not None or softcap is not None
     if masked:
@@ -952,6 +975,45 @@ def perform_streaming_attention(
     return _attend(query, seqs, Hkv, kv_dtype, scale, attention_mask, softcap, causal)
 
 
+def _on_host(page: KVPage) -> KVPage:
+    """`page` itself when its tensors are in host memory, else a host copy of
+    its used tokens (HELM's loop moves such a page with .to(device))."""
+    if page.k_tensor.device.type != "cuda":
+        return page
+    u = page.used_tokens
+    return KVPage(page.page_id, page.layer_id, page.start_token, u, page.capacity_tokens,
+                  page.k_tensor[:, :, :u, :].cpu(), page.v_tensor[:, :, :u, :].cpu(),
+                  torch.device("cpu"), page.state)
+
+
+def _cpu_query_attention(query: torch.Tensor, active_pages, gpu_pages, cpu_pages, scale: float,
+                         attention_mask: Optional[torch.Tensor], softcap: Optional[float]):
+    """perform_streaming_attention for a query on the CPU (HELM's CPU-stage
+    layers) on the host-CPU kernel.  With a mask or soft-cap: every active
+    page in token order, HELM's loop (kv_cache.py:468-555; a page held on a
+    GPU is first copied to the host, as the loop's .to(device) does).
+    Otherwise HELM's Path 2 over the CPU pages (:573-577: unmasked and not
+    causal, whatever q_len).  Without a mask, a CPU query over GPU-resident
+    pages is HELM's Path 1 or 3, whose torch ops fail across devices: it
+    raises RuntimeError here too."""
+    if attention_mask is not None or softcap is not None:
+        seq_pages = active_pages
+    elif gpu_pages:
+        raise RuntimeError("perform_streaming_attention: a query on the CPU over GPU-resident "
+                           "pages needs a mask or soft-cap (HELM's unmasked paths for it run "
+                           "torch ops across devices)")
+    else:
+        seq_pages = cpu_pages
+    if not seq_pages:
+        return torch.zeros_like(query)
+    seq_pages = [_on_host(p) for p in seq_pages]
+    first = seq_pages[0].k_tensor
+    Hkv, D, kv_dtype = first.size(1), query.size(-1), first.dtype
+    B = query.size(0)
+    seqs = [[_page_segments(p, b, B, Hkv, D, kv_dtype) for p in seq_pages] for b in range(B)]
+    return _attend(query, seqs, Hkv, kv_dtype, scale, attention_mask, softcap, 0)
+
+
 def _attend_layer_pages(query: torch.Tensor, pages: _LayerPages, scale: float,
                         attention_mask: Optional[torch.Tensor], softcap: Optional[float]):
     """perform_streaming_attention over a layer's unchanged page list from
@@ -959,7 +1021,8 @@ def _attend_layer_pages(query: torch.Tensor, pages: _LayerPages, scale: float,
     prefetch counting as the page-by-page branch below, without reading each
     page in Python.  None when the records cannot serve."""
     layer = pages._live_layer()
-    if layer is None or query.size(0) != 1 or not _async_kv_prefetch_enabled():
+    cpu = query.device.type != "cuda"
+    if layer is None or query.size(0) != 1 or (not cpu and not _async_kv_prefetch_enabled()):
         return None
     rec = layer.records()
     n = len(pages)
@@ -970,6 +1033,12 @@ def _attend_layer_pages(query: torch.Tensor, pages: _LayerPages, scale: float,
     t = int(rec["tok_off"][n - 1]) + int(rec["used"][n - 1])
     if t == 0:
         return torch.zeros_like(query)
+    if cpu:
+        # every page in host memory: the loop and Path 2 attend all of them
+        if layer._n_host != n:
+            return None
+        return _attend_records(query, rec, np.array([0, n], dtype=np.int32), t, Hkv, kv_dtype,
+                               scale, attention_mask, softcap, 0)
     host = layer._n_host > 0
     if host:
         _record_prefetch(layer._n_host, layer._host_bytes)

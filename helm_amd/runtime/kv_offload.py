@@ -8,7 +8,11 @@ modules and routes every attention through the HIP paged-attention library:
   otherwise per-item streaming attention with host-page prefetch
   (``_decode_batched``, kv_offload.py:86-186);
 * prefill appends the chunk to the pages; the first chunk attends over its
-  own K/V, later chunks stream over every cached page (kv_offload.py:197-227).
+  own K/V, later chunks stream over every cached page (kv_offload.py:197-227);
+* layers whose tensors are on the CPU (CPU stages of a hybrid plan) keep
+  their pages in host memory and attend on the host-CPU kernel of
+  libhelm_cpu.so, as HELM's patched forwards do on the CPU for every module
+  (kv_offload.py:736-762).
 
 The per-architecture differences of HELM's forwards (kv_offload.py:291-651) —
 where q/k norms apply, Gemma-2's scaling, soft-cap and sliding window — are
@@ -178,7 +182,8 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
     prefetched host pages), without touching each page in Python.  Returns
     None when a layer's records are unusable, so the page-list path runs.
     """
-    if q.device.type != "cuda" or not _async_kv_prefetch_enabled():
+    cpu = q.device.type != "cuda"
+    if not cpu and not _async_kv_prefetch_enabled():
         return None
     layers = [kvcm.layers.get(layer_idx) for kvcm in kvcms]
     recs = []
@@ -199,6 +204,13 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
         [r.view(np.uint64) for r in recs]).view(recs[0].dtype)
     seq_off = np.zeros(bsz + 1, dtype=np.int32)
     np.cumsum([len(r) for r in recs], out=seq_off[1:])
+    if cpu:
+        # a CPU-stage layer: every page in host memory, one host-CPU call for
+        # the batch (HELM's per-item loop or Path 2, kv_offload.py:176-186)
+        if any(layer._n_host != len(layer.pages) for layer in layers):
+            return None
+        return _attend_records(q, arr, seq_off, max(lens), Hkv, kv_dtype, scale,
+                               attention_mask, softcap, False)
     # HELM streams the items that hold host pages one by one and counts each
     # as a prefetch (kv_offload.py:176-186, kv_cache.py:441-447)
     for layer in layers:
@@ -270,7 +282,8 @@ def _prefill_from_records(kvcms, q, layer_idx: int, scale: float,
     pages are on the device, kv_cache.py:562-568; an exactly causal chunk mask
     as causal masking at its offset), from the layers' records;
     None when they cannot serve (the page-list path then runs)."""
-    if q.device.type != "cuda" or not _async_kv_prefetch_enabled():
+    cpu = q.device.type != "cuda"
+    if not cpu and not _async_kv_prefetch_enabled():
         return None
     B, _, S, D = q.shape
     layers = [kvcm.layers.get(layer_idx) for kvcm in kvcms[:B]]
@@ -294,6 +307,17 @@ def _prefill_from_records(kvcms, q, layer_idx: int, scale: float,
         past = _causal_mask_offset(attention_mask, S)
         if past is not None:
             attention_mask, causal_mask = None, 1 + past
+    if cpu:
+        # a CPU-stage layer, every page in host memory: HELM's loop under a
+        # mask, else its Path 2 (unmasked, not causal), in one host-CPU call
+        if any(layer._n_host != len(layer.pages) for layer in layers):
+            return None
+        arr = recs[0] if B == 1 else np.concatenate(
+            [r.view(np.uint64) for r in recs]).view(recs[0].dtype)
+        seq_off = np.zeros(B + 1, dtype=np.int32)
+        np.cumsum([len(r) for r in recs], out=seq_off[1:])
+        return _attend_records(q, arr, seq_off, max(lens), Hkv, kv_dtype, scale, attention_mask,
+                               softcap, causal_mask)
     masked = attention_mask is not None or softcap is not None or causal_mask > 0
     host = [layer._n_host > 0 for layer in layers]
     if not masked and any(host) and not all(host):
@@ -361,8 +385,8 @@ def _local_attention(q, k, v, scale, attention_mask, softcap=None):
     """First prefill chunk: attention over the chunk's own K/V (no pages yet),
     the SDPA / eager call of kv_offload.py:330-338, :605-613.  A mask that is
     exactly causal runs as causal masking (same result; the kernel then skips
-    the keys past each row instead of reading the mask)."""
-    _require_hip(q, "prefill attention")
+    the keys past each row instead of reading the mask).  A query on the CPU
+    (a CPU-stage layer) runs the host-CPU kernel."""
     if attention_mask is not None and attention_mask.dtype == torch.bool:
         attention_mask = torch.zeros(attention_mask.shape, dtype=torch.float32,
                                      device=attention_mask.device).masked_fill_(

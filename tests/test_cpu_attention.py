@@ -1,0 +1,457 @@
+"""The host-CPU streaming attention (libhelm_cpu.so, helm_cpu_stream_attn) —
+the attention of HELM's CPU-stage layers — against the oracle.
+
+CPU only.  Every case is checked against the float64 textbook formula
+(oracle.attention.attention_fp64 / attention_fp64_batched, pinned in
+tests/test_oracle.py) and, where HELM's own arithmetic decides the answer
+(finfo.min masks, soft-cap), against the oracle's restatement of HELM's fp32
+loop (kv_cache.py:468-555) or Path 2 (:573-577).  Tolerances: 1e-5 fp32,
+2e-3 fp16, 1e-2 bf16 (HELM's, test_streaming_attention.py:365).  Both
+instruction-set paths run (HELM_CPU_ISA=avx2 caps the library at AVX2).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helm_amd import _cpu_native, _native
+from helm_amd import workloads as W
+from helm_amd.runtime import kv_cache as KC
+from helm_amd.runtime.kv_allocator import KVAllocator
+from helm_amd.runtime.kv_cache import KVCacheManager, perform_streaming_attention
+from oracle import attention as A
+
+TOL = {torch.float32: 1e-5, torch.float16: 2e-3, torch.bfloat16: 1e-2}
+FINFO_MIN = torch.finfo(torch.float32).min
+
+needs_lib = pytest.mark.skipif(_cpu_native.try_load()[0] is None,
+                               reason="libhelm_cpu.so not built or no AVX2 on this CPU")
+pytestmark = needs_lib
+
+ISAS = ["avx512", "avx2"]
+
+
+@pytest.fixture(params=ISAS)
+def isa(request, monkeypatch):
+    if request.param == "avx2":
+        monkeypatch.setenv("HELM_CPU_ISA", "avx2")
+    elif _cpu_native.isa() != "avx512":
+        pytest.skip("this CPU has no AVX-512")
+    return request.param
+
+
+def _records(pool, table, n_pages, lens, P):
+    """helm_page records of pool slots (the allocator's arena layout
+    [slots, 2, Hkv, P, D]) in page-table order; sequence b owns
+    seq_off[b]:seq_off[b+1]."""
+    es = pool.element_size()
+    recs, seq_off = [], [0]
+    for b, n in enumerate(n_pages):
+        for i in range(n):
+            s = int(table[b, i])
+            used = min(P, lens[b] - i * P)
+            base = pool.data_ptr() + s * pool.stride(0) * es
+            recs.append((base, base + pool.stride(1) * es, used, i * P, pool.stride(2), 0))
+        seq_off.append(len(recs))
+    arr = np.array(recs, dtype=_native.PAGE_DTYPE) if recs else np.zeros(0, _native.PAGE_DTYPE)
+    return arr, np.array(seq_off, dtype=np.int32)
+
+
+def _gather(pool, table, b, n, t):
+    """Sequence b's K and V [Hkv, t, D] in token order (float32)."""
+    slots = table[b, :n].long()
+    K = pool[slots, 0].permute(1, 0, 2, 3).reshape(pool.size(2), -1, pool.size(4))[:, :t]
+    V = pool[slots, 1].permute(1, 0, 2, 3).reshape(pool.size(2), -1, pool.size(4))[:, :t]
+    return K.float(), V.float()
+
+
+def _call(q, arr, seq_off, Hkv, kv_dtype, scale=None, mask=None, softcap=None, causal=0,
+          threads=0):
+    B, Hq, S, D = q.shape
+    out = torch.empty_like(q)
+    mptr, mbs, mhs, mqs = None, 0, 0, 0
+    if mask is not None:
+        mptr = mask.data_ptr()
+        mbs = mask.stride(0) if mask.size(0) > 1 else 0
+        mhs = mask.stride(1) if mask.size(1) > 1 else 0
+        mqs = mask.stride(2) if mask.size(2) > 1 else 0
+    _cpu_native.call("helm_cpu_stream_attn", q.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
+                     _native.ptr(arr) if len(arr) else None, _native.ptr(seq_off),
+                     1.0 / math.sqrt(D) if scale is None else scale,
+                     softcap or 0.0, mptr, mbs, mhs, mqs, causal, _native.dtype_code(kv_dtype),
+                     _native.dtype_code(q.dtype), threads)
+    return out
+
+
+def _case(w, seed, lens=None, S=1):
+    case = W.make_pool_case(w, seed=seed, device="cpu", lens=lens)
+    if S > 1:
+        g = torch.Generator().manual_seed(seed + 1)
+        case["q"] = torch.randn(w.B if lens is None else len(lens), w.Hq, S, w.D,
+                                generator=g).to(w.dtype)
+    arr, seq_off = _records(case["pool"], case["table_cpu"], case["n_pages"], case["lens_list"],
+                            w.page_size)
+    return case, arr, seq_off
+
+
+def _check(case, out, w, mask=None, softcap=None, causal=0, scale=None, tol=None):
+    worst = 0.0
+    for b, t in enumerate(case["lens_list"]):
+        K, V = _gather(case["pool"], case["table_cpu"], b, case["n_pages"][b], t)
+        q = case["q"][b].float()
+        S = q.size(1)
+        m = None if mask is None else mask[b if mask.size(0) > 1 else 0]
+        if causal:
+            cm = torch.zeros(S, t, dtype=torch.float64)
+            cm[torch.arange(t)[None, :] > torch.arange(S)[:, None] + causal - 1] = -math.inf
+            m = cm if m is None else m.double() + cm
+        ref = A.attention_fp64_batched(q, K, V, scale=scale, mask=m, softcap=softcap)
+        worst = max(worst, (out[b].double() - ref).abs().max().item())
+    assert worst <= (tol or TOL[w.dtype]), f"max abs error {worst}"
+    return worst
+
+
+def test_qwen3_0p6b_2k_full_shape(isa):
+    """The Qwen3-0.6B decode shape (16 / 8 heads, fp16, 2,048 tokens in 128
+    pages under a random page table): unmasked (Path 2) and with the
+    production decode mask (zeros, pipeline_runtime.py:79-92)."""
+    w = W.WORKLOADS["qwen3-0.6b-2k"]
+    case, arr, seq_off = _case(w, seed=0)
+    out = _call(case["q"], arr, seq_off, w.Hkv, w.dtype)
+    _check(case, out, w)
+    mask = torch.zeros(1, 1, 1, 2048)
+    out_m = _call(case["q"], arr, seq_off, w.Hkv, w.dtype, mask=mask)
+    assert torch.equal(out, out_m)       # a zero mask adds exact zeros
+
+
+def test_qwen3_0p6b_2k_matches_helm_loop_and_path2():
+    """At the same shape, against the oracle's restatements of HELM's own fp32
+    arithmetic: Path 2 (cat + fp32 SDPA) and the masked loop."""
+    w = W.WORKLOADS["qwen3-0.6b-2k"]
+    case, arr, seq_off = _case(w, seed=3)
+    K, V = _gather(case["pool"], case["table_cpu"], 0, 128, 2048)
+    pages = A.split_pages(K[None].to(w.dtype), V[None].to(w.dtype), [16] * 128)
+    out = _call(case["q"], arr, seq_off, w.Hkv, w.dtype)
+    p2 = A.concat_sdpa(case["q"], pages)
+    mask = torch.zeros(1, 1, 1, 2048)
+    mask[..., 100:400] = FINFO_MIN
+    loop = A.online_softmax_pages(case["q"], pages, attention_mask=mask)
+    out_m = _call(case["q"], arr, seq_off, w.Hkv, w.dtype, mask=mask)
+    # both within one fp16 rounding of HELM's fp32 results
+    assert (out.float() - p2.float()).abs().max().item() <= 2e-3
+    assert (out_m.float() - loop.float()).abs().max().item() <= 2e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Hq,Hkv,D,P", [(4, 2, 8, 16), (8, 8, 64, 16), (5, 1, 80, 64),
+                                        (40, 8, 128, 16), (16, 4, 256, 64), (6, 3, 24, 16)])
+def test_shapes_dtypes_ragged_batch(dtype, Hq, Hkv, D, P, isa):
+    """GQA ratios 1-5, head dims that are and are not multiples of 16, pages
+    of 16 and 64 with partly filled last pages, a ragged batch."""
+    w = W.Workload("t", 3, Hq, Hkv, D, dtype, page_size=P)
+    lens = [1, 37, 300] if D <= 128 else [5, 129, 70]
+    case, arr, seq_off = _case(w, seed=Hq + D + P, lens=lens)
+    out = _call(case["q"], arr, seq_off, Hkv, dtype)
+    _check(case, out, w)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_masks_softcap_and_scale(dtype, isa):
+    """Per-(batch, head, row) additive masks with finfo.min holes, a
+    soft-cap and a custom scale (Gemma-2's path)."""
+    w = W.Workload("t", 2, 8, 2, 64, dtype)
+    case, arr, seq_off = _case(w, seed=9, lens=[70, 45], S=3)
+    g = torch.Generator().manual_seed(10)
+    mask = torch.randn(2, 8, 3, 70, generator=g)
+    mask[torch.rand(2, 8, 3, 70, generator=g) < 0.3] = FINFO_MIN
+    out = _call(case["q"], arr, seq_off, 2, dtype, scale=0.3, mask=mask, softcap=2.5)
+    _check(case, out, w, mask=mask, softcap=2.5, scale=0.3)
+
+
+@pytest.mark.parametrize("causal", [1, 5, 33])
+def test_causal_offsets_prompt_chunks(causal, isa):
+    """causal = 1 + past: a prompt chunk of 24 rows after `past` tokens."""
+    w = W.Workload("t", 2, 8, 4, 32, torch.float32)
+    T = 24 + causal - 1
+    case, arr, seq_off = _case(w, seed=causal, lens=[T, T], S=24)
+    out = _call(case["q"], arr, seq_off, 4, torch.float32, causal=causal)
+    _check(case, out, w, causal=causal)
+
+
+def test_causal_offset_equals_helms_chunk_mask_bit_for_bit():
+    """HELM's chunk mask (finfo.min past key past + i) and causal masking at
+    that offset give identical outputs: every masked weight underflows to 0."""
+    w = W.Workload("t", 1, 8, 2, 64, torch.bfloat16)
+    past, S = 40, 16
+    case, arr, seq_off = _case(w, seed=4, lens=[past + S], S=S)
+    mask = torch.zeros(1, 1, S, past + S)
+    mask[0, 0][torch.arange(past + S)[None, :] > past + torch.arange(S)[:, None]] = FINFO_MIN
+    a = _call(case["q"], arr, seq_off, 2, w.dtype, mask=mask)
+    b = _call(case["q"], arr, seq_off, 2, w.dtype, causal=1 + past)
+    assert torch.equal(a, b)
+
+
+def test_every_key_at_finfo_min_follows_helms_loop():
+    """HELM's loop weighs keys that are all at finfo.min uniformly (mean of V):
+    the logits absorb into finfo.min and exp(0) = 1."""
+    q, pages, K, V = _small(seed=2)
+    arr, seq_off = _page_records(pages)
+    mask = torch.full((1, 1, 1, 8), FINFO_MIN)
+    out = _call(q, arr, seq_off, 2, torch.float32, mask=mask)
+    helm = A.online_softmax_pages(q, pages, attention_mask=mask)
+    torch.testing.assert_close(out, helm, atol=1e-6, rtol=0)
+    # the first page fully masked: it contributes nothing
+    mask[..., 4:] = 0
+    out = _call(q, arr, seq_off, 2, torch.float32, mask=mask)
+    ref = A.attention_fp64(q, K[:, :, 4:], V[:, :, 4:])
+    np.testing.assert_allclose(out.double().numpy(), ref, atol=1e-5)
+
+
+def test_minus_inf_rows_and_empty_sequences_give_zeros():
+    """Keys at -inf add nothing; a row that sees none, and a sequence without
+    pages, give zeros (HELM's zeros_like, kv_cache.py:441-442)."""
+    q, pages, K, V = _small(seed=3)
+    arr, seq_off = _page_records(pages)
+    mask = torch.zeros(1, 1, 1, 8)
+    mask[..., :3] = -math.inf
+    out = _call(q, arr, seq_off, 2, torch.float32, mask=mask)
+    np.testing.assert_allclose(out.double().numpy(),
+                               A.attention_fp64(q, K, V, mask=mask.numpy()), atol=1e-5)
+    mask[...] = -math.inf
+    assert torch.all(_call(q, arr, seq_off, 2, torch.float32, mask=mask) == 0)
+    empty = _call(q.expand(2, -1, -1, -1).contiguous(), arr,
+                  np.array([0, 0, len(arr)], dtype=np.int32), 2, torch.float32)
+    assert torch.all(empty[0] == 0)
+    np.testing.assert_allclose(empty[1:].double().numpy(), A.attention_fp64(q, K, V), atol=1e-5)
+
+
+def test_large_logits_finite():
+    q = torch.ones(1, 1, 1, 64) * 100.0
+    k = torch.ones(1, 1, 8, 64) * 100.0
+    v = torch.randn(1, 1, 8, 64)
+    arr, seq_off = _page_records([(k, v)])
+    out = _call(q, arr, seq_off, 1, torch.float32)
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out[0, 0, 0], v[0, 0].mean(0), atol=1e-5, rtol=0)
+
+
+def test_thread_count_and_splits_do_not_change_beyond_rounding():
+    """Split-K over threads changes only the order of fp32 additions."""
+    w = W.WORKLOADS["qwen3-0.6b-2k"]
+    case, arr, seq_off = _case(w, seed=5)
+    outs = [_call(case["q"], arr, seq_off, w.Hkv, w.dtype, threads=t) for t in (1, 3, 8)]
+    for o in outs[1:]:
+        assert (o.float() - outs[0].float()).abs().max().item() <= 2e-3
+
+
+def test_exp_matches_libm_across_the_range(isa):
+    """The vector exp (Cody-Waite + degree-7 Taylor) seen through the kernel:
+    one key of logit 0 against one of logit x gives weight e^x / (1 + e^x);
+    checked against float64 for x down to the underflow bound."""
+    xs = torch.tensor([0.0, -1e-6, -0.3, -0.69, -1.0, -5.5, -20.0, -40.0, -80.0, -87.0])
+    D = 16
+    q = torch.zeros(len(xs), 1, 1, D)
+    q[:, 0, 0, 0] = 1.0
+    v = torch.zeros(1, 1, 2, D)
+    v[0, 0, 1, 0] = 1.0
+    recs, keep = [], []
+    for x in xs.tolist():
+        k = torch.zeros(1, 1, 2, D)
+        k[0, 0, 1, 0] = x
+        keep.append(k)
+        recs.append((k.data_ptr(), v.data_ptr(), 2, 0, 2 * D, 0))
+    arr = np.array(recs, dtype=_native.PAGE_DTYPE)
+    out = _call(q, arr, np.arange(len(xs) + 1, dtype=np.int32), 1, torch.float32, scale=1.0)
+    got = out[:, 0, 0, 0].double()
+    want = torch.exp(xs.double()) / (1 + torch.exp(xs.double()))
+    assert ((got - want).abs() / want).max().item() <= 4e-7
+
+
+def test_argument_errors():
+    q = torch.zeros(1, 4, 1, 8)
+    arr = np.zeros(0, dtype=_native.PAGE_DTYPE)
+    so = np.zeros(2, dtype=np.int32)
+    with pytest.raises(ValueError, match="multiple"):
+        _call(torch.zeros(1, 3, 1, 8), arr, so, 2, torch.float32)
+    with pytest.raises(ValueError, match="causal"):
+        _call(q, arr, so, 2, torch.float32, causal=-1)
+    bad = np.array([(0, 0, 4, 0, 32, 0)], dtype=_native.PAGE_DTYPE)
+    with pytest.raises(ValueError, match="page 0"):
+        _call(q, bad, np.array([0, 1], dtype=np.int32), 2, torch.float32)
+    with pytest.raises(NotImplementedError, match="512"):
+        _call(torch.zeros(1, 1, 1, 520), arr, so, 1, torch.float32)
+
+
+# ── the runtime surface: perform_streaming_attention with a CPU query ──────────
+def _small(seed, sizes=(4, 4), H=4, kvh=2, D=8):
+    return A_pages(sizes, H, D, seed, kvh)
+
+
+def A_pages(sizes, H, D, seed, kvh):
+    g = torch.Generator().manual_seed(seed)
+    ks = [torch.randn(1, kvh, n, D, generator=g) for n in sizes]
+    vs = [torch.randn(1, kvh, n, D, generator=g) for n in sizes]
+    q = torch.randn(1, H, 1, D, generator=g)
+    return q, list(zip(ks, vs)), torch.cat(ks, 2), torch.cat(vs, 2)
+
+
+def _page_records(pages):
+    recs, t = [], 0
+    for k, v in pages:
+        recs.append((k.data_ptr(), v.data_ptr(), k.size(2), t, k.stride(1), 0))
+        t += k.size(2)
+    return np.array(recs, dtype=_native.PAGE_DTYPE), np.array([0, len(recs)], dtype=np.int32)
+
+
+def _mgr(Hkv, D, dtype, page=16):
+    a = KVAllocator(2, Hkv, D, page_size=page, dtype=dtype)
+    return KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_perform_streaming_attention_cpu_paths(dtype):
+    """A CPU query over CPU pages: no mask -> HELM's Path 2 (not causal even
+    for q_len > 1, kv_cache.py:573-577); a mask or soft-cap -> the loop; the
+    layer page list and a plain list of the same pages agree bit for bit."""
+    g = torch.Generator().manual_seed(1)
+    Hq, Hkv, D, T, S = 8, 2, 32, 150, 3
+    K = torch.randn(1, Hkv, T, D, generator=g).to(dtype)
+    V = torch.randn(1, Hkv, T, D, generator=g).to(dtype)
+    q = torch.randn(1, Hq, S, D, generator=g).to(dtype)
+    mgr = _mgr(Hkv, D, dtype)
+    mgr.append_prefill(0, K, V)
+    pages = mgr.iterate_layer_pages(0)
+    assert all(p.state == "CPU" and p.device.type == "cpu" for p in pages)
+    ref = A.attention_fp64(q.float(), K.float(), V.float())
+    out = perform_streaming_attention(q, pages)
+    assert out.dtype == dtype and out.shape == q.shape
+    assert (out.double() - torch.from_numpy(ref)).abs().max().item() <= TOL[dtype]
+    plain = perform_streaming_attention(q, list(pages))
+    assert torch.equal(out, plain)
+    mask = torch.zeros(1, 1, S, T)
+    mask[..., 10:20] = FINFO_MIN
+    out_m = perform_streaming_attention(q, pages, attention_mask=mask, softcap=3.0)
+    ref_m = A.attention_fp64(q.float(), K.float(), V.float(), mask=mask.numpy(), softcap=3.0)
+    assert (out_m.double() - torch.from_numpy(ref_m)).abs().max().item() <= TOL[dtype]
+    assert torch.equal(out_m, perform_streaming_attention(q, list(pages), attention_mask=mask,
+                                                          softcap=3.0))
+    # CPU queries count no prefetch (kv_cache.py:444-447)
+    KC.reset_paging_stats()
+    perform_streaming_attention(q, pages, attention_mask=mask)
+    assert KC.get_paging_stats()["prefetch_calls"] == 0
+
+
+def test_cpu_query_edge_cases():
+    q = torch.randn(1, 2, 1, 8)
+    assert torch.all(perform_streaming_attention(q, []) == 0)
+    page = KC.KVPage(0, 0, 0, 4, 4, torch.randn(1, 2, 4, 8), torch.randn(1, 2, 4, 8),
+                     torch.device("cpu"), "CPU")
+    empty = KC.KVPage(1, 0, 4, 0, 4, torch.zeros(1, 2, 4, 8), torch.zeros(1, 2, 4, 8),
+                      torch.device("cpu"), "CPU")
+    a = perform_streaming_attention(q, [empty, page])
+    ref = A.attention_fp64(q, page.k_tensor, page.v_tensor)
+    np.testing.assert_allclose(a.double().numpy(), ref, atol=1e-5)
+    # HELM's unmasked paths over GPU-resident pages with a CPU query fail
+    gpu_page = KC.KVPage(2, 0, 0, 4, 4, torch.randn(1, 2, 4, 8), torch.randn(1, 2, 4, 8),
+                         torch.device("cuda"), "GPU")
+    with pytest.raises(RuntimeError, match="GPU-resident"):
+        perform_streaming_attention(q, [gpu_page])
+
+
+def test_batched_decode_and_prefill_on_cpu_layers():
+    """_decode_batched and _stream_prefill_batched for a CPU-stage layer: one
+    host-CPU call for the batch from the layers' records, equal to per-item
+    perform_streaming_attention over the page lists (HELM's per-item path,
+    kv_offload.py:176-186, :207-227)."""
+    from helm_amd.runtime.kv_offload import _decode_batched, _stream_prefill_batched
+    g = torch.Generator().manual_seed(7)
+    Hq, Hkv, D, dtype = 8, 4, 64, torch.bfloat16
+    a = KVAllocator(1, Hkv, D, page_size=16, dtype=dtype)
+    mgrs = [KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12) for _ in range(3)]
+    lens = [40, 17, 64]
+    kvs = []
+    for m, T in zip(mgrs, lens):
+        K = torch.randn(1, Hkv, T, D, generator=g).to(dtype)
+        V = torch.randn(1, Hkv, T, D, generator=g).to(dtype)
+        m.append_prefill(0, K, V)
+        kvs.append((K, V))
+    q = torch.randn(3, Hq, 1, D, generator=g).to(dtype)
+    kn = torch.randn(3, Hkv, 1, D, generator=g).to(dtype)
+    vn = torch.randn(3, Hkv, 1, D, generator=g).to(dtype)
+    T1 = max(lens) + 1
+    mask = torch.zeros(3, 1, 1, T1)
+    mask[1, ..., 18:] = FINFO_MIN         # pad keys of the shorter item
+    mask[2, ..., :5] = FINFO_MIN
+    out = _decode_batched(mgrs, q, kn, vn, 0, 1 / math.sqrt(D), mask)
+    for i in range(3):
+        K = torch.cat([kvs[i][0], kn[i:i + 1]], 2).float()[0]
+        V = torch.cat([kvs[i][1], vn[i:i + 1]], 2).float()[0]
+        ref = A.attention_fp64_batched(q[i].float(), K, V, mask=mask[i, :, :, :lens[i] + 1])
+        assert (out[i].double() - ref).abs().max().item() <= 1e-2
+        item = perform_streaming_attention(q[i:i + 1], list(mgrs[i].iterate_layer_pages(0)),
+                                           scale=1 / math.sqrt(D), attention_mask=mask[i:i + 1])
+        assert (out[i].float() - item[0].float()).abs().max().item() <= 1e-2
+    # a prompt chunk of 5 after the cached tokens, HELM's chunk mask
+    S = 5
+    qc = torch.randn(3, Hq, S, D, generator=g).to(dtype)
+    for m in mgrs:
+        m.append_prefill(0, torch.randn(1, Hkv, S, D, generator=g).to(dtype),
+                         torch.randn(1, Hkv, S, D, generator=g).to(dtype))
+    T2 = max(lens) + 1 + S
+    cm = torch.zeros(3, 1, S, T2)
+    for i, L in enumerate(lens):
+        past = L + 1
+        cm[i, 0][torch.arange(T2)[None, :] > past + torch.arange(S)[:, None]] = FINFO_MIN
+    out = _stream_prefill_batched(mgrs, qc, 0, 1 / math.sqrt(D), cm)
+    for i in range(3):
+        pages = [(p.k_tensor[:, :, :p.used_tokens], p.v_tensor[:, :, :p.used_tokens])
+                 for p in mgrs[i].iterate_layer_pages(0)]
+        K = torch.cat([k for k, _ in pages], 2)[0].float()
+        V = torch.cat([v for _, v in pages], 2)[0].float()
+        n = K.size(1)
+        ref = A.attention_fp64_batched(qc[i].float(), K, V, mask=cm[i, :, :, :n])
+        assert (out[i].double() - ref).abs().max().item() <= 1e-2
+
+
+def test_tiny_llama_on_cpu_greedy_matches_hf():
+    """A tiny random Llama with every layer on the CPU (a plan whose stages
+    are all CPU) generates HF's greedy tokens through the paged cache and the
+    host-CPU attention: prompt in two chunks, then decode."""
+    from transformers.models.llama import LlamaConfig, LlamaForCausalLM
+    from helm_amd.runtime.kv_offload import KVOffloadConfig, KVOffloadManager
+    torch.manual_seed(0)
+    cfg = LlamaConfig(vocab_size=97, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=256)
+    cfg._attn_implementation = "eager"
+    ref_model = LlamaForCausalLM(cfg).eval()
+    model = LlamaForCausalLM(cfg).eval()
+    model.load_state_dict(ref_model.state_dict())
+    conf = KVOffloadConfig.from_model(model, page_size=16)
+    mgr = KVOffloadManager(model, conf, batch_size=1)
+    prompt = torch.randint(0, 97, (1, 21), generator=torch.Generator().manual_seed(1))
+    steps = 24
+    with torch.no_grad():
+        ids = prompt.clone()
+        for _ in range(steps):
+            nxt = ref_model(ids, use_cache=False).logits[:, -1].argmax(-1, keepdim=True)
+            ids = torch.cat([ids, nxt], 1)
+        ref_tokens = ids[0, prompt.shape[1]:].tolist()
+        S, c1 = prompt.shape[1], 13
+        model(prompt[:, :c1], position_ids=torch.arange(c1)[None], use_cache=False)
+        n2 = S - c1
+        cmask = torch.zeros(1, 1, n2, S)
+        cmask[0, 0][torch.arange(S)[None, :] > (c1 + torch.arange(n2))[:, None]] = FINFO_MIN
+        logits = model(prompt[:, c1:], position_ids=torch.arange(c1, S)[None],
+                       attention_mask=cmask, use_cache=False,
+                       cache_position=torch.arange(c1, S)).logits
+        tok = logits[:, -1].argmax(-1, keepdim=True)
+        out_tokens = []
+        for t in range(steps):
+            out_tokens.append(int(tok))
+            pos = S + t
+            logits = model(tok, position_ids=torch.tensor([[pos]]), use_cache=False,
+                           cache_position=torch.tensor([pos])).logits
+            tok = logits[:, -1].argmax(-1, keepdim=True)
+    mgr.restore()
+    assert out_tokens == ref_tokens

@@ -187,21 +187,35 @@ def test_disable_env_takes_the_float32_branch(monkeypatch):
 
 @needs_kernel
 def test_patch_cpu_linears():
-    """Every fp16 CPU nn.Linear (nested too) is wrapped, sharing its
-    parameters; fp32 linears are left alone; decode outputs follow the GEMV."""
+    """Every fp16 CPU nn.Linear (nested too) is routed through the native
+    GEMV in place — same module objects and parameters; fp32 linears are left
+    alone; decode outputs follow the GEMV; a second call routes nothing new."""
     torch.manual_seed(4)
     m = nn.Sequential(nn.Linear(64, 32), nn.ReLU(),
                       nn.Sequential(nn.Linear(32, 16), nn.Linear(16, 8).float()))
     m[0].half()
     m[2][0].half()
-    w0 = m[0].weight
+    lin0, w0 = m[0], m[0].weight
+    keys = list(m.state_dict())
     assert kernels.patch_cpu_linears(m) == 2
-    assert isinstance(m[0], kernels._AVXLinear) and m[0].weight is w0
-    assert isinstance(m[2][1], nn.Linear)
+    assert m[0] is lin0 and type(m[0]) is nn.Linear and m[0].weight is w0
+    assert list(m.state_dict()) == keys
+    assert kernels.patch_cpu_linears(m) == 0
     x = torch.randn(1, 1, 64, dtype=torch.float16)
     y = m[0](x)
     assert torch.equal(y.reshape(-1), kernels.gemv_fp16(x, m[0].weight, m[0].bias).reshape(-1))
-    assert "avx=True" in repr(m[0])
+    # the fp32 linear still runs F.linear; a prefill-sized input takes HELM's fp32 branch
+    xf = torch.randn(3, 16)
+    assert torch.equal(m[2][1](xf), F.linear(xf, m[2][1].weight, m[2][1].bias))
+    xp = torch.randn(2, 9, 64, dtype=torch.float16)
+    assert torch.equal(m[0](xp), F.linear(xp.float(), w0.float(), m[0].bias.float()).half())
+
+
+def test_fp16_linear_empty_input_takes_the_float32_branch():
+    """Zero tokens: F.linear's empty [..., N] result, as HELM gives it."""
+    w = torch.randn(8, 16).half()
+    y = kernels.fp16_linear(torch.zeros(0, 16, dtype=torch.float16), w)
+    assert y.shape == (0, 8) and y.dtype == torch.float16
 
 
 # ---- against HELM's own kernel, built from its source by oracle/build_ref.py ------------

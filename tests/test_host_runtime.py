@@ -216,10 +216,17 @@ def test_paging_counters():
     assert (s["prefetch_calls"], s["pages_prefetched"], s["bytes_prefetched"]) == (1, 4, 4096)
 
 
-def test_cpu_query_has_no_fallback():
+def test_cpu_query_runs_the_host_kernel_without_a_torch_fallback(monkeypatch):
+    """A CPU query attends on libhelm_cpu.so; when that library cannot be
+    used the call raises instead of computing with torch."""
+    from helm_amd import _cpu_native
     q = torch.randn(1, 2, 1, 8)
     page = KC.KVPage(0, 0, 0, 4, 4, torch.randn(1, 2, 4, 8), torch.randn(1, 2, 4, 8), CPU, "CPU")
-    with pytest.raises(RuntimeError, match="HIP device"):
+    out = KC.perform_streaming_attention(q, [page])
+    assert out.shape == q.shape and torch.isfinite(out).all()
+    monkeypatch.setattr(_cpu_native, "_lib", None)
+    monkeypatch.setattr(_cpu_native, "_error", "not built")
+    with pytest.raises(RuntimeError, match="libhelm_cpu.so unavailable"):
         KC.perform_streaming_attention(q, [page])
     # no active pages -> zeros, as HELM
     assert torch.all(KC.perform_streaming_attention(q, []) == 0)
