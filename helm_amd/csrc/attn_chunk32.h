@@ -252,8 +252,9 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
     if (wave_rows) load_step_mask(sv_cur, 0);
   }
   // causal: the workgroup's last query position; stages starting past it
-  // add nothing for any of its rows (tokens only grow along the walk), so the
-  // walk ends there (uniform across the workgroup)
+  // add nothing for any of its rows (a causal call lists a launch's pages in
+  // token order, so tokens only grow along the walk), and the walk ends
+  // there (uniform across the workgroup)
   const int qrow_end = min(G * S, (int)(blockIdx.y / p.Hkv + 1) * kChunkStage * kChunk32Rows);
   const int s_last_wg = (qrow_end - 1) / G + coff;
   bool done = false;
@@ -295,7 +296,8 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
         // logits); masked, every mask value <= -1e30 while every row's max is
         // already above -1e20 (each weight underflows to 0 and the max stays)
         if constexpr (kCausal) {
-          if (sv_cur.tok0[bp] > s_last) continue;
+          if ((nt0 == 0 || sv_cur.tok0[bp] > s_last) && (nt1 == 0 || sv_cur.tok0[bp + 1] > s_last))
+            continue;
         }
         if constexpr (kMask) {
           float mm = mk[0];
@@ -322,10 +324,10 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
           x[r] = val;
         }
         // the per-token limits, only where a step reaches them (uniform tests):
-        // the causal limit when its last token is past the wave's first query
-        // position, the valid-token limit when a block is partial
+        // the causal limit when a block's last token is past the wave's first
+        // query position, the valid-token limit when a block is partial
         if constexpr (kCausal) {
-          if (sv_cur.tok0[bp + 1] + kBlockTok - 1 > s_first) {
+          if (max(sv_cur.tok0[bp], sv_cur.tok0[bp + 1]) + kBlockTok - 1 > s_first) {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
               if (sv_cur.tok0[bp + (r >> 3)] + 8 * hh + (r & 7) > s_vis) x[r] = -INFINITY;

@@ -899,7 +899,7 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   };
 
   // all pages on the device: the caller's records are uploaded as they are
-  const bool as_given = !n_hostflag;
+  bool as_given = !n_hostflag;
   if (!n_host) {
     if (n_hostflag)
       for (int b = 0; b < B; ++b) push_resident(seq_off[b], seq_off[b + 1]);
@@ -962,6 +962,34 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
         desc[i].v += base;
         desc[i].flags = 0;
       }
+    }
+  }
+
+  // ---- token order under causal masking -----------------------------------
+  // The chunk kernel ends a workgroup's page walk at the first block past its
+  // last query position, so a causal call must list each sequence's pages of
+  // a launch in token order.  Staged pages follow host addresses and pages
+  // read in place go first: each launch's range (each sequence's, without
+  // staging) is sorted back by token offset.  The copy runs were planned from
+  // the addresses and do not move.
+  if (causal > 0) {
+    auto by_tok = [](const helm_page& a, const helm_page& b) { return a.tok_off < b.tok_off; };
+    if (as_given) {
+      bool sorted = true;
+      for (int b = 0; b < B && sorted; ++b)
+        for (int i = seq_off[b] + 1; i < seq_off[b + 1] && sorted; ++i)
+          sorted = pages[i - 1].tok_off <= pages[i].tok_off;
+      if (!sorted) {
+        desc.assign(pages, pages + n_all);
+        as_given = false;
+      }
+    }
+    if (!as_given && !n_host) {
+      for (int b = 0; b < B; ++b)
+        std::stable_sort(desc.begin() + off[b], desc.begin() + off[b + 1], by_tok);
+    } else if (n_host) {
+      for (const Launch& L : launches)
+        std::stable_sort(desc.begin() + L.lo, desc.begin() + L.hi, by_tok);
     }
   }
 

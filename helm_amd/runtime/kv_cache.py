@@ -398,6 +398,7 @@ class KVCacheManager:
         self.gpu_high_watermark_bytes = gpu_high_watermark_bytes
         self.cont_K: dict = {}
         self.cont_V: dict = {}
+        self._cont: Optional[ContiguousKV] = None
         self.cont_capacity: int = 0
         self.cont_num_layers: int = 0
         self.cont_seq_len: int = 0
@@ -599,99 +600,175 @@ class KVCacheManager:
                 return False
         return True
 
-    # ── contiguous fast path (kv_cache.py:269-354) ──────────────────────────
+    # ── contiguous fast path (kv_cache.py:267-354) ──────────────────────────
+    # The buffers live in one ContiguousKV arena per manager; cont_K / cont_V
+    # are HELM's per-layer [1, Hkv, capacity, D] views into it.
     def build_contiguous(self, num_layers: int, num_kv_heads: int, head_dim: int,
                          capacity: int, device: torch.device, dtype: torch.dtype) -> bool:
-        cap = capacity
-        floor = max(1, min(capacity, 1024))
-        while cap >= floor:
-            try:
-                self.cont_K.clear()
-                self.cont_V.clear()
-                for lid in range(num_layers):
-                    self.cont_K[lid] = torch.zeros(1, num_kv_heads, cap, head_dim, device=device,
-                                                   dtype=dtype)
-                    self.cont_V[lid] = torch.zeros(1, num_kv_heads, cap, head_dim, device=device,
-                                                   dtype=dtype)
-                self.cont_capacity = cap
-                self.cont_num_layers = num_layers
-                self.use_contiguous = True
-                return True
-            except (torch.cuda.OutOfMemoryError, RuntimeError):
-                self.cont_K.clear()
-                self.cont_V.clear()
-                if device.type == 'cuda':
-                    torch.cuda.empty_cache()
-                cap //= 2
-        self.use_contiguous = False
-        return False
+        """Reserves the contiguous buffers of every layer; on an allocation
+        failure the capacity halves down to min(capacity, 1024) tokens
+        (kv_cache.py:269-299).  True with the capacity reached, else False
+        with the fast path off."""
+        self._cont = None
+        self.cont_K, self.cont_V = {}, {}
+        cont = ContiguousKV.allocate(num_layers, num_kv_heads, head_dim, capacity, device, dtype)
+        self.use_contiguous = cont is not None
+        if cont is None:
+            return False
+        self._cont = cont
+        self.cont_capacity = cont.capacity
+        self.cont_num_layers = num_layers
+        self.cont_K = {lid: cont.k_view(lid) for lid in range(num_layers)}
+        self.cont_V = {lid: cont.v_view(lid) for lid in range(num_layers)}
+        return True
 
     def prefill_contiguous(self, layer_id: int, K: torch.Tensor, V: torch.Tensor):
-        n = K.shape[2]
+        """The prompt's K/V also go to the buffers; layer 0 sets the lengths."""
         self._write_contiguous(layer_id, 0, K, V)
         if layer_id == 0:
-            self.cont_prefill_len = n
-            self.cont_seq_len = n
+            self.cont_prefill_len = self.cont_seq_len = K.shape[2]
 
     def write_decode_contiguous(self, layer_id: int, K_new: torch.Tensor, V_new: torch.Tensor):
+        """One decoded token at position cont_seq_len of the layer's buffers."""
         self._write_contiguous(layer_id, self.cont_seq_len, K_new, V_new)
 
     def _write_contiguous(self, layer_id: int, at: int, K: torch.Tensor, V: torch.Tensor):
+        self._queue_contiguous(layer_id, at, K, V)
+        self._appends.flush()
+
+    def _queue_contiguous(self, layer_id: int, at: int, K: torch.Tensor, V: torch.Tensor):
         dk, dv = self.cont_K[layer_id], self.cont_V[layer_id]
         if dk.device.type == "cuda" and K.device.type == "cuda":
             self._appends.add(dk, dv, at, K, V)
-            self._appends.flush()
         else:
-            n = K.shape[2]
-            dk[:, :, at:at + n, :].copy_(K)
-            dv[:, :, at:at + n, :].copy_(V)
+            self._appends.flush()
+            dk[:, :, at:at + K.shape[2], :].copy_(K)
+            dv[:, :, at:at + V.shape[2], :].copy_(V)
 
     def get_kv_contiguous(self, layer_id: int):
+        """Views of the layer's tokens including the one being decoded."""
         n = self.cont_seq_len + 1
         return self.cont_K[layer_id][:, :, :n, :], self.cont_V[layer_id][:, :, :n, :]
 
     def advance_contiguous(self):
+        """Commits the decoded token (once per step, after the last layer)."""
         self.cont_seq_len += 1
 
     def migrate_contiguous_to_pages(self):
-        if not self.cont_K:
+        """The decoded tokens that only the buffers hold (cont_prefill_len ..
+        cont_seq_len; the prompt went to pages at prefill) become pages of
+        every layer, with the residency policy applied as append_prefill
+        applies it; then the buffers are released (kv_cache.py:325-342)."""
+        cont = self._cont
+        if cont is None:
             return
-        decode_start = self.cont_prefill_len
-        decode_end = self.cont_seq_len
-        if decode_end > decode_start:
-            for layer_id in range(self.cont_num_layers):
-                decode_K = self.cont_K[layer_id][:, :, decode_start:decode_end, :]
-                decode_V = self.cont_V[layer_id][:, :, decode_start:decode_end, :]
-                self.append_prefill(layer_id, decode_K, decode_V)
+        lo, hi = self.cont_prefill_len, self.cont_seq_len
+        for lid in range(self.cont_num_layers if hi > lo else 0):
+            self.append_prefill(lid, cont.k_view(lid)[:, :, lo:hi], cont.v_view(lid)[:, :, lo:hi])
         self.drop_contiguous()
 
     def drop_contiguous(self):
-        self.cont_K.clear()
-        self.cont_V.clear()
+        """Releases the buffers; attention goes back to the pages."""
+        self._appends.flush()
+        self._cont = None
+        self.cont_K, self.cont_V = {}, {}
         self.use_contiguous = False
 
     def reset_contiguous(self):
-        if self.cont_K:
+        """Re-arms kept buffers for the next request (kv_cache.py:351-354)."""
+        if self._cont is not None:
             self.use_contiguous = True
-            self.cont_seq_len = 0
-            self.cont_prefill_len = 0
+            self.cont_seq_len = self.cont_prefill_len = 0
+
+    def contiguous_records(self, layer_id: int):
+        """(device address of the layer's contiguous-buffer records, whether
+        every record is 16-byte aligned) — see ContiguousKV."""
+        return self._cont.records_ptr(layer_id), self._cont.aligned16
 
     def layers_keys(self):
         return sorted(self.layers.keys())
 
     def report_bytes_per_tier(self) -> dict:
-        gpu_bytes = 0
-        cpu_bytes = 0
+        """Whole-page K+V bytes of the GPU- and CPU-resident pages
+        (kv_cache.py:356-375); DEAD placeholders count nowhere."""
+        tally = {"GPU": 0, "CPU": 0}
         for layer in self.layers.values():
             for page in layer.pages:
-                if page.state == 'DEAD':
-                    continue
-                b = _page_bytes(page)
-                if page.state == 'GPU':
-                    gpu_bytes += b
-                elif page.state == 'CPU':
-                    cpu_bytes += b
-        return {"gpu_active_bytes": gpu_bytes, "cpu_active_bytes": cpu_bytes}
+                if page.state in tally:
+                    tally[page.state] += _page_bytes(page)
+        return {"gpu_active_bytes": tally["GPU"], "cpu_active_bytes": tally["CPU"]}
+
+
+class ContiguousKV:
+    """The contiguous cache of one sequence, HELM's Accelerate-style fast path
+    (kv_cache.py:267-354), as one arena [layers, 2, Hkv, capacity, D]: layer
+    l's K is arena[l, 0], its V arena[l, 1].
+
+    The attention kernels read it as pages: each layer's buffer is cut into
+    16-token virtual pages whose ``helm_page`` records are written to device
+    memory once, when the arena is made.  A decode step passes those records
+    and its token count to ``helm_paged_attn_seqs`` (the kernel stops at the
+    token count), so nothing is built or uploaded per call."""
+
+    BLOCK = 16
+
+    def __init__(self, arena: torch.Tensor):
+        self.arena = arena
+        L, _, hkv, cap, d = arena.shape
+        self.capacity = cap
+        self.blocks = -(-cap // self.BLOCK)
+        es = arena.element_size()
+        self.aligned16 = (arena.data_ptr() % 16 == 0 and (arena.stride(1) * es) % 16 == 0
+                          and (cap * d * es) % 16 == 0 and (self.BLOCK * d * es) % 16 == 0)
+        self._rec = None
+        if arena.device.type == "cuda":
+            es = arena.element_size()
+            t = np.arange(self.blocks, dtype=np.int64) * self.BLOCK
+            rec = np.zeros((L, self.blocks), dtype=_native.PAGE_DTYPE)
+            for lid in range(L):
+                kb = arena[lid, 0].data_ptr()
+                vb = arena[lid, 1].data_ptr()
+                rec["k"][lid] = kb + t * d * es
+                rec["v"][lid] = vb + t * d * es
+            rec["used"] = np.minimum(self.BLOCK, cap - t)[None, :]
+            rec["tok_off"] = t[None, :]
+            rec["head_stride"] = cap * d
+            self._rec = torch.from_numpy(rec.view(np.uint8).reshape(-1)).to(arena.device)
+
+    @staticmethod
+    def _new_arena(shape, device: torch.device, dtype: torch.dtype) -> torch.Tensor:
+        if shape[3] * shape[4] >= 1 << 31:
+            raise ValueError("contiguous capacity x head_dim must stay below 2^31 elements")
+        return torch.empty(shape, device=device, dtype=dtype)
+
+    @classmethod
+    def allocate(cls, num_layers: int, num_kv_heads: int, head_dim: int, capacity: int,
+                 device: torch.device, dtype: torch.dtype) -> Optional["ContiguousKV"]:
+        """An arena of `capacity` tokens or, where that allocation fails, of
+        the first of capacity / 2, / 4, ... (not below min(capacity, 1024))
+        that succeeds; None when none does."""
+        floor = max(1, min(capacity, 1024))
+        sizes = []
+        while capacity >= floor:
+            sizes.append(capacity)
+            capacity //= 2
+        for cap in sizes:
+            try:
+                return cls(cls._new_arena((num_layers, 2, num_kv_heads, cap, head_dim),
+                                          device, dtype))
+            except (torch.cuda.OutOfMemoryError, RuntimeError):
+                if device.type == "cuda":
+                    torch.cuda.empty_cache()
+        return None
+
+    def k_view(self, lid: int) -> torch.Tensor:
+        return self.arena[lid, 0].unsqueeze(0)
+
+    def v_view(self, lid: int) -> torch.Tensor:
+        return self.arena[lid, 1].unsqueeze(0)
+
+    def records_ptr(self, lid: int) -> int:
+        return self._rec.data_ptr() + lid * self.blocks * _native.PAGE_DTYPE.itemsize
 
 
 # ── copy stream (kv_cache.py:383-396) ──────────────────────────────────────────
@@ -859,8 +936,6 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
     through the layer's device-resident records (uploaded only where they
     changed); lens[b] tokens.  Every page must be device-resident."""
     device = query.device
-    B, Hq, S, D = query.shape
-    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, max(lens), attention_mask)
     eng = _engine.get_engine(device)
     stream = _engine.stream_ptr(device)
     ptrs = np.array([layer._device_records(device, eng, stream).data_ptr() for layer in layers],
@@ -870,7 +945,7 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
     if causal:
         # causal c: keys from S + c - 1 on are masked for every row; the pages
         # holding only such keys are left out (records are in token order)
-        limit = S + int(causal) - 1
+        limit = query.size(2) + int(causal) - 1
         for b, layer in enumerate(layers):
             if tokens[b] > limit:
                 tokens[b] = limit
@@ -878,11 +953,41 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
                                                 "left"))
     page_tokens = max(layer._page_tokens for layer in layers)
     aligned = all(layer._aligned16 for layer in layers)
-    _native.call("helm_paged_attn_seqs", eng, q.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
-                 _native.ptr(ptrs), _native.ptr(npages), _native.ptr(tokens), page_tokens,
-                 1 if aligned else 0, float(scale),
+    return _attend_device_records(query, ptrs, npages, tokens, page_tokens, aligned, Hkv,
+                                  kv_dtype, scale, attention_mask, softcap, causal)
+
+
+def _attend_device_records(query: torch.Tensor, ptrs: np.ndarray, npages: np.ndarray,
+                           tokens: np.ndarray, page_tokens: int, aligned: bool, Hkv: int,
+                           kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
+                           softcap: Optional[float], causal: int) -> torch.Tensor:
+    """helm_paged_attn_seqs over record arrays already in device memory:
+    sequence b reads npages[b] records at ptrs[b] (token order), tokens[b]
+    tokens; at most 16 sequences per call (more are issued in groups)."""
+    device = query.device
+    B = query.size(0)
+    if B > 16:
+        outs = []
+        for b0 in range(0, B, 16):
+            m = attention_mask
+            if m is not None and m.size(0) > 1:
+                m = m[b0:b0 + 16]
+            outs.append(_attend_device_records(
+                query[b0:b0 + 16], ptrs[b0:b0 + 16], npages[b0:b0 + 16], tokens[b0:b0 + 16],
+                page_tokens, aligned, Hkv, kv_dtype, scale, m, softcap, causal))
+        return torch.cat(outs, 0)
+    _, Hq, S, D = query.shape
+    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, int(tokens.max()),
+                                           attention_mask)
+    ptrs = np.ascontiguousarray(ptrs, dtype=np.uint64)
+    npages = np.ascontiguousarray(npages, dtype=np.int32)
+    tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+    _native.call("helm_paged_attn_seqs", _engine.get_engine(device), q.data_ptr(),
+                 out.data_ptr(), B, Hq, Hkv, S, D, _native.ptr(ptrs), _native.ptr(npages),
+                 _native.ptr(tokens), page_tokens, 1 if aligned else 0, float(scale),
                  float(softcap) if softcap is not None else 0.0, *margs, int(causal),
-                 _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype), stream)
+                 _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype),
+                 _engine.stream_ptr(device))
     return out if out.dtype == query.dtype else out.to(query.dtype)
 
 

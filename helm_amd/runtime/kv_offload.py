@@ -34,10 +34,10 @@ import torch
 from helm_amd import _native
 from helm_amd.runtime import engine as _engine
 from helm_amd.runtime.kv_allocator import KVAllocator
-from helm_amd.runtime.kv_cache import (KVCacheManager, _async_kv_prefetch_enabled, _attend,
-                                       _attend_layers, _attend_records, _contiguous_segments,
-                                       _page_segments, _record_prefetch,
-                                       perform_streaming_attention)
+from helm_amd.runtime.kv_cache import (ContiguousKV, KVCacheManager, _async_kv_prefetch_enabled,
+                                       _attend, _attend_device_records, _attend_layers,
+                                       _attend_records, _contiguous_segments, _page_segments,
+                                       _record_prefetch, perform_streaming_attention)
 
 
 # ── config (kv_offload.py:33-79) ───────────────────────────────────────────────
@@ -99,14 +99,13 @@ def _decode_batched(kvcms, q, k, v, layer_idx: int, scale: float,
     if kvcms[0].use_contiguous:
         if kvcms[0].cont_seq_len < kvcms[0].cont_capacity:
             _require_hip(q, "_decode_batched")
-            for i in range(bsz):
-                kvcms[i].write_decode_contiguous(layer_idx, k[i:i + 1], v[i:i + 1])
-            views = [kvcms[i].get_kv_contiguous(layer_idx) for i in range(bsz)]
+            out = _decode_contiguous(kvcms[:bsz], q, k, v, layer_idx, Hkv, scale,
+                                     attention_mask)
+            # the step's token is committed after the last layer
             if layer_idx == kvcms[0].cont_num_layers - 1:
                 for kvcm in kvcms:
                     kvcm.advance_contiguous()
-            seqs = [_contiguous_segments(K, V, 0) for K, V in views]
-            return _attend(q, seqs, Hkv, views[0][0].dtype, scale, attention_mask, None, False)
+            return out
         for kvcm in kvcms:
             kvcm.migrate_contiguous_to_pages()
 
@@ -117,6 +116,26 @@ def _decode_batched(kvcms, q, k, v, layer_idx: int, scale: float,
         kvcms[i]._enforce_residency_policy()
     _flush_appends([kvcm._appends for kvcm in kvcms])
     return _decode_attend(kvcms, q, layer_idx, Hkv, scale, attention_mask)
+
+
+def _decode_contiguous(kvcms, q, k, v, layer_idx: int, Hkv: int, scale: float,
+                       attention_mask: Optional[torch.Tensor]):
+    """The contiguous fast path of a decode step (kv_offload.py:116-138):
+    every item's token written into its buffers at its position (one append
+    launch), then one attention call over the buffers' device-resident
+    virtual-page records (ContiguousKV), each item over its tokens so far
+    including this one."""
+    for i, kvcm in enumerate(kvcms):
+        kvcm._queue_contiguous(layer_idx, kvcm.cont_seq_len, k[i:i + 1], v[i:i + 1])
+    _flush_appends([kvcm._appends for kvcm in kvcms])
+    recs = [kvcm.contiguous_records(layer_idx) for kvcm in kvcms]
+    ptrs = np.array([r[0] for r in recs], dtype=np.uint64)
+    tokens = np.array([kvcm.cont_seq_len + 1 for kvcm in kvcms], dtype=np.int32)
+    npages = (tokens + ContiguousKV.BLOCK - 1) // ContiguousKV.BLOCK
+    kv_dtype = kvcms[0].cont_K[layer_idx].dtype
+    return _attend_device_records(q, ptrs, npages.astype(np.int32), tokens, ContiguousKV.BLOCK,
+                                  all(r[1] for r in recs), Hkv, kv_dtype, scale, attention_mask,
+                                  None, 0)
 
 
 def _decode_attend(kvcms, q, layer_idx: int, Hkv: int, scale: float,

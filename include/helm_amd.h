@@ -154,7 +154,8 @@ int helm_paged_decode_attn(const void* q, void* out,
  * causal mask of HELM's is_causal=q_len>1 (Path 1); c = 1 + past is the
  * chunk mask of a prefill chunk after `past` cached tokens
  * (helm/runtime/pipeline_runtime.py:94-113) without reading it; causal < 0
- * is HELM_E_INVALID.  A sequence
+ * is HELM_E_INVALID.  Under causal masking the pages of each sequence are
+ * attended in token-offset order whatever their order in `pages`.  A sequence
  * with no pages yields zeros.  Staged host pages require B == 1
  * (HELM_E_UNSUPPORTED otherwise).  Environment HELM_AMD_HOST_READ=copy stages
  * every host page, =direct reads every readable one in place. */

@@ -1145,3 +1145,45 @@ def test_chunk32_rows_that_start_fully_masked_follow_helms_loop():
                                    mask=mask[0, :, 5:].double(), scale=1 / math.sqrt(D))
     assert (out[0, :, 5:].double() - ref).abs().max().item() <= 1e-2
     mgr.clear()
+
+
+@pytest.mark.parametrize("host_mode", ["copy", "direct"])
+def test_causal_chunk_over_host_pages_out_of_token_order(host_mode, monkeypatch):
+    """One sequence whose pages, the prompt chunk's own included, are almost
+    all evicted (watermark 0).  Host slots come LIFO from reserves of 16, so
+    host addresses run against token order inside each reserve, and staged
+    pages are copied in address order.  A 100-row prompt chunk under HELM's
+    chunk mask (run as causal masking at its offset) and the masked call
+    both match the fp64 oracle, whether the host pages are staged or read
+    in place.  (They are not compared bit for bit: the causal call attends
+    the pages in token order, the masked call in descriptor order — staged
+    pages by address, pages read in place ahead of the device pages, among
+    them the prompt's partly filled last page — so their fp32 sums run in
+    different orders.)"""
+    from helm_amd.runtime import kv_offload as KO
+    monkeypatch.setenv("HELM_AMD_HOST_READ", host_mode)
+    Hq, kvh, D, P, past, S = 8, 2, 128, 16, 500, 100
+    T = past + S
+    g = torch.Generator().manual_seed(61)
+    k = torch.randn(1, kvh, T, D, generator=g).bfloat16()
+    v = torch.randn(1, kvh, T, D, generator=g).bfloat16()
+    q = torch.randn(1, Hq, S, D, generator=g).bfloat16()
+    a = KVAllocator(1, kvh, D, page_size=P, dtype=torch.bfloat16)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=0)
+    mgr.append_prefill(0, k[:, :, :past].to(DEV), v[:, :, :past].to(DEV))
+    mgr.append_prefill(0, k[:, :, past:].to(DEV), v[:, :, past:].to(DEV))
+    rec = mgr.layers[0].records()
+    host = rec[(rec["flags"] & _native.HELM_PAGE_HOST) != 0]
+    assert len(host) > 16 and np.any(np.diff(host["k"].astype(np.int64)) < 0)
+    mask = _chunk_mask(past, S, torch.float32).to(DEV)
+    assert KO._causal_mask_offset(mask, S) == past
+    scale = 1 / math.sqrt(D)
+    fast = _stream_prefill_batched([mgr], q.to(DEV), 0, scale, attention_mask=mask)
+    monkeypatch.setattr(KO, "_causal_mask_offset", lambda *a: None)
+    slow = _stream_prefill_batched([mgr], q.to(DEV), 0, scale, attention_mask=mask)
+    monkeypatch.undo()
+    ref = A.attention_fp64_batched(q[0].float(), k[0].float(), v[0].float(),
+                                   mask=mask[0].double().cpu())
+    assert (fast[0].double().cpu() - ref).abs().max().item() <= 1e-2
+    assert (slow[0].double().cpu() - ref).abs().max().item() <= 1e-2
+    mgr.clear()

@@ -179,22 +179,58 @@ def test_build_contiguous_small_capacities():
 def test_build_contiguous_halves_on_oom(monkeypatch):
     # kv_cache.py:277-299: on allocation failure the capacity halves down to
     # a floor of min(capacity, 1024)
-    real = torch.zeros
+    real = KC.ContiguousKV._new_arena
     tried = []
 
-    def flaky(*shape, **kw):
-        tried.append(shape[2])
-        if shape[2] > 1024:
+    def flaky(shape, device, dtype):
+        tried.append(shape[3])
+        if shape[3] > 1024:
             raise RuntimeError("out of memory")
-        return real(*shape, **kw)
+        return real(shape, device, dtype)
 
     a = KVAllocator(num_layers=1, num_kv_heads=2, head_dim=8, page_size=4, dtype=torch.float32)
     m = KVCacheManager(a)
-    monkeypatch.setattr(torch, "zeros", flaky)
+    monkeypatch.setattr(KC.ContiguousKV, "_new_arena", staticmethod(flaky))
     assert m.build_contiguous(1, 2, 8, 4096, CPU, torch.float32)
-    assert m.cont_capacity == 1024 and tried[0] == 4096 and 2048 in tried
-    monkeypatch.setattr(torch, "zeros", lambda *s, **k: (_ for _ in ()).throw(RuntimeError("oom")))
+    assert m.cont_capacity == 1024 and tried == [4096, 2048, 1024]
+    assert m.cont_K[0].shape == (1, 2, 1024, 8) and m.cont_V[0].shape == (1, 2, 1024, 8)
+
+    def oom(shape, device, dtype):
+        raise RuntimeError("oom")
+    monkeypatch.setattr(KC.ContiguousKV, "_new_arena", staticmethod(oom))
     assert not m.build_contiguous(1, 2, 8, 4096, CPU, torch.float32)
+    assert not m.use_contiguous and m.cont_K == {}
+
+
+def test_contiguous_buffers_and_migration_on_cpu():
+    """prefill_contiguous / write_decode_contiguous / get_kv_contiguous /
+    migrate_contiguous_to_pages (kv_cache.py:301-342): the buffers hold the
+    prompt and the decoded tokens; migration appends only the decoded ones to
+    the pages, after which pages hold every token and the buffers are gone."""
+    a = KVAllocator(num_layers=2, num_kv_heads=2, head_dim=8, page_size=4, dtype=torch.float32)
+    m = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 9)
+    assert m.build_contiguous(2, 2, 8, 16, CPU, torch.float32)
+    g = torch.Generator().manual_seed(3)
+    K = torch.randn(1, 2, 13, 8, generator=g)
+    V = torch.randn(1, 2, 13, 8, generator=g)
+    for lid in range(2):
+        m.append_prefill(lid, K[:, :, :10], V[:, :, :10])
+        m.prefill_contiguous(lid, K[:, :, :10], V[:, :, :10])
+    assert (m.cont_prefill_len, m.cont_seq_len) == (10, 10)
+    for t in range(10, 13):
+        for lid in range(2):
+            m.write_decode_contiguous(lid, K[:, :, t:t + 1], V[:, :, t:t + 1])
+            k, v = m.get_kv_contiguous(lid)
+            assert torch.equal(k, K[:, :, :t + 1]) and torch.equal(v, V[:, :, :t + 1])
+        m.advance_contiguous()
+    m.migrate_contiguous_to_pages()
+    assert not m.use_contiguous and m.cont_K == {}
+    for lid in range(2):
+        pages = m.layers[lid].pages
+        assert [p.start_token for p in pages] == [0, 4, 8, 10]
+        k = torch.cat([p.k_tensor[:, :, :p.used_tokens] for p in pages], 2)
+        assert torch.equal(k, K)
+    m.reset_contiguous()             # buffers dropped: stays off
     assert not m.use_contiguous
 
 
