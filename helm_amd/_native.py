@@ -17,6 +17,7 @@ HELM_F16, HELM_BF16, HELM_F32 = 0, 1, 2
 HELM_OK = 0
 HELM_E_INVALID, HELM_E_UNSUPPORTED, HELM_E_WORKSPACE = -1, -2, -3
 HELM_PAGE_HOST = 1
+HELM_STATIC_SCRATCH_BYTES = 16 << 20
 
 # struct helm_page (32 bytes)
 PAGE_DTYPE = np.dtype([
@@ -49,6 +50,11 @@ SIGNATURES = {
         _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32, _f32, _c_void_p, _i64, _i64, _i64,
         ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p, _sz, _c_void_p]),
+    "helm_paged_decode_attn_static": (ctypes.c_int, [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, ctypes.c_int,
+        _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32, _f32, _c_void_p, _i64, _i64, _i64,
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
     "helm_stream_attn": (ctypes.c_int, [
         _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_int, _c_void_p, _c_void_p, _f32, _f32, _c_void_p, _i64, _i64,

@@ -429,7 +429,52 @@ struct helm_engine {
   std::vector<std::pair<uint64_t, uint64_t>> host_ranges;
 };
 
+// ---- the no-allocation entry point's scratch ---------------------------------
+// One array per GPU, in the code object's device memory: it exists from the
+// module's load on that GPU to the end of the process.  Host code reaches it
+// only through the address hipGetSymbolAddress returns for the current
+// device (its name on the host is a stand-in, not a device address).
+static __device__ __align__(256) unsigned char scratch[HELM_STATIC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+bool g_scratch_dirty[kMaxScratchDevices] = {};
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+// The current device's scratch address (looked up once per device), with
+// its ticket region cleared on `st` the first time, and again after a call
+// that may not have completed (the split-merge tickets must start at zero;
+// every completed call leaves them zero).  Allocates nothing.
+int static_scratch(hipStream_t st, int* dev_out, void** out) {
+  int dev = -1;
+  HELM_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(HELM_E_UNSUPPORTED, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    HELM_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[dev] = p;
+    g_scratch_dirty[dev] = true;
+  }
+  if (g_scratch_dirty[dev]) {
+    const int words = static_cast<int>(kTicketRegionBytes / 4);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, st,
+                       static_cast<uint32_t*>(g_scratch_ptr[dev]), words);
+    HELM_HIP(hipGetLastError());
+    g_scratch_dirty[dev] = false;
+  }
+  *dev_out = dev;
+  *out = g_scratch_ptr[dev];
+  return HELM_OK;
+}
 
 int engine_ensure_ws(helm_engine* e, size_t need, hipStream_t st) {
   if (need <= e->ws_bytes) return HELM_OK;
@@ -822,6 +867,39 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
   e = launch_merge(s, B, Hkv, st);
   if (e != hipSuccess) return hip_fail(e, "merge launch");
   return HELM_OK;
+}
+
+int helm_paged_decode_attn_static(const void* q, void* out, const void* k_pool,
+                                  const void* v_pool, int64_t slot_stride,
+                                  int64_t head_stride, const int32_t* page_table,
+                                  int table_stride, const int32_t* seq_lens, int B,
+                                  int Hq, int Hkv, int q_len, int D, int page_size,
+                                  int max_pages, int total_pages, float scale,
+                                  float softcap, const float* mask,
+                                  int64_t mask_bstride, int64_t mask_hstride,
+                                  int64_t mask_qstride, int kv_dtype, int q_dtype,
+                                  int pages_per_split, void* stream) {
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int dev = -1;
+  void* ws = nullptr;
+  int rc = static_scratch(st, &dev, &ws);
+  if (rc != HELM_OK) return rc;
+  rc = helm_paged_decode_attn(q, out, k_pool, v_pool, slot_stride, head_stride, page_table,
+                              table_stride, seq_lens, B, Hq, Hkv, q_len, D, page_size,
+                              max_pages, total_pages, scale, softcap, mask, mask_bstride,
+                              mask_hstride, mask_qstride, kv_dtype, q_dtype, pages_per_split,
+                              ws, HELM_STATIC_SCRATCH_BYTES, stream);
+  if (rc > 0) {
+    // a launch failed part-way: the tickets may not be back at zero
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    g_scratch_dirty[dev] = true;
+  }
+  if (rc == HELM_E_WORKSPACE)
+    return fail(HELM_E_WORKSPACE,
+                "this shape needs more than the static scratch's " +
+                    std::to_string(HELM_STATIC_SCRATCH_BYTES >> 20) +
+                    " MiB (use helm_paged_decode_attn with a workspace)");
+  return rc;
 }
 
 int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,

@@ -135,6 +135,33 @@ int helm_paged_decode_attn(const void* q, void* out,
                            int kv_dtype, int q_dtype, int pages_per_split,
                            void* workspace, size_t ws_bytes, void* stream);
 
+/* The call of helm_paged_decode_attn without a workspace argument, for
+ * callers that cannot allocate device memory: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  It has no
+ * counterpart in the reference.  Its split-merge tickets, split counts and
+ * partials live in a fixed array of HELM_STATIC_SCRATCH_BYTES in the
+ * library's device memory (one per GPU, held from the library's load to the
+ * end of the process); the call allocates nothing, so a shape whose plan
+ * needs more scratch is refused with HELM_E_WORKSPACE.  The caller still
+ * passes every input and output.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other host threads)
+ * race and must be ordered by the caller.  The first call on a GPU (and the
+ * next call after one whose launch failed) first clears the ticket region
+ * with a small kernel on `stream`. */
+#define HELM_STATIC_SCRATCH_BYTES (16u << 20)
+int helm_paged_decode_attn_static(const void* q, void* out,
+                                  const void* k_pool, const void* v_pool,
+                                  int64_t slot_stride, int64_t head_stride,
+                                  const int32_t* page_table, int table_stride,
+                                  const int32_t* seq_lens,
+                                  int B, int Hq, int Hkv, int q_len, int D,
+                                  int page_size, int max_pages, int total_pages,
+                                  float scale, float softcap,
+                                  const float* mask, int64_t mask_bstride,
+                                  int64_t mask_hstride, int64_t mask_qstride,
+                                  int kv_dtype, int q_dtype, int pages_per_split,
+                                  void* stream);
+
 /* Streaming attention over explicit page lists with mixed residency — the
  * drop-in for perform_streaming_attention (helm/runtime/kv_cache.py:405-662),
  * all four paths.  `pages` (host array) holds the active pages of every
