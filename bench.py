@@ -23,7 +23,17 @@ Also measured (extra keys of the one JSON line):
   prefill path (TFLOP/s against the matrix cores' dense bf16 peak);
 * HELM's CPU-stage fp16 linear (helm/kernels): one Qwen3-8B layer's
   decode-step GEMVs on this host's cores, the native GEMV beside HELM's own
-  AVX2 kernel built from its source and HELM's float32 fallback.
+  AVX2 kernel built from its source and HELM's float32 fallback;
+* the headline shape under HELM's decode mask (zeros [1,1,1,T]), the mask
+  every production decode step passes;
+* the other configurations at their stated shapes: Qwen3-0.6B 2k (fp16),
+  Qwen3-14B B8 ragged 4k-32k, Llama-2-13B 128k with 75% of its pages in
+  pinned host RAM — time, GB/s, roofline fraction, error against fp64;
+* the production decode call (``_decode_batched``: append, residency,
+  attention) on the Qwen3-8B 32k shape, masked and unmasked, and the
+  40-layer step under the decode mask;
+* Qwen3-0.6B 2k on the host CPU path, HELM's CPU-stage attention: the native
+  host kernel beside the oracle's restatement of HELM's torch code.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -73,15 +83,22 @@ def parse():
     ap.add_argument("--full-step-steps", type=int, default=64)
     ap.add_argument("--full-step-budgets", default="64,32",
                     help="device KV budgets (GB) of the full-step runs")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the qwen3-0.6b / qwen3-14b ragged / llama2-13b 128k legs")
+    ap.add_argument("--no-runtime", action="store_true",
+                    help="skip the _decode_batched production-call leg")
     ap.add_argument("--all", action="store_true",
                     help="also measure every benchmark configuration (gpurun_out/bench_all.json)")
     return ap.parse_args()
 
 
-def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=None, steps=None):
+def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=None, steps=None,
+                 masked=False):
     """Pool-layout decode attention of one workload, all pages resident.
     Pools are rotated so that at least 1 GiB of KV passes between two reads
-    of the same pool (the 256 MB Infinity Cache cannot serve it)."""
+    of the same pool (the 256 MB Infinity Cache cannot serve it).  masked:
+    HELM's decode mask, zeros [B, 1, 1, T] (pipeline_runtime.py:79-92), the
+    mask every production decode step passes."""
     w = W.WORKLOADS[name]
     dev = torch.device("cuda:0")
     case = W.make_pool_case(w, seed=seed, device=dev)
@@ -94,9 +111,11 @@ def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=Non
     alg = W.algorithmic_bytes(w, lens)
     # argument list built once: a step is one C-ABI call (decode kernel +
     # split merge) on torch's current stream, over the next rotated pool
+    mask = (torch.zeros(w.B, 1, 1, max(lens), device=dev) if masked else None)
     prep = paged.prepare_paged_decode(case["q"], case["k_pool"], case["v_pool"], case["table"],
                                       case["lens"], max_pages=case["max_pages"],
-                                      total_pages=sum(case["n_pages"]), pages_per_split=args.pps)
+                                      total_pages=sum(case["n_pages"]), pages_per_split=args.pps,
+                                      attention_mask=mask)
     views = [(p[:, 0], p[:, 1]) for p in pools]
 
     def step(i):
@@ -142,7 +161,8 @@ def h2d_peak(torch):
     return best
 
 
-def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=None):
+def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=None,
+                check_heads=None):
     """The oldest offload_frac of the context in pinned host pages, streamed
     through the engine's staging ring while the resident pages are attended."""
     from helm_amd import _native
@@ -208,10 +228,13 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
     peak = h2d_peak(torch)
     # parity spot check of this exact configuration against the oracle
     from oracle.attention import attention_fp64_batched
-    K = case["pool"][table.to(dev), 0].permute(1, 0, 2, 3).reshape(w.Hkv, -1, w.D).cpu()
-    V = case["pool"][table.to(dev), 1].permute(1, 0, 2, 3).reshape(w.Hkv, -1, w.D).cpu()
-    ref = attention_fp64_batched(case["q"][0].cpu(), K, V)
-    err = (out[0].double().cpu() - ref).abs().max().item()
+    err = 0.0
+    for kvh in (check_heads if check_heads is not None else range(w.Hkv)):
+        K = case["pool"][table.to(dev), 0, kvh].reshape(-1, w.D)[None].cpu()
+        V = case["pool"][table.to(dev), 1, kvh].reshape(-1, w.D)[None].cpu()
+        hs = slice(kvh * w.G, (kvh + 1) * w.G)
+        ref = attention_fp64_batched(case["q"][0, hs].cpu(), K, V)
+        err = max(err, (out[0, hs].double().cpu() - ref).abs().max().item())
     return {
         "host_pages": n_host, "host_bytes": host_bytes, "ms_per_call": per * 1e3,
         "host_link_GBs": host_bytes / per / 1e9, "measured_h2d_GBs": peak,
@@ -227,7 +250,8 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
     }
 
 
-def gpu_full_step(args, torch, W, budget_gb, steps, name="qwen3-14b-40l-b4-64k", seed=5):
+def gpu_full_step(args, torch, W, budget_gb, steps, name="qwen3-14b-40l-b4-64k", seed=5,
+                  masked_steps=0):
     """The 40-layer Qwen3-14B decode step through HELM's runtime API.
 
     Four sequences of 65,536 tokens per layer in 16-token pages taken from a
@@ -237,7 +261,9 @@ def gpu_full_step(args, torch, W, budget_gb, steps, name="qwen3-14b-40l-b4-64k",
     the 40 layers, ``_decode_batched``: append each sequence's new token (a
     fresh page every 16 tokens), enforce the residency watermark (evicting the
     oldest full pages to pinned host RAM when over budget), and attend over
-    every page (host pages streamed back through the staging ring).
+    every page (host pages streamed back through the staging ring).  Then
+    `masked_steps` more steps under the pipeline's decode mask, zeros
+    [B, 1, 1, T] (pipeline_runtime.py:79-92, :217): HELM's production path.
     """
     import random
     from helm_amd.runtime import kv_cache as KC
@@ -290,6 +316,22 @@ def gpu_full_step(args, torch, W, budget_gb, steps, name="qwen3-14b-40l-b4-64k",
     wall = time.perf_counter() - t0
     gpu_s = e0.elapsed_time(e1) / 1e3
     stats = KC.get_paging_stats()
+    masked = None
+    if masked_steps:
+        zeros = torch.zeros(B, 1, 1, w.T + warmup + steps + masked_steps + 2, device=dev)
+        torch.cuda.synchronize()
+        tm = time.perf_counter()
+        for s in range(masked_steps):
+            mask = zeros[..., :kvcms[0].layers[0].total_tokens + 1]
+            for layer in range(L):
+                out = _decode_batched(kvcms, q[layer], kn[layer], vn[layer], layer, scale, mask)
+        torch.cuda.synchronize()
+        wm = time.perf_counter() - tm
+        ctx_m = w.T + warmup + steps + masked_steps
+        kv_m = L * B * (ctx_m - (masked_steps - 1) / 2) * w.token_bytes()
+        masked = {"steps": masked_steps, "steps_per_s": masked_steps / wm,
+                  "ms_per_step": wm * 1e3 / masked_steps, "kv_GBs": kv_m * masked_steps / wm / 1e9,
+                  "mask": "zeros [B, 1, 1, T] (HELM's decode mask)"}
     # spot check: the last layer's output of the last step against the oracle
     from oracle.attention import attention_fp64_batched
     pages = kvcms[0].layers[L - 1].pages
@@ -297,9 +339,9 @@ def gpu_full_step(args, torch, W, budget_gb, steps, name="qwen3-14b-40l-b4-64k",
     V = torch.cat([p.v_tensor[0, :, :p.used_tokens].cpu() for p in pages], 1)
     ref = attention_fp64_batched(q[L - 1, 0].cpu(), K, V)
     err = (out[0].double().cpu() - ref).abs().max().item()
-    ctx = w.T + warmup + steps
+    ctx = w.T + warmup + steps + masked_steps
     # KV read per step: the mean context over the timed steps
-    kv_step = L * B * (ctx - (steps - 1) / 2) * w.token_bytes()
+    kv_step = L * B * (w.T + warmup + steps - (steps - 1) / 2) * w.token_bytes()
     host_pages = sum(layer._n_host for m in kvcms for layer in m.layers.values())
     res = {
         "workload": f"{name}: 40 layers x (append + decode attention), B={B}, Hq={w.Hq}, "
@@ -314,6 +356,7 @@ def gpu_full_step(args, torch, W, budget_gb, steps, name="qwen3-14b-40l-b4-64k",
         "evicted_in_setup": prefill_stats["pages_evicted"],
         "paging_stats_timed": stats,
         "setup_s": setup_s, "max_abs_err_vs_fp64": err,
+        "masked_production_decode": masked,
     }
     del kvcms, alloc, q, kn, vn, out
     torch.cuda.empty_cache()
@@ -395,6 +438,220 @@ def all_configs(args, torch, W, paged):
     return rows
 
 
+def pool_error(torch, h, heads):
+    """max |out - fp64| of a pool-layout leg's last call (all pools hold the
+    same data), over the query heads of the given KV heads of every sequence."""
+    from oracle.attention import attention_fp64_batched
+    w, case, out = h["w"], h["case"], h["prep"].out
+    G = w.Hq // w.Hkv
+    worst = 0.0
+    for b, t in enumerate(case["lens_list"]):
+        n = case["n_pages"][b]
+        slots = case["table_cpu"][b, :n].long().to(case["pool"].device)
+        for kvh in heads:
+            K = case["pool"][slots, 0, kvh].reshape(-1, w.D)[:t][None].cpu()
+            V = case["pool"][slots, 1, kvh].reshape(-1, w.D)[:t][None].cpu()
+            hs = slice(kvh * G, (kvh + 1) * G)
+            ref = attention_fp64_batched(case["q"][b, hs].cpu(), K, V)
+            worst = max(worst, (out[b, hs].double().cpu() - ref).abs().max().item())
+    return worst
+
+
+def gpu_configs(args, torch, W, paged):
+    """The other configurations of the benchmark set, each at its stated
+    shape: Qwen3-0.6B 2k (fp16) and Qwen3-14B B8 ragged 4k-32k (bf16) through
+    the pool-layout decode call (rotated pools), Llama-2-13B 128k (fp16, MHA)
+    with its oldest 75% of pages in pinned host memory through
+    helm_stream_attn; per-call time, GB/s, roofline fraction, max |error|
+    against the fp64 oracle."""
+    res = {}
+    for name, seed, tol in (("qwen3-0.6b-2k", 0, 2e-3), ("qwen3-14b-ragged-b8", 3, 1e-2)):
+        h = gpu_headline(args, torch, W, paged, name=name, seed=seed, steps=100)
+        gbs = h["alg_bytes"] / h["per_call_s"] / 1e9
+        w = h["w"]
+        res[name] = {
+            "workload": f"{name}: B={w.B}, Hq={w.Hq}, Hkv={w.Hkv}, D={w.D}, "
+                        f"{str(w.dtype).split('.')[-1]}, contexts {h['lens']}, pages of 16, "
+                        f"all resident, {h['pools']} rotated pools",
+            "us_per_call": round(h["per_call_s"] * 1e6, 3), "GBs": round(gbs, 1),
+            "roofline_frac": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes": h["alg_bytes"],
+            "max_abs_err_vs_fp64": pool_error(torch, h, [0, w.Hkv - 1]), "tolerance": tol}
+        log(json.dumps(res[name]))
+        del h
+        torch.cuda.empty_cache()
+    o = gpu_offload(args, torch, W, name="llama2-13b-128k-offload75", seed=4, steps=5,
+                    check_heads=[0, 13, 27, 39])
+    o["workload"] = ("llama2-13b-128k-offload75: B=1, Hq=Hkv=40, D=128, fp16, 131072 tokens "
+                     "in 8192 pages, oldest 75% in pinned host")
+    o["tolerance"] = 2e-3
+    res["llama2-13b-128k-offload75"] = o
+    log(json.dumps(o))
+    torch.cuda.empty_cache()
+    return res
+
+
+def gpu_runtime_decode(args, torch, W, layers=8, steps=25, seed=11):
+    """HELM's production decode call on the Qwen3-8B 32k shape: the per-layer
+    ``_decode_batched`` of the patched forwards (append the token, residency,
+    attention over the layer's records) under the pipeline's decode mask,
+    zeros [1, 1, 1, T] (pipeline_runtime.py:79-92, :217), and without a mask
+    for comparison.  Eight layers of 32k tokens are rotated (1 GiB of KV, so
+    the Infinity Cache cannot serve a layer twice).  Wall time per layer call
+    (host issue included) and the GPU time between events around the loop."""
+    import random
+    from helm_amd.runtime.kv_allocator import KVAllocator
+    from helm_amd.runtime.kv_cache import KVCacheManager
+    from helm_amd.runtime.kv_offload import _decode_batched
+    from oracle.attention import attention_fp64_batched
+    w = W.WORKLOADS["qwen3-8b-32k"]
+    dev = torch.device("cuda:0")
+    P = w.page_size
+    a = KVAllocator(layers, w.Hkv, w.D, page_size=P, dtype=w.dtype)
+    a.reserve_batch(layers * (w.T // P + 4 * steps // P + 4), dev)
+    random.Random(seed).shuffle(a.gpu_free_pool)
+    m = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 13)
+    m.initialize_layer_caches(layers)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    for lid in range(layers):
+        m.append_prefill(lid, torch.randn((1, w.Hkv, w.T, w.D), generator=g, device=dev,
+                                          dtype=w.dtype),
+                         torch.randn((1, w.Hkv, w.T, w.D), generator=g, device=dev,
+                                     dtype=w.dtype))
+    q = torch.randn((layers, 1, w.Hq, 1, w.D), generator=g, device=dev, dtype=w.dtype)
+    kn = torch.randn((layers, 1, w.Hkv, 1, w.D), generator=g, device=dev, dtype=w.dtype)
+    vn = torch.randn((layers, 1, w.Hkv, 1, w.D), generator=g, device=dev, dtype=w.dtype)
+    zeros = torch.zeros(1, 1, 1, w.T + 4 * steps + 8, device=dev)
+    scale = 1.0 / math.sqrt(w.D)
+    stream = torch.cuda.current_stream(dev)
+    out = None
+
+    def run(n, masked):
+        nonlocal out
+        for _ in range(n):
+            for lid in range(layers):
+                t = m.layers[lid].total_tokens + 1
+                out = _decode_batched([m], q[lid], kn[lid], vn[lid], lid, scale,
+                                      zeros[..., :t] if masked else None)
+
+    res = {"workload": f"qwen3-8b-32k through _decode_batched: {layers} layers of {w.T} "
+                       "tokens rotated, B=1, bf16, one call per layer per step"}
+    for label, masked in (("masked", True), ("unmasked", False)):
+        run(1, masked)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        run(steps, masked)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / (steps * layers)
+        gpu = e0.elapsed_time(e1) / 1e3 / (steps * layers)
+        alg = W.algorithmic_bytes(w, [m.layers[0].total_tokens])
+        res[label] = {"us_per_call_wall": round(wall * 1e6, 2),
+                      "us_per_call_gpu_events": round(gpu * 1e6, 2),
+                      "GBs_wall": round(alg / wall / 1e9, 1),
+                      "roofline_frac_wall": round(alg / wall / 1e9 / HBM_PEAK_GBS, 4)}
+    # the last call (layer layers-1, unmasked) against the oracle on two KV heads
+    lid = layers - 1
+    pages = m.layers[lid].pages
+    err = 0.0
+    for kvh in (0, w.Hkv - 1):
+        K = torch.cat([p.k_tensor[0, kvh, :p.used_tokens] for p in pages], 0)[None].cpu()
+        V = torch.cat([p.v_tensor[0, kvh, :p.used_tokens] for p in pages], 0)[None].cpu()
+        hs = slice(kvh * w.G, (kvh + 1) * w.G)
+        ref = attention_fp64_batched(q[lid, 0, hs].cpu(), K, V)
+        err = max(err, (out[0, hs].double().cpu() - ref).abs().max().item())
+    res["max_abs_err_vs_fp64"] = err
+    m.clear()
+    del m, a, q, kn, vn
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_info():
+    """The host CPU: model name, logical CPUs this process may use, and the
+    physical cores behind them (distinct (package, core) pairs)."""
+    model, cores, cur = None, set(), {}
+    allowed = os.sched_getaffinity(0)
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f.read().splitlines() + [""]:
+                if not line.strip():
+                    if cur.get("processor") is not None and cur["processor"] in allowed:
+                        cores.add((cur.get("physical id"), cur.get("core id", cur["processor"])))
+                    cur = {}
+                    continue
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                if k == "processor":
+                    cur["processor"] = int(v)
+                elif k in ("physical id", "core id"):
+                    cur[k] = v
+    except OSError:
+        pass
+    return {"model": model, "logical_cpus_allowed": len(allowed),
+            "physical_cores_allowed": len(cores) or len(allowed)}
+
+
+def cpu_threads():
+    """Threads for the host-CPU legs: one per physical core this process may
+    use, at most the OpenMP thread count the box sets (its CPU share)."""
+    info = cpu_info()
+    cap = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    return max(1, min(info["physical_cores_allowed"], cap)), info
+
+
+def cpu_c1(args, torch, W, seconds=4.0):
+    """Qwen3-0.6B 2k (fp16) on the host CPU path, the path HELM runs a CPU
+    stage's attention on: the native host kernel here (libhelm_cpu.so,
+    helm_cpu_stream_attn, production decode mask) beside the oracle's
+    restatement of HELM's torch code (Path 2, cat + fp32 SDPA; and the masked
+    per-page loop), same inputs; bounded samples."""
+    from helm_amd.runtime.kv_cache import _attend_records_cpu
+    from oracle import attention as A
+    threads, info = cpu_threads()
+    torch.set_num_threads(threads)
+    w = W.WORKLOADS["qwen3-0.6b-2k"]
+    case = W.make_pool_case(w, seed=0, device="cpu")
+    arr, seq_off = W.pool_records(case, w)
+    T = w.T
+    mask = torch.zeros(1, 1, 1, T)
+    slots = case["table_cpu"][0].long()
+    K = case["pool"][slots, 0].permute(1, 0, 2, 3).reshape(w.Hkv, -1, w.D)
+    V = case["pool"][slots, 1].permute(1, 0, 2, 3).reshape(w.Hkv, -1, w.D)
+    pages = A.split_pages(K[None], V[None], [w.page_size] * (T // w.page_size))
+    alg = W.algorithmic_bytes(w, [T])
+    legs = {
+        "native_host_kernel": lambda: _attend_records_cpu(case["q"], arr, seq_off, T, w.Hkv,
+                                                          w.dtype, case["scale"], mask, None, 0),
+        "oracle_path2_concat_sdpa": lambda: A.concat_sdpa(case["q"], pages),
+        "oracle_masked_online_softmax": lambda: A.online_softmax_pages(case["q"], pages,
+                                                                       attention_mask=mask),
+    }
+    res = {"workload": "qwen3-0.6b-2k: B=1, Hq=16, Hkv=8, D=128, fp16, 2048 tokens in 128 "
+                       "pages of 16 (random page table), on the host CPU",
+           "threads": threads, "cpu": info}
+    outs = {}
+    for name, fn in legs.items():
+        outs[name] = fn()
+        t0, calls = time.perf_counter(), 0
+        while True:
+            fn()
+            calls += 1
+            if time.perf_counter() - t0 > seconds / 3:
+                break
+        per = (time.perf_counter() - t0) / calls
+        res[name] = {"us_per_call": round(per * 1e6, 2), "GBs": round(alg / per / 1e9, 3),
+                     "calls": calls}
+    ref = A.attention_fp64_batched(case["q"][0].float(), K.float(), V.float())
+    res["native_max_abs_err_vs_fp64"] = (outs["native_host_kernel"][0].double() - ref).abs().max().item()
+    res["native_speedup_vs_path2"] = round(res["oracle_path2_concat_sdpa"]["us_per_call"]
+                                           / res["native_host_kernel"]["us_per_call"], 1)
+    return res
+
+
 # Qwen3-8B decode-step linears of one layer (out x in): q, k, v, o, gate, up, down
 GEMV_SHAPES = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (12288, 4096),
                (12288, 4096), (4096, 12288)]
@@ -410,7 +667,7 @@ def cpu_gemv(args, torch, reps=10, layers=2, seed=7):
     float32, the weight widened every call).  Bound: host DRAM bandwidth
     (bytes = the weights; x and y are cache resident)."""
     from helm_amd import kernels
-    threads = min(16, os.cpu_count() or 1)
+    threads, _ = cpu_threads()
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(seed)
     Ws = [[(0.02 * torch.randn(n, k, generator=g)).half() for n, k in GEMV_SHAPES]
@@ -477,7 +734,7 @@ def cpu_baseline(args, torch, W):
     on the headline shape; bounded to about args.cpu_seconds."""
     from oracle import attention as A
     w = W.WORKLOADS["qwen3-8b-32k"]
-    threads = min(16, os.cpu_count() or 1)
+    threads, info = cpu_threads()
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(1)
     P, n = w.page_size, w.T // w.page_size
@@ -501,6 +758,7 @@ def cpu_baseline(args, torch, W):
                 break
         per = (time.perf_counter() - t0) / calls
         res[name] = {"s_per_call": per, "GBs": alg / per / 1e9, "calls": calls}
+    res["cpu"] = info
     return res, threads
 
 
@@ -534,6 +792,27 @@ def main():
     if args.all:
         all_configs(args, torch, W, paged)
 
+    log("headline shape under HELM's decode mask (zeros [1,1,1,T])")
+    hm = gpu_headline(args, torch, W, paged, masked=True)
+    hm_gbs = hm["alg_bytes"] / hm["per_call_s"] / 1e9
+    masked_c2 = {"us_per_call": round(hm["per_call_s"] * 1e6, 3), "GBs": round(hm_gbs, 1),
+                 "roofline_frac": round(hm_gbs / HBM_PEAK_GBS, 4),
+                 "max_abs_err_vs_fp64": pool_error(torch, hm, [0, 7]),
+                 "mask": "zeros [1, 1, 1, 32768] (HELM's decode mask), read by the kernel"}
+    del hm
+    log(json.dumps(masked_c2))
+
+    configs = None
+    if not args.no_configs:
+        log("configs: qwen3-0.6b-2k, qwen3-14b-ragged-b8, llama2-13b-128k-offload75")
+        configs = gpu_configs(args, torch, W, paged)
+
+    runtime = None
+    if not args.no_runtime:
+        log("production decode call: _decode_batched over 8 rotated 32k layers")
+        runtime = gpu_runtime_decode(args, torch, W)
+        log(json.dumps(runtime))
+
     full = None
     if not args.no_full_step:
         full = {}
@@ -541,7 +820,8 @@ def main():
         for budget in budgets:
             label = f"budget_{budget:g}GB" + ("" if budget >= 64 else "_eviction")
             log(f"full step: qwen3-14b 40 layers, B4 x 64k, device KV budget {budget:.0f} GB")
-            r = gpu_full_step(args, torch, W, budget, args.full_step_steps)
+            r = gpu_full_step(args, torch, W, budget, args.full_step_steps,
+                              masked_steps=args.full_step_steps if budget >= 64 else 16)
             log(json.dumps(r))
             full[label] = r
 
@@ -563,6 +843,12 @@ def main():
         log("cpu gemv: qwen3-8b decode-step linears on host cores (HELM's CPU stages)")
         gemv = cpu_gemv(args, torch)
         log(json.dumps(gemv))
+
+    c1_cpu = None
+    if not args.no_cpu:
+        log("cpu path: qwen3-0.6b-2k on the host (native kernel beside the oracle's torch code)")
+        c1_cpu = cpu_c1(args, torch, W)
+        log(json.dumps(c1_cpu))
 
     cpu = None
     threads = 0
@@ -611,6 +897,10 @@ def main():
                                "merge_splits_d128_kernel, timed with HIP events on its stream",
                      "rocprof_kernel_us": prof,
                      "host_issue_us_per_call": round(h["host_issue_us_per_call"], 2)},
+        "decode_masked_32k": masked_c2,
+        "configs": configs,
+        "runtime_decode_32k": runtime,
+        "c1_cpu_path": c1_cpu,
         "offload50": off,
         "full_step_40l": full,
         "prefill_chunk": pre,
@@ -618,7 +908,11 @@ def main():
         "cpu_baseline": None if cpu is None else {
             "value": round(cpu["path2_concat_sdpa"]["GBs"], 3), "unit": "GB/s",
             "cores": threads, "kind": "port",
-            "sample": (f"qwen3-8b-32k shape on host cores, HELM Path 2 (cat + fp32 SDPA) "
+            "cpu_model": cpu["cpu"]["model"],
+            "physical_cores_allowed": cpu["cpu"]["physical_cores_allowed"],
+            "logical_cpus_allowed": cpu["cpu"]["logical_cpus_allowed"],
+            "sample": (f"qwen3-8b-32k shape on {threads} host threads (one per physical core "
+                       f"of this process's CPU share), HELM Path 2 (cat + fp32 SDPA) "
                        f"{cpu['path2_concat_sdpa']['calls']} calls; masked online-softmax loop "
                        f"{cpu['masked_online_softmax']['calls']} calls at "
                        f"{cpu['masked_online_softmax']['GBs']:.3f} GB/s")},

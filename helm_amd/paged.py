@@ -63,12 +63,13 @@ def prepare_paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Te
                          max_pages: Optional[int] = None, total_pages: int = 0,
                          scale: Optional[float] = None, softcap: Optional[float] = None,
                          out: Optional[torch.Tensor] = None,
-                         pages_per_split: int = 0) -> PreparedDecode:
+                         pages_per_split: int = 0,
+                         attention_mask: Optional[torch.Tensor] = None) -> PreparedDecode:
     """Validates the shapes once and returns a PreparedDecode bound to torch's
-    current stream on q's device (same arguments as paged_decode_attention,
-    without a mask)."""
+    current stream on q's device (same arguments as paged_decode_attention;
+    the mask, if any, is read at every run)."""
     args, keep = _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages,
-                              scale, softcap, None, out, pages_per_split)
+                              scale, softcap, attention_mask, out, pages_per_split)
     prep = PreparedDecode(args, 2, _native.load().helm_paged_decode_attn)
     prep.out = keep["out"]
     prep._keep = keep

@@ -112,3 +112,24 @@ def algorithmic_bytes(w: Workload, lens: list) -> int:
     es = torch.tensor([], dtype=w.dtype).element_size()
     pages = sum(math.ceil(t / w.page_size) for t in lens)
     return kv_bytes(w, lens) + 2 * w.B * w.Hq * w.D * es + 4 * pages
+
+
+def pool_records(case: dict, w: Workload):
+    """``helm_page`` records of a pool case in page-table order (sequence b
+    owns seq_off[b]:seq_off[b+1]; token offsets from 0 per sequence), for the
+    entry points that take page records (helm_stream_attn,
+    helm_cpu_stream_attn).  Returns (records, seq_off) numpy arrays."""
+    import numpy as np
+    from helm_amd import _native
+    pool, table, P = case["pool"], case["table_cpu"], w.page_size
+    es = pool.element_size()
+    recs, seq_off = [], [0]
+    for b, n in enumerate(case["n_pages"]):
+        t = case["lens_list"][b]
+        for i in range(n):
+            base = pool.data_ptr() + int(table[b, i]) * pool.stride(0) * es
+            recs.append((base, base + pool.stride(1) * es, min(P, t - i * P), i * P,
+                         pool.stride(2), 0))
+        seq_off.append(len(recs))
+    arr = np.array(recs, dtype=_native.PAGE_DTYPE) if recs else np.zeros(0, _native.PAGE_DTYPE)
+    return arr, np.array(seq_off, dtype=np.int32)

@@ -41,23 +41,6 @@ def isa(request, monkeypatch):
     return request.param
 
 
-def _records(pool, table, n_pages, lens, P):
-    """helm_page records of pool slots (the allocator's arena layout
-    [slots, 2, Hkv, P, D]) in page-table order; sequence b owns
-    seq_off[b]:seq_off[b+1]."""
-    es = pool.element_size()
-    recs, seq_off = [], [0]
-    for b, n in enumerate(n_pages):
-        for i in range(n):
-            s = int(table[b, i])
-            used = min(P, lens[b] - i * P)
-            base = pool.data_ptr() + s * pool.stride(0) * es
-            recs.append((base, base + pool.stride(1) * es, used, i * P, pool.stride(2), 0))
-        seq_off.append(len(recs))
-    arr = np.array(recs, dtype=_native.PAGE_DTYPE) if recs else np.zeros(0, _native.PAGE_DTYPE)
-    return arr, np.array(seq_off, dtype=np.int32)
-
-
 def _gather(pool, table, b, n, t):
     """Sequence b's K and V [Hkv, t, D] in token order (float32)."""
     slots = table[b, :n].long()
@@ -90,8 +73,7 @@ def _case(w, seed, lens=None, S=1):
         g = torch.Generator().manual_seed(seed + 1)
         case["q"] = torch.randn(w.B if lens is None else len(lens), w.Hq, S, w.D,
                                 generator=g).to(w.dtype)
-    arr, seq_off = _records(case["pool"], case["table_cpu"], case["n_pages"], case["lens_list"],
-                            w.page_size)
+    arr, seq_off = W.pool_records(case, w)
     return case, arr, seq_off
 
 
