@@ -844,6 +844,16 @@ def main():
         gemv = cpu_gemv(args, torch)
         log(json.dumps(gemv))
 
+    log("device profile: HBM copy and pinned host-link bandwidth (native probe)")
+    from helm_amd import device_profiler as DP
+    dprof = DP.measure_links(0)
+    dprof = {"hbm_copy_GBs": round(dprof["device_copy_bytes_per_s"] / 1e9, 1),
+             "pinned_h2d_GBs": round(dprof["h2d_bytes_per_s"] / 1e9, 2),
+             "pinned_d2h_GBs": round(dprof["d2h_bytes_per_s"] / 1e9, 2),
+             "probe": "helm_measure_bandwidth: 256 MB streaming copy (read + write), "
+                      "64 MB pinned copies each way, 8 timed repetitions"}
+    log(json.dumps(dprof))
+
     c1_cpu = None
     if not args.no_cpu:
         log("cpu path: qwen3-0.6b-2k on the host (native kernel beside the oracle's torch code)")
@@ -901,6 +911,7 @@ def main():
         "configs": configs,
         "runtime_decode_32k": runtime,
         "c1_cpu_path": c1_cpu,
+        "device_profile": dprof,
         "offload50": off,
         "full_step_40l": full,
         "prefill_chunk": pre,

@@ -34,6 +34,13 @@ APPEND_DTYPE = np.dtype([
 ])
 assert APPEND_DTYPE.itemsize == 64
 
+# struct helm_bandwidth (32 bytes)
+BANDWIDTH_DTYPE = np.dtype([
+    ("device_copy_bytes_per_s", "<f8"), ("h2d_bytes_per_s", "<f8"), ("d2h_bytes_per_s", "<f8"),
+    ("copy_mismatched_words", "<i8"),
+])
+assert BANDWIDTH_DTYPE.itemsize == 32
+
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _u64, _f32, _sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_size_t
 
@@ -74,6 +81,8 @@ SIGNATURES = {
         _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, ctypes.c_int, _f32,
         _c_void_p, _c_void_p, _i64, ctypes.c_int, _c_void_p, _c_void_p, ctypes.c_int,
         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
+    "helm_measure_bandwidth": (ctypes.c_int, [ctypes.c_int, _u64, _u64, ctypes.c_int,
+                                              _c_void_p]),
     "helm_evict_pages": (ctypes.c_int, [_c_void_p, ctypes.c_int, _c_void_p, _c_void_p,
                                         _c_void_p, ctypes.c_int, _c_void_p]),
     "helm_prefetch_pages": (ctypes.c_int, [_c_void_p, ctypes.c_int, _c_void_p, _c_void_p,

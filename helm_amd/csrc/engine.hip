@@ -399,6 +399,11 @@ __global__ __launch_bounds__(256) void page_append_kernel(AppendArgs a) {
 }
 
 }  // namespace
+
+// Sets this thread's message (helm_last_error_string) for the library's
+// other translation units; returns code.
+int report_error(int code, const std::string& msg) { return fail(code, msg); }
+
 }  // namespace helm
 
 using namespace helm;

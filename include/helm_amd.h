@@ -284,6 +284,27 @@ int helm_prefetch_pages(helm_engine* eng, int n, const uint64_t* src_host,
                         const uint64_t* dst_dev, const uint64_t* bytes,
                         int sync, void* stream);
 
+/* ---- device profile ------------------------------------------------------- */
+
+/* Bandwidths of one device, as HELM's device profiler measures them for its
+ * planner (helm/compiler/optimization/device_profiler.py:188-240: _bench_gpu's
+ * stream copy, counted as 2 x bytes per copy; _bench_pcie's pinned H2D / D2H
+ * copies), in bytes per second, each the mean of `iters` timed repetitions
+ * after one warm-up on a stream of the probe's own. */
+typedef struct helm_bandwidth {
+  double device_copy_bytes_per_s; /* HBM: a streaming-copy kernel, read + write */
+  double h2d_bytes_per_s;         /* pinned host -> device, hipMemcpyAsync       */
+  double d2h_bytes_per_s;         /* device -> pinned host, hipMemcpyAsync       */
+  int64_t copy_mismatched_words;  /* the copy checked word by word: 0 expected   */
+} helm_bandwidth;
+
+/* Measures `device` (made current for the call, then restored): a device copy
+ * of stream_bytes (HELM: 256 MB) and host-link copies of link_bytes (HELM:
+ * 64 MB).  Allocates its buffers (device, pinned host) and frees them before
+ * returning.  Byte counts >= 4096 and multiples of 16, iters >= 1. */
+int helm_measure_bandwidth(int device, uint64_t stream_bytes, uint64_t link_bytes,
+                           int iters, helm_bandwidth* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,6 +29,16 @@ needs_lib = pytest.mark.skipif(_cpu_native.try_load()[0] is None,
                                reason="libhelm_cpu.so not built or no AVX2 on this CPU")
 pytestmark = needs_lib
 
+
+# Every test here runs twice: in the CPU suite, and under the `gpu` marker so
+# that the GPU run exercises the host-CPU code on the GPU box's own host CPU
+# (another microarchitecture than the build machine's).
+@pytest.fixture(autouse=True, params=[pytest.param("host", id="host"),
+                                      pytest.param("box", id="box", marks=pytest.mark.gpu)])
+def _where(request):
+    return request.param
+
+
 ISAS = ["avx512", "avx2"]
 
 

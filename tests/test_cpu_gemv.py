@@ -21,6 +21,15 @@ needs_kernel = pytest.mark.skipif(not kernels.is_available(),
                                   reason=f"native GEMV unavailable: {kernels.load_error()}")
 
 
+# Every test here runs twice: in the CPU suite, and under the `gpu` marker so
+# that the GPU run exercises the host-CPU code on the GPU box's own host CPU
+# (another microarchitecture than the build machine's).
+@pytest.fixture(autouse=True, params=[pytest.param("host", id="host"),
+                                      pytest.param("box", id="box", marks=pytest.mark.gpu)])
+def _where(request):
+    return request.param
+
+
 def _rand(shape, seed, scale=1.0):
     g = torch.Generator().manual_seed(seed)
     return (scale * torch.randn(*shape, generator=g)).half()

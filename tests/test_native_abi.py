@@ -44,6 +44,7 @@ def test_abi_version():
 def test_struct_layouts_match_header():
     assert _native.PAGE_DTYPE.itemsize == 32
     assert _native.APPEND_DTYPE.itemsize == 64
+    assert _native.BANDWIDTH_DTYPE.itemsize == 32
 
 
 def test_workspace_sizing_host_only():
