@@ -26,7 +26,7 @@ def device_index(device: torch.device) -> int:
 
 
 def get_engine(device: torch.device) -> ctypes.c_void_p:
-    idx = device_index(device)
+    idx = device.index if device.index is not None else device_index(device)
     eng = _engines.get(idx)
     if eng is None:
         _native.load()
@@ -50,9 +50,16 @@ def copy_stream(device: torch.device) -> torch.cuda.ExternalStream:
     return s
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_ptr(device: torch.device) -> int:
-    """hipStream_t of torch's current stream on `device`."""
-    return torch.cuda.current_stream(device).cuda_stream
+    """hipStream_t of torch's current stream on `device` (torch's raw-stream
+    query where this torch has it: no Stream object per call)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(idx)
+    return torch.cuda.current_stream(idx).cuda_stream
 
 
 @atexit.register

@@ -266,6 +266,14 @@ class LayerKVCache:
                          (hi - lo) * rb, stream)
         return self._dev
 
+    def total_tokens_recorded(self) -> int:
+        """Tokens in the layer's records (its active pages)."""
+        n = len(self.pages)
+        if n == 0:
+            return 0
+        last = self._rec[n - 1]
+        return int(last["tok_off"]) + int(last["used"])
+
     def records(self):
         """The pages' ``helm_page`` records in token order (a view), or None."""
         if not self._rec_ok:
@@ -977,11 +985,14 @@ def _attend_device_records(query: torch.Tensor, ptrs: np.ndarray, npages: np.nda
                 page_tokens, aligned, Hkv, kv_dtype, scale, m, softcap, causal))
         return torch.cat(outs, 0)
     _, Hq, S, D = query.shape
-    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, int(tokens.max()),
-                                           attention_mask)
-    ptrs = np.ascontiguousarray(ptrs, dtype=np.uint64)
-    npages = np.ascontiguousarray(npages, dtype=np.int32)
-    tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+    t_max = int(tokens[0]) if B == 1 else int(tokens.max())
+    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, t_max, attention_mask)
+    if ptrs.dtype != np.uint64 or not ptrs.flags["C_CONTIGUOUS"]:
+        ptrs = np.ascontiguousarray(ptrs, dtype=np.uint64)
+    if npages.dtype != np.int32 or not npages.flags["C_CONTIGUOUS"]:
+        npages = np.ascontiguousarray(npages, dtype=np.int32)
+    if tokens.dtype != np.int32 or not tokens.flags["C_CONTIGUOUS"]:
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
     _native.call("helm_paged_attn_seqs", _engine.get_engine(device), q.data_ptr(),
                  out.data_ptr(), B, Hq, Hkv, S, D, _native.ptr(ptrs), _native.ptr(npages),
                  _native.ptr(tokens), page_tokens, 1 if aligned else 0, float(scale),

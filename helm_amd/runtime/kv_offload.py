@@ -215,8 +215,19 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
     kv_dtype = layers[0]._rec_sig[0]
     if any(layer._rec_sig[0] != kv_dtype for layer in layers):
         return None
-    lens = [int(r["tok_off"][-1]) + int(r["used"][-1]) for r in recs]
+    lens = [layer.total_tokens_recorded() for layer in layers]
     bsz = len(layers)
+    host = any(layer._n_host for layer in layers)
+    if not cpu:
+        # HELM streams the items that hold host pages one by one and counts
+        # each as a prefetch (kv_offload.py:176-186, kv_cache.py:441-447)
+        if host:
+            for layer in layers:
+                _record_prefetch(layer._n_host, layer._host_bytes)
+        elif bsz <= _MAX_SEQ_ARGS:
+            # every page on the device: the layers' device-resident records
+            return _attend_layers(q, layers, lens, Hkv, kv_dtype, scale, attention_mask,
+                                  softcap, False)
     # (concatenated as raw 8-byte words: numpy's structured-dtype
     # concatenate is ~15x slower)
     arr = recs[0] if bsz == 1 else np.concatenate(
@@ -230,15 +241,7 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
             return None
         return _attend_records(q, arr, seq_off, max(lens), Hkv, kv_dtype, scale,
                                attention_mask, softcap, False)
-    # HELM streams the items that hold host pages one by one and counts each
-    # as a prefetch (kv_offload.py:176-186, kv_cache.py:441-447)
-    for layer in layers:
-        _record_prefetch(layer._n_host, layer._host_bytes)
-    if bsz <= _MAX_SEQ_ARGS and not any(layer._n_host for layer in layers):
-        # every page on the device: the layers' device-resident records
-        return _attend_layers(q, layers, lens, Hkv, kv_dtype, scale, attention_mask, softcap,
-                              False)
-    if bsz == 1 or not any(layer._n_host for layer in layers):
+    if bsz == 1 or not host:
         return _attend_records(q, arr, seq_off, max(lens), Hkv, kv_dtype, scale,
                                attention_mask, softcap, False)
     try:

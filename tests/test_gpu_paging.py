@@ -1187,3 +1187,14 @@ def test_causal_chunk_over_host_pages_out_of_token_order(host_mode, monkeypatch)
     assert (fast[0].double().cpu() - ref).abs().max().item() <= 1e-2
     assert (slow[0].double().cpu() - ref).abs().max().item() <= 1e-2
     mgr.clear()
+
+
+def test_raw_stream_pointer_is_torchs_current_stream():
+    """The launch stream the runtime passes is torch's current stream, also
+    inside a `with torch.cuda.stream(...)` block."""
+    from helm_amd.runtime import engine
+    assert engine.stream_ptr(DEV) == torch.cuda.current_stream(DEV).cuda_stream
+    s = torch.cuda.Stream(device=DEV)
+    with torch.cuda.stream(s):
+        assert engine.stream_ptr(DEV) == s.cuda_stream
+    assert engine.stream_ptr(torch.device("cuda")) == torch.cuda.current_stream().cuda_stream
