@@ -17,10 +17,16 @@
 //           tau(8g + 4h + t) = 16 (g >> 1) + 8h + 4 (g & 1) + t register r holds
 //           token 8hh + (r & 7) of block r >> 3 of the step.
 //   P . V   O += P V: A = the weights of row j for tokens 8hh .. 8hh + 7 of a
-//           block (exactly registers 8u .. 8u + 7 above), split into 16-bit hi
-//           and lo parts (two MFMAs); B = V of those tokens at dim 32e + j,
-//           fetched by LDS transpose reads; O register 4g + t of dim group e
-//           is row 8g + 4hh + t, dim 32e + j.
+//           block (exactly registers 8u .. 8u + 7 above), rounded once to the
+//           16-bit type; B = V of those tokens at dim 32e + j, fetched by LDS
+//           transpose reads; O register 4g + t of dim group e is row
+//           8g + 4hh + t, dim 32e + j.  A fifth MFMA per block multiplies the
+//           same weights by a column of ones: the row sums of exactly the
+//           weights P . V used, so that each output row is an exact weighted
+//           mean of V under the rounded weights (their rounding perturbs the
+//           weights by <= 2^-9 relative, bf16, and the mean by that times the
+//           spread of V).  HELM_CHUNK32_HILO=1 builds the split into hi and lo
+//           16-bit parts instead (weights to ~2^-17, one more MFMA per group).
 // Online softmax per query row with the lazy rescale of the decode kernel.
 #pragma once
 
@@ -46,6 +52,20 @@ template <> struct Mfma32<f16_t> {
 
 constexpr int kChunk32Rows = 32;   // query rows per wave
 
+// LDS swizzle of a staged block: chunk c (16 B) of token t (0..15) sits at
+// slot c ^ swz(t) of the token's 256-byte row, swz(4a + b) = 4b + a.  The
+// q . k reads (one chunk, 16 tokens per 16 lanes) meet 16 distinct slots
+// mod 16, and so do the V transpose reads (chunks c0 .. c0 + 3, c0 a
+// multiple of 4, of four consecutive tokens 4a .. 4a + 3 per 32 lanes): each
+// group of accesses covers every 16-byte bank group once.
+__device__ __forceinline__ int swz(int t) { return ((t & 3) << 2) | (t >> 2); }
+// P . V with the weights split into 16-bit hi and lo parts (1) or rounded
+// once to 16 bits (0: the default — a query chunk is bound by the matrix
+// cores, and the single rounding stays far inside the tolerance)
+#ifndef HELM_CHUNK32_HILO
+#define HELM_CHUNK32_HILO 0
+#endif
+
 // 16 bytes per lane from a buffer straight into LDS: lane i writes
 // lds_dst + 16 i (the address must be the same in every lane); loads past the
 // buffer's size write zeros
@@ -66,7 +86,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   // two stage buffers as two objects, so that the compiler sees that the
   // loads filling one never touch the reads of the other:
   // [K, V][block of the stage][16-byte chunk], chunk c of token t at slot
-  // t * 16 + (c ^ t)
+  // t * 16 + (c ^ swz(t)) (see swz)
   typedef mf_u32x4 StageBuf[2][kChunkStage][kBlk / 16];
   __shared__ StageBuf lds0, lds1;
 
@@ -151,7 +171,17 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   const float inv_cap = kCap ? 1.f / cap : 0.f;
 
   float m = -INFINITY;   // running max of row jr (same in both halves)
+#if HELM_CHUNK32_HILO
   float lsum = 0.f;      // this lane's share of the row's weight sum
+#else
+  // the rows' weight sums on the matrix cores: P times a column of ones, so
+  // the sum takes exactly the 16-bit weights that P . V takes; register
+  // 4g + t holds row 8g + 4hh + t (the same value in every lane of a half)
+  mf_f32x16 osum;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) osum[r] = 0.f;
+  const mf_u32x4 ones = Ops::ones8();
+#endif
   mf_f32x16 o[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e)
@@ -207,7 +237,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int t = 4 * u + (lane >> 4);
-      const int off = t * kRow + 16 * ((lane & 15) ^ t);
+      const int off = t * kRow + 16 * ((lane & 15) ^ swz(t));
       buf_load16_lds(rk, &dst[0][wave][64 * u], off);
       buf_load16_lds(rv, &dst[1][wave][64 * u], off);
     }
@@ -223,7 +253,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   auto vaddr = [&](const StageBuf& cur, int blk, int z, int e) -> const char* {
     const int vtok = 8 * hh + 4 * z + (nl >> 2);
     const int chunk = 4 * e + 2 * (jr >> 4) + ((nl & 3) >> 1);
-    return reinterpret_cast<const char*>(&cur[1][blk][vtok * 16 + (chunk ^ vtok)]) +
+    return reinterpret_cast<const char*>(&cur[1][blk][vtok * 16 + (chunk ^ swz(vtok))]) +
            8 * (nl & 1);
   };
 
@@ -312,7 +342,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
         for (int r = 0; r < 16; ++r) sc[r] = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const mf_u32x4 ka = cur[0][bp + kblk][ktok * 16 + ((2 * i + hh) ^ ktok)];
+          const mf_u32x4 ka = cur[0][bp + kblk][ktok * 16 + ((2 * i + hh) ^ swz(ktok))];
           sc = M32::mma(ka, qop[i], sc);
         }
         float x[16];
@@ -345,7 +375,14 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
           // refresh the row max (both halves of the row agree)
           const float mn = fmaxf(m, fmaxf(bm, __shfl_xor(bm, 32, 64)));
           const float a = fexp(m - ((mn == -INFINITY) ? 0.f : mn));
+#if HELM_CHUNK32_HILO
           lsum *= a;
+#else
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) osum[4 * g + t] *= __shfl(a, 8 * g + 4 * hh + t, 64);
+#endif
           m = mn;
           // O register 4g + t is row 8g + 4hh + t: that row's factor
 #pragma unroll
@@ -362,8 +399,13 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           const float w0 = fexp(x[2 * q] - base), w1 = fexp(x[2 * q + 1] - base);
+#if HELM_CHUNK32_HILO
           lsum += w0 + w1;
           Ops::split2(w0, w1, hw[q], lw[q]);
+#else
+          hw[q] = Ops::pk(w0, w1);
+          lw[q] = 0u;
+#endif
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -378,8 +420,13 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
           }
 #pragma unroll
           for (int e = 0; e < 4; ++e) o[e] = M32::mma(phi, vop[e], o[e]);
+#if HELM_CHUNK32_HILO
 #pragma unroll
           for (int e = 0; e < 4; ++e) o[e] = M32::mma(plo, vop[e], o[e]);
+#else
+          (void)plo;
+          osum = M32::mma(phi, ones, osum);
+#endif
         }
       }
     }
@@ -391,7 +438,17 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   }
 
   if (!wave_rows) return;
+#if HELM_CHUNK32_HILO
   const float lrow = lsum + __shfl_xor(lsum, 32, 64);     // row jr's sum
+#else
+  // row jr's sum: held by the half hh = (jr >> 2) & 1, register 4 (jr >> 3) + (jr & 3)
+  float lself = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    if (r == 4 * (jr >> 3) + (jr & 3)) lself = osum[r];
+  const float lother = __shfl_xor(lself, 32, 64);
+  const float lrow = (((jr >> 2) & 1) == hh) ? lself : lother;
+#endif
   if (p.direct_out) {
     // the call's only split: normalized rows straight to the output
     // (HELM's final out / max(sum, 1e-12), kv_cache.py:554-555)
@@ -400,7 +457,11 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int i = 8 * g + 4 * hh + t;
+#if HELM_CHUNK32_HILO
         const float inv = 1.f / fmaxf(__shfl(lrow, i, 64), 1e-12f);
+#else
+        const float inv = 1.f / fmaxf(osum[4 * g + t], 1e-12f);
+#endif
         if (i < nrows)
 #pragma unroll
           for (int e = 0; e < 4; ++e)

@@ -72,6 +72,10 @@ template <> struct MfmaOps<bf16_t> {
     typedef float f2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, bf2));
   }
+  // eight 16-bit ones (an MFMA operand)
+  __device__ static __forceinline__ mf_u32x4 ones8() {
+    return mf_u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  }
 };
 
 template <> struct MfmaOps<f16_t> {
@@ -83,6 +87,10 @@ template <> struct MfmaOps<f16_t> {
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     typedef float f2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, h2));
+  }
+  // eight 16-bit ones (an MFMA operand)
+  __device__ static __forceinline__ mf_u32x4 ones8() {
+    return mf_u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
   }
   // hi = RNE(w), lo = RNE(w - hi) in fp16, packed two per word (v_cvt_pk_f16_f32)
   __device__ static __forceinline__ void split2(float w0, float w1, uint32_t& hi,
