@@ -1,13 +1,15 @@
 // Query chunks on 32 x 32 matrix-core tiles (v_mfma_f32_32x32x16_{bf16,f16}).
 //
-// The same page walk and LDS staging as chunk_mfma_kernel (a workgroup of
-// four waves, stages of four 16-token blocks, one per wave, swizzled into LDS,
-// one barrier per stage; here the blocks go from memory straight into LDS by
-// buffer loads with the LDS destination), but each wave owns 32 query rows (two
-// 16-row tiles of the partial layout) and computes 32 tokens (two blocks) per
-// step, so the softmax of a step covers 1024 scores instead of 256 and its
-// fixed costs (max refresh check, weight split, scalar bookkeeping) are shared
-// by four times the matrix work.
+// The same page walk and LDS staging as chunk_mfma_kernel (stages of four
+// 16-token blocks swizzled into LDS, two stage buffers, one barrier per stage;
+// here the blocks go from memory straight into LDS by buffer loads with the
+// LDS destination, shared out over the workgroup's waves), but each wave owns
+// 32 query rows (two 16-row tiles of the partial layout) and computes 32
+// tokens (two blocks) per step, so the softmax of a step covers 1024 scores
+// instead of 256 and its fixed costs (max refresh check, weight rounding,
+// scalar bookkeeping) are shared by four times the matrix work.  A workgroup
+// has four waves (128 rows; two workgroups per CU) or eight (256 rows; one
+// per CU, half the stage loads per row).
 //
 // Lane l = 32 hh + j (j = l % 32):
 //   q . k   S^T = K Q^T: A = K (row m = token tau(m), dims 16i + 8hh .. + 7),
@@ -27,8 +29,12 @@
 //           weights by <= 2^-9 relative, bf16, and the mean by that times the
 //           spread of V).  HELM_CHUNK32_HILO=1 builds the split into hi and lo
 //           16-bit parts instead (weights to ~2^-17, one more MFMA per group).
-// Online softmax per query row with the lazy rescale of the decode kernel.
+// Online softmax per query row with the lazy rescale of the decode kernel, in
+// base-2 units (logits scaled by log2(e) with the softmax scale, weights
+// 2^(x - m); the partials' max goes out in natural units).
 #pragma once
+
+#include <type_traits>
 
 #include "attn_mfma.h"
 
@@ -65,6 +71,8 @@ __device__ __forceinline__ int swz(int t) { return ((t & 3) << 2) | (t >> 2); }
 #ifndef HELM_CHUNK32_HILO
 #define HELM_CHUNK32_HILO 0
 #endif
+constexpr float kLog2E = 1.4426950408889634f;   // log2(e)
+constexpr float kLn2 = 0.6931471805599453f;     // ln(2)
 
 // 16 bytes per lane from a buffer straight into LDS: lane i writes
 // lds_dst + 16 i (the address must be the same in every lane); loads past the
@@ -74,8 +82,12 @@ __device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, void* l
                                            off, 0, 0, 0);
 }
 
-template <typename T, class Src, int FEAT>
-__global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src) {
+// NW waves per workgroup (4: two workgroups per CU; 8: one, which halves the
+// stage loads per query row), 32 query rows each.
+template <typename T, class Src, int FEAT, int NW>
+__global__ __launch_bounds__(NW * 64, 2) void chunk32_mfma_kernel(AttnParams p, Src src) {
+  static_assert(NW == 4 || NW == 8, "waves per workgroup");
+  constexpr int SB = kChunkStage;   // 16-token blocks per stage
   using Ops = MfmaOps<T>;
   using M32 = Mfma32<T>;
   constexpr int kRow = 256;                // bytes per token row (128 dims x 2 B)
@@ -83,11 +95,15 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   constexpr bool kMask = (FEAT & kFeatMask) != 0;
   constexpr bool kCap = (FEAT & kFeatCap) != 0;
   constexpr bool kCausal = (FEAT & kFeatCausal) != 0;
+  // 16-byte-per-lane loads (1 KiB each) a wave issues per stage: a stage is
+  // SB blocks of K and of V, 4 loads each, shared out over the NW waves in
+  // order (wave w takes loads w * kLoads ..), all in one block per wave
+  constexpr int kLoads = 8 * SB / NW;
   // two stage buffers as two objects, so that the compiler sees that the
   // loads filling one never touch the reads of the other:
   // [K, V][block of the stage][16-byte chunk], chunk c of token t at slot
   // t * 16 + (c ^ swz(t)) (see swz)
-  typedef mf_u32x4 StageBuf[2][kChunkStage][kBlk / 16];
+  typedef mf_u32x4 StageBuf[2][SB][kBlk / 16];
   __shared__ StageBuf lds0, lds1;
 
   const int tid = threadIdx.x;
@@ -99,7 +115,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   const int split_local = blockIdx.x;
   const int hk = blockIdx.y % p.Hkv;
   const int n32 = (p.n_qtiles + 1) / 2;                 // 32-row groups of the head
-  const int wt = (blockIdx.y / p.Hkv) * kChunkStage + wave;
+  const int wt = (blockIdx.y / p.Hkv) * NW + wave;
   const bool wave_rows = wt < n32;
   const int wtc = wave_rows ? wt : n32 - 1;
   const int b = blockIdx.z;
@@ -169,6 +185,11 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   const float scale = p.scale;
   const float cap = p.softcap;
   const float inv_cap = kCap ? 1.f / cap : 0.f;
+  // logits, running max and weights in base-2 units: one multiply per score
+  // turns q . k into x = s * scale * log2(e), and each weight is 2^(x - m)
+  const float scale2 = scale * kLog2E;
+  const float cap2 = cap * kLog2E;
+  auto sexp = [](float v) { return __builtin_amdgcn_exp2f(v); };
 
   float m = -INFINITY;   // running max of row jr (same in both halves)
 #if HELM_CHUNK32_HILO
@@ -190,7 +211,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
 
   const int bpp = p.bpp;
   const int nblk = npg * bpp;
-  const int nstage = (nblk + kChunkStage - 1) / kChunkStage;
+  const int nstage = (nblk + SB - 1) / SB;
 
   // page records: window [win, win + 64) of the split's pages (the next
   // window is read when the walk enters it, once per 64 pages)
@@ -198,27 +219,31 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   int win = 0;
   int cur_pi = 0, cur_sub = 0;   // page (relative to pg0) and sub-block of the next view
 
-  struct StageView {
-    int ntok[kChunkStage], tok0[kChunkStage];
-    int own_ntok;
+  // a stage's blocks: valid tokens and first token offset of each (kept for
+  // the stage's compute, one stage after its loads were issued), and the
+  // block this wave loads
+  int vnt[2][SB], vt0[2][SB];
+  struct OwnBlock {
+    int ntok;
     const char *kb, *vb;
   };
-  auto view_stage = [&](int st, StageView& sv) {
+  const int own_blk = (wave * kLoads) >> 3;
+  auto view_stage = [&](int st, int (&ntok)[SB], int (&tok0)[SB], OwnBlock& ob) {
 #pragma unroll
-    for (int j = 0; j < kChunkStage; ++j) {
+    for (int j = 0; j < SB; ++j) {
       if (cur_pi - win >= kRecWindow) {   // uniform: the page lies in the next window
         win += kRecWindow;
         lanes = lane_pages(src, b, pg0 + win, lane);
       }
       const PageView pv = lane_page_view(src, lanes, b, pg0 + cur_pi, cur_pi - win, hk);
       const int tok_in = cur_sub * kBlockTok;
-      const int nt = st * kChunkStage + j < nblk ? sclamp(pv.used - tok_in, 0, kBlockTok) : 0;
-      sv.ntok[j] = nt;
-      sv.tok0[j] = pv.tok_off + tok_in;
-      if (j == wave) {
-        sv.own_ntok = nt;
-        sv.kb = pv.k + tok_in * kRow;
-        sv.vb = pv.v + tok_in * kRow;
+      const int nt = st * SB + j < nblk ? sclamp(pv.used - tok_in, 0, kBlockTok) : 0;
+      ntok[j] = nt;
+      tok0[j] = pv.tok_off + tok_in;
+      if (j == own_blk) {
+        ob.ntok = nt;
+        ob.kb = pv.k + tok_in * kRow;
+        ob.vb = pv.v + tok_in * kRow;
       }
       if (++cur_sub == bpp) {
         cur_sub = 0;
@@ -227,19 +252,25 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
     }
   };
 
-  // a stage's block of this wave straight from memory into LDS (no VGPRs):
-  // instruction u writes slots 64u .. 64u + 63, lane i slot 64u + i, which
-  // holds chunk (i & 15) ^ t of token t = 4u + (i >> 4) (the swizzle), so
-  // each lane fetches that chunk; loads past the block's tokens write zeros
-  auto dma_stage = [&](const StageView& sv, StageBuf& dst) {
-    const auto rk = make_rsrc(sv.kb, sv.own_ntok * kRow);
-    const auto rv = make_rsrc(sv.vb, sv.own_ntok * kRow);
+  // this wave's loads of a stage straight from memory into LDS (no VGPRs):
+  // load i = wave * kLoads + k covers K (bit 2 of i clear) or V of the
+  // wave's block, slots 64u .. 64u + 63 with u = i % 4, lane l slot 64u + l,
+  // which holds chunk (l & 15) ^ swz(t) of token t = 4u + (l >> 4) (the
+  // swizzle), so each lane fetches that chunk; loads past the block's tokens
+  // write zeros
+  auto dma_stage = [&](const OwnBlock& ob, StageBuf& dst) {
+    const auto rk = make_rsrc(ob.kb, ob.ntok * kRow);
+    const auto rv = make_rsrc(ob.vb, ob.ntok * kRow);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int k = 0; k < kLoads; ++k) {
+      const int i = wave * kLoads + k;
+      const int u = i & 3;
       const int t = 4 * u + (lane >> 4);
       const int off = t * kRow + 16 * ((lane & 15) ^ swz(t));
-      buf_load16_lds(rk, &dst[0][wave][64 * u], off);
-      buf_load16_lds(rv, &dst[1][wave][64 * u], off);
+      if ((i >> 2) & 1)
+        buf_load16_lds(rv, &dst[1][own_blk][64 * u], off);
+      else
+        buf_load16_lds(rk, &dst[0][own_blk][64 * u], off);
     }
   };
 
@@ -260,38 +291,45 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   // additive mask of row jr for the step of blocks bp, bp + 1 of a stage:
   // tokens 8hh .. 8hh + 7 of each block, bounded by its valid tokens
   float mk_next[16];
-  auto load_step_mask = [&](const StageView& sv, int bp) {
+  auto load_step_mask = [&](const int (&ntok)[SB], const int (&tok0)[SB], int bp) {
     if constexpr (kMask) {
       // (plain loads: the row differs between lanes; past the block's last
       // valid token the index is clamped to it)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int nt = sv.ntok[bp + u];
+        const int nt = ntok[bp + u];
         const int last = max(nt - 1, 0);
-        const float* mb = mrow + sv.tok0[bp + u];
+        const float* mb = mrow + tok0[bp + u];
 #pragma unroll
         for (int i = 0; i < 8; ++i) mk_next[8 * u + i] = nt > 0 ? mb[min(8 * hh + i, last)] : 0.f;
       }
     }
   };
 
-  StageView sv_cur, sv_next;
-  if (nstage > 0) {
-    view_stage(0, sv_cur);
-    dma_stage(sv_cur, lds0);
-    if (wave_rows) load_step_mask(sv_cur, 0);
+  // the first stage's loads
+  {
+    OwnBlock ob;
+    if (nstage > 0) {
+      view_stage(0, vnt[0], vt0[0], ob);
+      dma_stage(ob, lds0);
+      if (wave_rows) load_step_mask(vnt[0], vt0[0], 0);
+    }
   }
   // causal: the workgroup's last query position; stages starting past it
   // add nothing for any of its rows (a causal call lists a launch's pages in
   // token order, so tokens only grow along the walk), and the walk ends
   // there (uniform across the workgroup)
-  const int qrow_end = min(G * S, (int)(blockIdx.y / p.Hkv + 1) * kChunkStage * kChunk32Rows);
+  const int qrow_end = min(G * S, (int)(blockIdx.y / p.Hkv + 1) * NW * kChunk32Rows);
   const int s_last_wg = (qrow_end - 1) / G + coff;
   bool done = false;
-  // stage st computes from `cur` while stage st + 1 loads into `nxt`
-  auto stage = [&](int st, const StageBuf& cur, StageBuf& nxt) {
+  // stage st (view slot K = st % 2) computes from `cur` while the loads of
+  // stage st + 1 go into `nxt` (the buffer stage st - 1 computed from)
+  auto stage = [&](int st, auto kslot, const StageBuf& cur, StageBuf& nxt) {
+    constexpr int K = decltype(kslot)::value;
+    const int (&ntok_c)[SB] = vnt[K];
+    const int (&tok0_c)[SB] = vt0[K];
     if constexpr (kCausal) {
-      if (sv_cur.tok0[0] > s_last_wg) {
+      if (tok0_c[0] > s_last_wg) {
         __builtin_amdgcn_s_waitcnt(0x0F70);   // this stage's loads land before the exit
         done = true;
         return;
@@ -302,41 +340,13 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     __syncthreads();
     if (st + 1 < nstage) {
-      view_stage(st + 1, sv_next);
-      dma_stage(sv_next, nxt);
+      OwnBlock ob;
+      view_stage(st + 1, vnt[K ^ 1], vt0[K ^ 1], ob);
+      dma_stage(ob, nxt);
     }
     if (wave_rows) {
-#pragma unroll
-      for (int bp = 0; bp < kChunkStage; bp += 2) {     // the step's blocks bp, bp + 1
-        const int nt0 = sv_cur.ntok[bp], nt1 = sv_cur.ntok[bp + 1];
-        // the mask of the next step is loaded now, one step ahead of its use
-        float mk[16];
-        if constexpr (kMask) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mk[r] = mk_next[r];
-          if (bp == 0)
-            load_step_mask(sv_cur, 2);
-          else if (st + 1 < nstage)
-            load_step_mask(sv_next, 0);
-        }
-        if (nt0 == 0 && nt1 == 0) continue;   // uniform; an empty block of a step
-                                               // holds zeros and -inf logits
-        // steps that add exactly nothing for any row of the wave are skipped:
-        // causal, every token past the wave's last query position (-inf
-        // logits); masked, every mask value <= -1e30 while every row's max is
-        // already above -1e20 (each weight underflows to 0 and the max stays)
-        if constexpr (kCausal) {
-          if ((nt0 == 0 || sv_cur.tok0[bp] > s_last) && (nt1 == 0 || sv_cur.tok0[bp + 1] > s_last))
-            continue;
-        }
-        if constexpr (kMask) {
-          float mm = mk[0];
-#pragma unroll
-          for (int r = 1; r < 16; ++r) mm = fmaxf(mm, mk[r]);
-          if (!__builtin_amdgcn_ballot_w64(mm > -1e30f) &&
-              !__builtin_amdgcn_ballot_w64(m <= -1e20f))
-            continue;
-        }
+      // q . k of the step of blocks bp, bp + 1: S^T for the wave's 32 rows
+      auto qk = [&](int bp) -> mf_f32x16 {
         mf_f32x16 sc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] = 0.f;
@@ -345,22 +355,44 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
           const mf_u32x4 ka = cur[0][bp + kblk][ktok * 16 + ((2 * i + hh) ^ swz(ktok))];
           sc = M32::mma(ka, qop[i], sc);
         }
+        return sc;
+      };
+      // steps that add exactly nothing for any row of the wave are skipped
+      // (uniform tests): both blocks empty (an empty block holds zeros and
+      // -inf logits), or, causal, every token past the wave's last query
+      // position
+      auto idle_step = [&](int bp) -> bool {
+        const int nt0 = ntok_c[bp], nt1 = ntok_c[bp + 1];
+        if (nt0 == 0 && nt1 == 0) return true;
+        if constexpr (kCausal)
+          return (nt0 == 0 || tok0_c[bp] > s_last) &&
+                 (nt1 == 0 || tok0_c[bp + 1] > s_last);
+        return false;
+      };
+      // logits, online softmax and P . V of one step
+      auto finish = [&](int bp, const mf_f32x16& sc, const float* mk) {
+        const int nt0 = ntok_c[bp], nt1 = ntok_c[bp + 1];
         float x[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float val = sc[r] * scale;
-          if constexpr (kCap) val = tanhf(val * inv_cap) * cap;
-          if constexpr (kMask) val += mk[r];
+          float val;
+          if constexpr (kCap)
+            val = tanhf(sc[r] * scale * inv_cap) * cap2;
+          else
+            val = sc[r] * scale2;
+          // finfo.min masks stay finite, as in natural units (a row masked
+          // everywhere gets equal weights, as HELM's loop gives it)
+          if constexpr (kMask) val = fmaxf(fmaf(mk[r], kLog2E, val), -__FLT_MAX__);
           x[r] = val;
         }
         // the per-token limits, only where a step reaches them (uniform tests):
         // the causal limit when a block's last token is past the wave's first
         // query position, the valid-token limit when a block is partial
         if constexpr (kCausal) {
-          if (max(sv_cur.tok0[bp], sv_cur.tok0[bp + 1]) + kBlockTok - 1 > s_first) {
+          if (max(tok0_c[bp], tok0_c[bp + 1]) + kBlockTok - 1 > s_first) {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-              if (sv_cur.tok0[bp + (r >> 3)] + 8 * hh + (r & 7) > s_vis) x[r] = -INFINITY;
+              if (tok0_c[bp + (r >> 3)] + 8 * hh + (r & 7) > s_vis) x[r] = -INFINITY;
           }
         }
         if (nt0 < kBlockTok || nt1 < kBlockTok) {
@@ -374,7 +406,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
         if (__builtin_amdgcn_ballot_w64(bm > m + kMfmaSlack)) {
           // refresh the row max (both halves of the row agree)
           const float mn = fmaxf(m, fmaxf(bm, __shfl_xor(bm, 32, 64)));
-          const float a = fexp(m - ((mn == -INFINITY) ? 0.f : mn));
+          const float a = sexp(m - ((mn == -INFINITY) ? 0.f : mn));
 #if HELM_CHUNK32_HILO
           lsum *= a;
 #else
@@ -398,7 +430,7 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
         uint32_t hw[8], lw[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          const float w0 = fexp(x[2 * q] - base), w1 = fexp(x[2 * q + 1] - base);
+          const float w0 = sexp(x[2 * q] - base), w1 = sexp(x[2 * q + 1] - base);
 #if HELM_CHUNK32_HILO
           lsum += w0 + w1;
           Ops::split2(w0, w1, hw[q], lw[q]);
@@ -428,13 +460,42 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
           osum = M32::mma(phi, ones, osum);
 #endif
         }
+      };
+      {
+#pragma unroll
+        for (int bp = 0; bp < SB; bp += 2) {     // the step's blocks bp, bp + 1
+          // the mask of the next step is loaded now, one step ahead of its use
+          float mk[16];
+          if constexpr (kMask) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mk[r] = mk_next[r];
+            if (bp + 2 < SB)
+              load_step_mask(ntok_c, tok0_c, bp + 2);
+            else if (st + 1 < nstage)
+              load_step_mask(vnt[K ^ 1], vt0[K ^ 1], 0);
+          }
+          if (idle_step(bp)) continue;
+          // masked, a step whose every mask value is <= -1e30 while every
+          // row's max is already above -1e20 adds exactly nothing (each
+          // weight underflows to 0 and the max stays)
+          if constexpr (kMask) {
+            float mm = mk[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mm = fmaxf(mm, mk[r]);
+            if (!__builtin_amdgcn_ballot_w64(mm > -1e30f) &&
+                !__builtin_amdgcn_ballot_w64(m <= -1e20f))
+              continue;
+          }
+          finish(bp, qk(bp), mk);
+        }
       }
     }
-    sv_cur = sv_next;
   };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
   for (int st = 0; st < nstage && !done; st += 2) {
-    stage(st, lds0, lds1);
-    if (st + 1 < nstage && !done) stage(st + 1, lds1, lds0);
+    stage(st, I0{}, lds0, lds1);
+    if (st + 1 < nstage && !done) stage(st + 1, I1{}, lds1, lds0);
   }
 
   if (!wave_rows) return;
@@ -473,8 +534,9 @@ __global__ __launch_bounds__(256) void chunk32_mfma_kernel(AttnParams p, Src src
   auto part_row = [&](int i) -> int64_t {
     return ((int64_t)(tile0 + (i >> 4)) * p.max_splits + split) * p.rows_per_tile + (i & 15);
   };
+  const float m_nat = m * kLn2;   // the partials' max in natural units
   if (hh == 0 && jr < nrows)
-    *reinterpret_cast<float2*>(&p.ws_ml[part_row(jr) * 2]) = make_float2(m, lrow);
+    *reinterpret_cast<float2*>(&p.ws_ml[part_row(jr) * 2]) = make_float2(m_nat, lrow);
 #pragma unroll
   for (int g = 0; g < 4; ++g)
 #pragma unroll

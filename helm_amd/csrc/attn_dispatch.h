@@ -39,9 +39,12 @@ hipError_t launch_generic(const LaunchSpec& s, hipStream_t st) {
 // Matrix-core kernels: D = 128, q and KV of the same 16-bit type.
 template <typename T, class Src, int FEAT>
 hipError_t launch_mfma_feat(const LaunchSpec& s, const Src& src, hipStream_t st) {
-  if (s.p.row_waves == 2)
-    hipLaunchKernelGGL((chunk32_mfma_kernel<T, Src, FEAT>), s.grid, dim3(256), 0, st, s.p, src);
-  else if (s.p.row_waves)
+  if (s.p.row_waves == 2) {
+    if (s.nw == 8)
+      hipLaunchKernelGGL((chunk32_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), 0, st, s.p, src);
+    else
+      hipLaunchKernelGGL((chunk32_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), 0, st, s.p, src);
+  } else if (s.p.row_waves)
     hipLaunchKernelGGL((chunk_mfma_kernel<T, Src, FEAT>), s.grid, dim3(256), 0, st, s.p, src);
   else if (s.nw == 8)
     hipLaunchKernelGGL((decode_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), 0, st, s.p,

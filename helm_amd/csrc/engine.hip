@@ -168,7 +168,7 @@ void plan_shape(Plan& pl, int G, int q_len, int D, int max_tok_per_page) {
   pl.row_waves = (pl.mfma && pl.n_qtiles >= 2 && env_int("HELM_AMD_ROW_WAVES", 1))
                      ? (env_int("HELM_AMD_CHUNK", 32) == 16 ? 1 : 2)
                      : 0;
-  if (pl.row_waves) pl.nw = kChunkStage;  // four waves per workgroup
+  if (pl.row_waves) pl.nw = kChunkStage;  // four waves per workgroup (see make_plan)
 }
 
 // chunk_mfma_kernel reads its page records in windows: a split may be long
@@ -200,12 +200,27 @@ int make_plan(Plan& pl, int kv_dtype, int q_dtype, int B, int Hq, int Hkv,
   pl.mfma = (choice >= 2 && same16) ? 1 : 0;
   pl.fast = (!pl.mfma && choice >= 1 && same16 && G <= 8) ? 1 : 0;
   plan_shape(pl, G, q_len, D, max_tok_per_page);
+  // chunk32 with eight waves (one workgroup of 256 query rows per CU) where a
+  // KV head has at least 256 rows and the chunk attends over at least twice
+  // its own length: each stage's K/V then crosses into LDS once per 256 rows
+  // instead of once per 128 (512-token chunk over 32k: 0.43 -> 0.41 ms); a
+  // first prompt chunk keeps four (its causal walks end earlier per
+  // workgroup).  HELM_AMD_CHUNK_WAVES = 4 | 8 forces one.
+  if (pl.row_waves == 2) {
+    const int forced = env_int("HELM_AMD_CHUNK_WAVES", 0);
+    const bool eight = forced ? forced == 8
+                              : pl.n_qtiles >= 16 &&
+                                    avg_pages * max_tok_per_page >= 2.0 * q_len;
+    if (eight) pl.nw = 8;
+  }
   int pps = pps_req > 0 ? pps_req : env_int("HELM_AMD_PPS", 0);
   if (pps <= 0) {
     const double units = (double)B * Hkv * pl.qblocks();
-    // one workgroup per CU (two for the chunk kernel, whose 64 KiB of LDS and
-    // 2 waves per SIMD let two share a CU): longer splits mean fewer partials
-    const int target = env_int("HELM_AMD_WG_PER_CU", pl.row_waves ? 2 : 1) * device_cus();
+    // one workgroup per CU (two for the four-wave chunk kernels, whose 64 KiB
+    // of LDS and 2 waves per SIMD let two share a CU): longer splits mean
+    // fewer partials
+    const int target =
+        env_int("HELM_AMD_WG_PER_CU", pl.row_waves && pl.nw == 4 ? 2 : 1) * device_cus();
     const double splits = std::max(1.0, target / units);
     pps = (int)std::ceil(std::max(1.0, avg_pages) / splits);
     pps = std::max(pps, min_pps(pl.bpp, pl.nw));

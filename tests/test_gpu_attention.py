@@ -315,6 +315,53 @@ def test_streaming_d128_row_tiles_causal_and_chunk_mask(Hq, Hkv, S, dtype, kerne
         assert np.abs(out.cpu().double().numpy() - ref).max() <= TOL[dtype]
 
 
+@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("pps", [0, 3])
+@pytest.mark.parametrize("variant", ["chunk_mask", "causal", "softcap_mask"])
+def test_chunk32_workgroup_shapes(waves, pps, variant, monkeypatch):
+    """The 32-row chunk kernel with four- and eight-wave workgroups: 320 query
+    rows per KV head (an eight-wave workgroup of 256 rows and one with two
+    active waves), ragged pages, one or several splits, under HELM's chunk
+    mask, Path 1's causal mask and a soft-cap with the mask, against fp64."""
+    monkeypatch.setenv("HELM_AMD_CHUNK_WAVES", str(waves))
+    if pps:
+        monkeypatch.setenv("HELM_AMD_PPS", str(pps))
+    Hq, Hkv, S, dtype = 32, 8, 80, torch.bfloat16
+    g = torch.Generator().manual_seed(1000 + waves + pps)
+    sizes = [16] * 9 + [11, 16, 16, 5, 16, 16, 16, 16, 16]
+    T = sum(sizes)
+    ks = [torch.randn(1, Hkv, n, 128, generator=g).to(dtype) for n in sizes]
+    vs = [torch.randn(1, Hkv, n, 128, generator=g).to(dtype) for n in sizes]
+    pages, start = [], 0
+    for i, (k, v) in enumerate(zip(ks, vs)):
+        pages.append(_page(k.to(DEV), v.to(DEV), i, start))
+        start += k.size(2)
+    q = (2 * torch.randn(1, Hq, S, 128, generator=g)).to(dtype)
+    K, V = torch.cat(ks, 2).float(), torch.cat(vs, 2).float()
+    past = T - S
+    mn = torch.finfo(torch.float32).min
+    mask = torch.where(torch.arange(T)[None, :] <= past + torch.arange(S)[:, None],
+                       torch.zeros(()), torch.full((), mn))[None, None]
+    if variant == "causal":
+        out = perform_streaming_attention(q.to(DEV), pages)
+        ref = A.attention_fp64(q.float(), K, V, causal=True)
+    elif variant == "chunk_mask":
+        out = perform_streaming_attention(q.to(DEV), pages, attention_mask=mask.to(DEV))
+        ref = A.attention_fp64(q.float(), K, V, mask=mask.numpy())
+    else:
+        # a mask that is not the chunk pattern (every 7th key hidden as well),
+        # so the kernel reads it, with a soft-cap of 30
+        m2 = mask.clone()
+        m2[..., ::7] = mn
+        m2[..., 0] = 0.0
+        out = perform_streaming_attention(q.to(DEV), pages, attention_mask=m2.to(DEV), softcap=30.0)
+        ref = A.attention_fp64(q.float(), K, V, mask=m2.numpy(), softcap=30.0)
+    # rows that see a few keys reach |out| > 4, where the bf16 output's own
+    # rounding (half an ulp: 2^-9 relative) exceeds 1e-2: that term is added
+    err = np.abs(out.cpu().double().numpy() - ref)
+    assert (err <= TOL[dtype] + np.abs(ref) * 2.0 ** -9).all()
+
+
 def test_kernels_agree_at_full_size():
     """The matrix-core and vector-ALU kernels give the same attention (to
     fp32 rounding of their different summation orders) on the full 32k
