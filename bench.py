@@ -698,10 +698,11 @@ def cpu_gemv(args, torch, reps=10, layers=2, seed=7):
     legs = {}
     if kernels.is_available():
         x8 = {k: torch.randn(8, k, generator=g).half() for _, k in GEMV_SHAPES}
-        legs["native"] = lambda ws: [kernels.gemv_fp16(xs[w.shape[1]], w, threads=threads)
-                                     for w in ws]
-        legs["native_8_tokens"] = lambda ws: [kernels.gemv_fp16(x8[w.shape[1]], w,
-                                                                threads=threads) for w in ws]
+        # the product call (HELM's fp16_linear surface), as HELM's leg calls
+        # its extension's helm_fp16_linear
+        legs["native"] = lambda ws: [kernels.fp16_linear(xs[w.shape[1]], w) for w in ws]
+        legs["native_8_tokens"] = lambda ws: [kernels.fp16_linear(x8[w.shape[1]], w)
+                                              for w in ws]
     else:
         res["native"] = {"unavailable": kernels.load_error()}
     if ref is not None:

@@ -68,6 +68,13 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+def error_text(fn: str, rc: int) -> str:
+    """`fn`'s failure with status `rc`, with the library's message."""
+    msg = load().helm_cpu_last_error().decode(errors="replace")
+    kind = "unsupported" if rc == HELM_CPU_E_UNSUPPORTED else "invalid argument"
+    return f"{fn} ({kind}): {msg}"
+
+
 def call(fn: str, *args) -> None:
     """Calls entry point `fn`; a non-zero status raises ValueError
     (invalid arguments) or NotImplementedError (unsupported)."""

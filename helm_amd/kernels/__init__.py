@@ -53,44 +53,52 @@ def isa() -> str:
     return _cpu_native.isa()
 
 
+_F16 = torch.float16
+_entry = None    # helm_cpu_fp16_gemv_batch, bound once the library has loaded
+
+
+def _gemv_entry():
+    global _entry
+    if _entry is None:
+        lib, why = _cpu_native.try_load()
+        if lib is None:
+            raise RuntimeError(f"native fp16 GEMV unavailable: {why}")
+        _entry = lib.helm_cpu_fp16_gemv_batch
+    return _entry
+
+
+def _gemv_into(y: torch.Tensor, x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor],
+               M: int, N: int, K: int, threads: int) -> None:
+    """One native call: y [M, N] = fp16(w x + bias) for contiguous x [M, K], w [N, K]."""
+    code, ptr, b = 0, None, None
+    if bias is not None:
+        if bias.numel() != N or not bias.is_cpu:
+            raise ValueError(f"bias must hold {N} values on the CPU")
+        b = bias.reshape(N).contiguous()
+        if b.dtype is not _F16:
+            b = b.float()
+        code, ptr = (1 if b.dtype is _F16 else 2), b.data_ptr()
+    rc = _gemv_entry()(x.data_ptr(), w.data_ptr(), ptr, code, y.data_ptr(), M, N, K, threads)
+    if rc:
+        raise RuntimeError(_cpu_native.error_text("helm_cpu_fp16_gemv_batch", rc))
+
+
 def gemv_fp16(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
               threads: int = 0) -> torch.Tensor:
     """y = fp16(weight @ x + bias) through libhelm_cpu.so: x [K] or [M, K]
     fp16 (M <= 8 vectors, W read once), weight [N, K] fp16, bias [N] fp16 /
     fp32 or None; returns [N] (or [M, N]) fp16."""
-    if weight.dim() != 2 or weight.dtype != torch.float16 or weight.device.type != "cpu":
+    if weight.dim() != 2 or weight.dtype is not _F16 or not weight.is_cpu:
         raise ValueError("weight must be a 2-D fp16 CPU tensor")
     N, K = weight.shape
-    if x.dtype != torch.float16 or x.device.type != "cpu" or x.numel() % K or x.numel() == 0:
+    if x.dtype is not _F16 or not x.is_cpu or x.numel() % K or x.numel() == 0:
         raise ValueError(f"x must hold a multiple of {K} fp16 values on the CPU")
     M = x.numel() // K
     if M > MAX_BATCH:
         raise ValueError(f"at most {MAX_BATCH} vectors per call, got {M}")
-    lib_ok, why = _cpu_native.try_load()
-    if lib_ok is None:
-        raise RuntimeError(f"native fp16 GEMV unavailable: {why}")
-    w = weight.contiguous()
-    xv = x.reshape(M, K).contiguous()
-    bias_code, bias_ptr, b = 0, None, None
-    if bias is not None:
-        if bias.numel() != N or bias.device.type != "cpu":
-            raise ValueError(f"bias must hold {N} values on the CPU")
-        b = bias.reshape(N).contiguous()
-        if b.dtype != torch.float16:
-            b = b.float()
-        bias_code, bias_ptr = (1 if b.dtype == torch.float16 else 2), b.data_ptr()
-    y = torch.empty(M, N, dtype=torch.float16)
-    try:
-        _cpu_native.call("helm_cpu_fp16_gemv_batch", xv.data_ptr(), w.data_ptr(), bias_ptr,
-                         bias_code, y.data_ptr(), M, N, K, int(threads))
-    except (ValueError, NotImplementedError) as e:
-        raise RuntimeError(str(e)) from None
+    y = torch.empty(M, N, dtype=_F16)
+    _gemv_into(y, x.reshape(M, K).contiguous(), weight.contiguous(), bias, M, N, K, int(threads))
     return y if x.dim() > 1 else y.reshape(N)
-
-
-def _native_applies(input: torch.Tensor, weight: torch.Tensor) -> bool:
-    return (weight.dtype == torch.float16 and input.dtype == torch.float16
-            and weight.device.type == "cpu" and input.device.type == "cpu")
 
 
 def fp16_linear(input: torch.Tensor, weight: torch.Tensor,
@@ -101,17 +109,23 @@ def fp16_linear(input: torch.Tensor, weight: torch.Tensor,
     step) run the native GEMV, the weight read once; any other count (prefill,
     or an empty input) runs F.linear in float32 and rounds to fp16 — HELM's
     branch for every count but 1, the same float32 sums and one rounding;
-    inputs that are not fp16 on the CPU take plain F.linear."""
-    if not _native_applies(input, weight):
+    inputs that are not fp16 on the CPU take plain F.linear.  The decode
+    branch is one native call and one output allocation (a layer's seven
+    linears are a few hundred microseconds in all, so per-call work counts)."""
+    if not (weight.dtype is _F16 and input.dtype is _F16 and weight.is_cpu and input.is_cpu
+            and weight.dim() == 2):
         return F.linear(input, weight, bias)
-    K = weight.shape[1]
-    tokens = input.numel() // K if input.shape[-1] == K else -1
-    if (1 <= tokens <= MAX_BATCH and not os.environ.get("HELM_DISABLE_AVX")
-            and is_available()):
-        y = gemv_fp16(input.reshape(tokens, K), weight, bias)
-        return y.reshape(*input.shape[:-1], weight.shape[0])
-    if input.shape[-1] != K:
-        raise RuntimeError(f"fp16_linear: input last dim ({input.shape[-1]}) != weight K ({K})")
+    N, K = weight.shape
+    shape = input.shape
+    if shape[-1] != K:
+        raise RuntimeError(f"fp16_linear: input last dim ({shape[-1]}) != weight K ({K})")
+    tokens = input.numel() // K
+    if 1 <= tokens <= MAX_BATCH and not os.environ.get("HELM_DISABLE_AVX") and is_available():
+        y = torch.empty(*shape[:-1], N, dtype=_F16)
+        _gemv_into(y, input if input.is_contiguous() else input.contiguous(),
+                   weight if weight.is_contiguous() else weight.contiguous(),
+                   bias, tokens, N, K, 0)
+        return y
     return F.linear(input.float(), weight.float(),
                     bias.float() if bias is not None else None).half()
 
@@ -119,9 +133,7 @@ def fp16_linear(input: torch.Tensor, weight: torch.Tensor,
 def _bound_forward(self: nn.Linear, x: torch.Tensor) -> torch.Tensor:
     """The forward bound onto a patched nn.Linear: the native GEMV path when
     the weight and input are fp16 on the CPU at call time, else F.linear."""
-    if _native_applies(x, self.weight):
-        return fp16_linear(x, self.weight, self.bias)
-    return F.linear(x, self.weight, self.bias)
+    return fp16_linear(x, self.weight, self.bias)
 
 
 def patch_cpu_linears(module: nn.Module, verbose: bool = False) -> int:

@@ -261,19 +261,24 @@ def test_reference_kernel_within_oracle_bound_and_beside_ours(N, K, bias):
 @needs_kernel
 @pytest.mark.parametrize("isa", ["auto", "avx2"])
 @pytest.mark.parametrize("M", [2, 3, 4, 5, 7, 8])
-def test_batch_equals_single_calls_and_oracle(M, isa, monkeypatch):
-    """M vectors in one call (W read once): each output row equals the
-    single-vector call on that vector bit for bit (same summation order), and
-    lies within the oracle's bound; odd N and K exercise every tail."""
+def test_batch_is_invariant_and_within_oracle(M, isa, monkeypatch):
+    """M vectors in one call (W read once): each output row equals that
+    vector's row in a two-vector call bit for bit (the batched kernel's
+    summation order depends on K alone, not on the batch size, grouping or
+    thread count), and lies within the oracle's bound, as the one-vector call
+    (its own order) does; odd N and K exercise every tail."""
     if isa == "avx2":
         monkeypatch.setenv("HELM_CPU_ISA", "avx2")
     N, K = 203, 517
     x, W, b = _rand((M, K), 70 + M), _rand((N, K), 71), _rand((N,), 72)
     y = kernels.gemv_fp16(x, W, b)
     assert y.shape == (M, N)
+    assert torch.equal(kernels.gemv_fp16(x, W, b, threads=3), y)
     for m in range(M):
-        assert torch.equal(y[m], kernels.gemv_fp16(x[m], W, b))
+        pair = torch.stack([x[m], x[(m + 1) % M]])
+        assert torch.equal(y[m], kernels.gemv_fp16(pair, W, b)[0])
         _check(y[m], x[m], W, b)
+        _check(kernels.gemv_fp16(x[m], W, b), x[m], W, b)
 
 
 @needs_kernel
