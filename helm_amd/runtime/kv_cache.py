@@ -275,10 +275,76 @@ class LayerKVCache:
         return int(last["tok_off"]) + int(last["used"])
 
     def records(self):
-        """The pages' ``helm_page`` records in token order (a view), or None."""
+        """The pages' ``helm_page`` records in token order (a view), or None
+        (validated first in the validation mode: ``check_records``)."""
         if not self._rec_ok:
             return None
+        if check_records_enabled():
+            self.check_records()
         return self._rec[:len(self.pages)]
+
+    def check_records(self, device: Optional[torch.device] = None) -> None:
+        """Validation mode (``HELM_AMD_CHECK_RECORDS=1`` runs it before every
+        launch that reads this layer's records): every record must describe
+        its page as the page is now — K/V addresses and head stride of the
+        page's tensors, its used tokens, the running token offset, the host
+        flag of its device — and every byte the kernel may read through it
+        (Hkv heads x the page's capacity x D) must lie inside the page
+        tensors' own storage.  With `device`, the device-resident copy is
+        read back and must equal the host records (the tail record carrying
+        the tail page's capacity).  Raises RuntimeError naming the layer,
+        page and field; launches nothing."""
+        n = len(self.pages)
+        if not self._rec_ok:
+            raise RuntimeError(f"layer {self.layer_id}: records disabled (a page the kernel "
+                               "cannot read in place)")
+        rec = self._rec[:n]
+        off = 0
+        for i, page in enumerate(self.pages):
+            where = f"layer {self.layer_id} page {i} (id {page.page_id})"
+            fields = _page_record_fields(page)
+            if fields is None:
+                raise RuntimeError(f"{where}: not readable in place")
+            r = rec[i]
+            want = {"k": fields[0], "v": fields[1], "head_stride": fields[2],
+                    "used": page.used_tokens, "tok_off": off,
+                    "flags": _native.HELM_PAGE_HOST if fields[3] else 0}
+            for name, value in want.items():
+                if int(r[name]) != int(value):
+                    raise RuntimeError(f"{where}: record {name} = {int(r[name])}, "
+                                       f"page has {int(value)}")
+            off += page.used_tokens
+            k, v = page.k_tensor, page.v_tensor
+            es = k.element_size()
+            span = ((k.size(1) - 1) * k.stride(1) + max(page.capacity_tokens, page.used_tokens)
+                    * k.size(3)) * es
+            for name, t, addr in (("k", k, fields[0]), ("v", v, fields[1])):
+                st = t.untyped_storage()
+                lo, hi = st.data_ptr(), st.data_ptr() + st.nbytes()
+                if not (lo <= addr and addr + span <= hi):
+                    raise RuntimeError(f"{where}: {name} reads [{addr:#x}, {addr + span:#x}) "
+                                       f"outside its storage [{lo:#x}, {hi:#x})")
+        if off != self.total_tokens_recorded():
+            raise RuntimeError(f"layer {self.layer_id}: token offsets end at "
+                               f"{self.total_tokens_recorded()}, pages hold {off}")
+        if device is not None and n:
+            if self._dev is None or self._dev_all or self._dev_dirty:
+                raise RuntimeError(f"layer {self.layer_id}: device records not uploaded")
+            rb = _native.PAGE_DTYPE.itemsize
+            dev = self._dev[:n * rb].cpu().numpy().view(_native.PAGE_DTYPE)
+            host = rec.copy()
+            host["used"][-1] = max(int(host["used"][-1]), self.tail_page.capacity_tokens)
+            bad = np.flatnonzero(dev != host)
+            if len(bad):
+                raise RuntimeError(f"layer {self.layer_id}: device record {int(bad[0])} differs "
+                                   f"from the host record ({dev[bad[0]]} vs {host[bad[0]]})")
+
+
+def check_records_enabled() -> bool:
+    """``HELM_AMD_CHECK_RECORDS`` set (to anything but 0): every launch that
+    reads layer records validates them first (``LayerKVCache.check_records``)."""
+    v = os.environ.get("HELM_AMD_CHECK_RECORDS")
+    return bool(v) and v != "0"
 
 
 def _used_bytes(page: KVPage) -> int:
@@ -948,6 +1014,9 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
     stream = _engine.stream_ptr(device)
     ptrs = np.array([layer._device_records(device, eng, stream).data_ptr() for layer in layers],
                     dtype=np.uint64)
+    if check_records_enabled():
+        for layer in layers:
+            layer.check_records(device)
     npages = np.array([len(layer.pages) for layer in layers], dtype=np.int32)
     tokens = np.array(lens, dtype=np.int32)
     if causal:

@@ -205,7 +205,9 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out,
  * are min(used, seq_tokens[b] - tok_off)).  page_tokens bounds `used`.
  * Every page must be readable by the device: device memory, or pinned host
  * memory mapped at the same address (helm_host_pages_in_place); records are
- * not checked.  aligned16 != 0 promises 16-byte aligned K/V bases and head
+ * not read on the host (the Python runtime's validation mode,
+ * HELM_AMD_CHECK_RECORDS=1, checks them and their device copy against the
+ * pages before every launch).  aligned16 != 0 promises 16-byte aligned K/V bases and head
  * strides.  B <= 16 (HELM_E_UNSUPPORTED otherwise).  Same semantics as
  * helm_stream_attn otherwise; the engine's workspace serves the split
  * partials, so calls on one engine are ordered on one stream. */

@@ -1198,3 +1198,39 @@ def test_raw_stream_pointer_is_torchs_current_stream():
     with torch.cuda.stream(s):
         assert engine.stream_ptr(DEV) == s.cuda_stream
     assert engine.stream_ptr(torch.device("cuda")) == torch.cuda.current_stream().cuda_stream
+
+
+def test_record_validation_mode_checks_the_device_copy(monkeypatch):
+    """HELM_AMD_CHECK_RECORDS=1 on the device-records path: decode steps
+    through _decode_batched validate every layer's records and read back
+    their device copy (results unchanged, against fp64); a device record
+    that drifted from its page (here a smaller used count: a harmless
+    change, should the check miss it) makes the next call raise before any
+    launch."""
+    monkeypatch.setenv("HELM_AMD_CHECK_RECORDS", "1")
+    Hq, Hkv, D, T, dtype = 8, 2, 128, 200, torch.bfloat16
+    a = KVAllocator(1, Hkv, D, page_size=16, dtype=dtype)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12)
+    g = torch.Generator(device=DEV).manual_seed(61)
+    k = torch.randn((1, Hkv, T, D), generator=g, device=DEV, dtype=dtype)
+    v = torch.randn((1, Hkv, T, D), generator=g, device=DEV, dtype=dtype)
+    mgr.append_prefill(0, k, v)
+    K, V = k[0].cpu(), v[0].cpu()
+    for step in range(3):
+        q = torch.randn((1, Hq, 1, D), generator=g, device=DEV, dtype=dtype)
+        kn = torch.randn((1, Hkv, 1, D), generator=g, device=DEV, dtype=dtype)
+        vn = torch.randn((1, Hkv, 1, D), generator=g, device=DEV, dtype=dtype)
+        out = _decode_batched([mgr], q, kn, vn, 0, 1 / math.sqrt(D), None)
+        K, V = torch.cat([K, kn[0].cpu()], 1), torch.cat([V, vn[0].cpu()], 1)
+        ref = A.attention_fp64_batched(q[0].float().cpu(), K.float(), V.float())
+        assert (out[0].double().cpu() - ref).abs().max().item() <= 1e-2
+    layer = mgr.layers[0]
+    torch.cuda.synchronize()
+    rb = _native.PAGE_DTYPE.itemsize
+    dev = layer._dev[:rb].cpu().numpy().view(_native.PAGE_DTYPE).copy()
+    dev["used"][0] -= 1
+    layer._dev[:rb].copy_(torch.from_numpy(dev.view(np.uint8)).to(DEV))
+    q = torch.randn((1, Hq, 1, D), generator=g, device=DEV, dtype=dtype)
+    with pytest.raises(RuntimeError, match="device record 0 differs"):
+        perform_streaming_attention(q, mgr.iterate_layer_pages(0))
+    mgr.clear()

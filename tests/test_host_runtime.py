@@ -386,6 +386,46 @@ def test_layer_records_follow_pages():
                                             if p.state == "CPU")
 
 
+def test_record_validation_mode(monkeypatch):
+    """HELM_AMD_CHECK_RECORDS=1: records are validated against their pages
+    whenever they are handed out (prefill, decode and eviction pass), and a
+    record that no longer describes its page — wrong used count, token
+    offset or address, or a page whose capacity reaches past its storage —
+    raises RuntimeError naming the layer and page instead of reaching a
+    kernel."""
+    monkeypatch.setenv("HELM_AMD_CHECK_RECORDS", "1")
+    H, D, P = 2, 8, 4
+    a = _CpuBackedGpuAllocator(2, H, D, page_size=P, dtype=torch.float16)
+    mgr = KVCacheManager(a, gpu_high_watermark_bytes=2 * (2 * H * P * D * 2))
+    rng = np.random.default_rng(9)
+    for _ in range(40):
+        lid = int(rng.integers(0, 2))
+        if rng.random() < 0.3:
+            mgr.append_prefill(lid, *_kv(int(rng.integers(1, 10))))
+        else:
+            mgr.append_decode(lid, *_kv(1))
+        for layer in mgr.layers.values():
+            assert layer.records() is not None        # validated, consistent
+    layer = mgr.layers[0]
+    assert len(layer.pages) >= 3
+    for field, delta in (("used", -1), ("tok_off", 1), ("k", 64), ("head_stride", 1)):
+        saved = int(layer._rec[field][1])
+        layer._rec[field][1] = saved + delta
+        with pytest.raises(RuntimeError, match=f"layer 0 page 1 .*{field}"):
+            layer.records()
+        layer._rec[field][1] = saved
+    assert layer.records() is not None
+    page = layer.pages[0]
+    cap = page.capacity_tokens
+    page.capacity_tokens = 10 ** 7     # past the end of the slot arena it lives in
+    with pytest.raises(RuntimeError, match="outside its storage"):
+        layer.records()
+    page.capacity_tokens = cap
+    monkeypatch.delenv("HELM_AMD_CHECK_RECORDS")
+    layer._rec["used"][1] += 1
+    assert layer.records() is not None                # not checked outside the mode
+
+
 def test_external_layer_changes_rebuild_the_heap():
     H, D, P = 2, 4, 4
     a = _CpuBackedGpuAllocator(3, H, D, page_size=P, dtype=torch.float32)
