@@ -134,6 +134,18 @@ def call(fn: str, *args) -> None:
     check(fn, getattr(load(), fn)(*args))
 
 
+_entries = {}
+
+
+def entry(fn: str):
+    """Entry point `fn` of the loaded library, bound once (for the per-call
+    paths: the caller checks the status with ``check``)."""
+    f = _entries.get(fn)
+    if f is None:
+        f = _entries[fn] = getattr(load(), fn)
+    return f
+
+
 def ptr(a: np.ndarray) -> int:
     """Address of a C-contiguous numpy array's data."""
     assert a.flags["C_CONTIGUOUS"]

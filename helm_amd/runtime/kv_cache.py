@@ -23,6 +23,7 @@ from __future__ import annotations
 import heapq
 import math
 import os
+import threading
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
@@ -404,6 +405,8 @@ class _AppendQueue:
         self.dtype = None
         self.hkv = 0
         self.d = 0
+        self._segs = np.zeros(8, dtype=_native.APPEND_DTYPE)   # reused between flushes
+        self._segs_addr = self._segs.ctypes.data
 
     def add(self, dst_k: torch.Tensor, dst_v: torch.Tensor, dst_tok: int, K: torch.Tensor,
             V: torch.Tensor) -> None:
@@ -427,11 +430,20 @@ class _AppendQueue:
         self.keep.append((K, V))
 
     def flush(self) -> None:
-        if not self.rows:
+        n = len(self.rows)
+        if not n:
             return
-        segs = np.array(self.rows, dtype=_native.APPEND_DTYPE)
-        _native.call("helm_page_append", _native.ptr(segs), len(segs), self.hkv, self.d,
-                     _native.dtype_code(self.dtype), _engine.stream_ptr(self.device))
+        if n > len(self._segs):
+            self._segs = np.zeros(max(n, 2 * len(self._segs)), dtype=_native.APPEND_DTYPE)
+            self._segs_addr = self._segs.ctypes.data
+        segs = self._segs
+        for i, row in enumerate(self.rows):
+            segs[i] = row
+        rc = _native.entry("helm_page_append")(self._segs_addr, n, self.hkv, self.d,
+                                               _native.dtype_code(self.dtype),
+                                               _engine.stream_ptr(self.device))
+        if rc:
+            _native.check("helm_page_append", rc)
         self.rows.clear()
         self.keep.clear()
 
@@ -940,12 +952,15 @@ def _query_and_mask(query: torch.Tensor, Hkv: int, kv_dtype, t_max: int,
     q = query
     if q.dtype != kv_dtype and q.dtype != torch.float32:
         q = q.float()
-    q = q.contiguous()
-    out = torch.empty(q.shape, dtype=q.dtype, device=device)
+    if not q.is_contiguous():
+        q = q.contiguous()
+    out = torch.empty_like(q)
     mask_ptr, mbs, mhs, mqs = None, 0, 0, 0
     m = None
     if attention_mask is not None:
-        m = attention_mask.to(device=device, dtype=torch.float32)
+        m = attention_mask
+        if m.dtype != torch.float32 or m.device != device:
+            m = m.to(device=device, dtype=torch.float32)
         if m.dim() != 4:
             raise ValueError("attention_mask must be 4-D [B, H, q_len, kv_len]")
         Bm, Hm, Sm, Tm = m.shape
@@ -1003,6 +1018,21 @@ def _attend_records_cpu(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarra
     return out if out.dtype == query.dtype else out.to(query.dtype)
 
 
+_tls = threading.local()
+
+
+def _seq_args(B: int):
+    """This thread's (record pointers, page counts, token counts) argument
+    arrays for a call over B sequences — views of arrays kept between calls
+    (the native call reads them before it returns) — and their addresses."""
+    a = getattr(_tls, "seq_args", None)
+    if a is None or len(a[0]) < B:
+        n = max(16, B)
+        arrs = (np.zeros(n, np.uint64), np.zeros(n, np.int32), np.zeros(n, np.int32))
+        a = _tls.seq_args = arrs + (tuple(x.ctypes.data for x in arrs),)
+    return a[0][:B], a[1][:B], a[2][:B], a[3]
+
+
 def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Sequence[int],
                    Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
                    softcap: Optional[float], causal: int) -> torch.Tensor:
@@ -1012,13 +1042,14 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
     device = query.device
     eng = _engine.get_engine(device)
     stream = _engine.stream_ptr(device)
-    ptrs = np.array([layer._device_records(device, eng, stream).data_ptr() for layer in layers],
-                    dtype=np.uint64)
+    ptrs, npages, tokens, addrs = _seq_args(len(layers))
+    for b, layer in enumerate(layers):
+        ptrs[b] = layer._device_records(device, eng, stream).data_ptr()
+        npages[b] = len(layer.pages)
+        tokens[b] = lens[b]
     if check_records_enabled():
         for layer in layers:
             layer.check_records(device)
-    npages = np.array([len(layer.pages) for layer in layers], dtype=np.int32)
-    tokens = np.array(lens, dtype=np.int32)
     if causal:
         # causal c: keys from S + c - 1 on are masked for every row; the pages
         # holding only such keys are left out (records are in token order)
@@ -1030,6 +1061,11 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
                                                 "left"))
     page_tokens = max(layer._page_tokens for layer in layers)
     aligned = all(layer._aligned16 for layer in layers)
+    B = len(layers)
+    if B <= _MAX_SEQS:
+        t_max = int(tokens[0]) if B == 1 else int(tokens.max())
+        return _launch_seqs(query, addrs, t_max, page_tokens, aligned, Hkv, kv_dtype, scale,
+                            attention_mask, softcap, causal)
     return _attend_device_records(query, ptrs, npages, tokens, page_tokens, aligned, Hkv,
                                   kv_dtype, scale, attention_mask, softcap, causal)
 
@@ -1041,33 +1077,48 @@ def _attend_device_records(query: torch.Tensor, ptrs: np.ndarray, npages: np.nda
     """helm_paged_attn_seqs over record arrays already in device memory:
     sequence b reads npages[b] records at ptrs[b] (token order), tokens[b]
     tokens; at most 16 sequences per call (more are issued in groups)."""
-    device = query.device
     B = query.size(0)
-    if B > 16:
+    if B > _MAX_SEQS:
         outs = []
-        for b0 in range(0, B, 16):
+        for b0 in range(0, B, _MAX_SEQS):
             m = attention_mask
             if m is not None and m.size(0) > 1:
-                m = m[b0:b0 + 16]
+                m = m[b0:b0 + _MAX_SEQS]
             outs.append(_attend_device_records(
-                query[b0:b0 + 16], ptrs[b0:b0 + 16], npages[b0:b0 + 16], tokens[b0:b0 + 16],
-                page_tokens, aligned, Hkv, kv_dtype, scale, m, softcap, causal))
+                query[b0:b0 + _MAX_SEQS], ptrs[b0:b0 + _MAX_SEQS], npages[b0:b0 + _MAX_SEQS],
+                tokens[b0:b0 + _MAX_SEQS], page_tokens, aligned, Hkv, kv_dtype, scale, m,
+                softcap, causal))
         return torch.cat(outs, 0)
-    _, Hq, S, D = query.shape
     t_max = int(tokens[0]) if B == 1 else int(tokens.max())
-    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, t_max, attention_mask)
     if ptrs.dtype != np.uint64 or not ptrs.flags["C_CONTIGUOUS"]:
         ptrs = np.ascontiguousarray(ptrs, dtype=np.uint64)
     if npages.dtype != np.int32 or not npages.flags["C_CONTIGUOUS"]:
         npages = np.ascontiguousarray(npages, dtype=np.int32)
     if tokens.dtype != np.int32 or not tokens.flags["C_CONTIGUOUS"]:
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)
-    _native.call("helm_paged_attn_seqs", _engine.get_engine(device), q.data_ptr(),
-                 out.data_ptr(), B, Hq, Hkv, S, D, _native.ptr(ptrs), _native.ptr(npages),
-                 _native.ptr(tokens), page_tokens, 1 if aligned else 0, float(scale),
-                 float(softcap) if softcap is not None else 0.0, *margs, int(causal),
-                 _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype),
-                 _engine.stream_ptr(device))
+    return _launch_seqs(query, (_native.ptr(ptrs), _native.ptr(npages), _native.ptr(tokens)),
+                        t_max, page_tokens, aligned, Hkv, kv_dtype, scale, attention_mask,
+                        softcap, causal, (ptrs, npages, tokens))
+
+
+_MAX_SEQS = 16     # sequences one helm_paged_attn_seqs call carries
+
+
+def _launch_seqs(query: torch.Tensor, addrs, t_max: int, page_tokens: int, aligned: bool,
+                 Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
+                 softcap: Optional[float], causal: int, _keep_args=None) -> torch.Tensor:
+    """The helm_paged_attn_seqs call itself: `addrs` = host addresses of the
+    B record pointers, page counts and token counts (B <= 16)."""
+    device = query.device
+    B, Hq, S, D = query.shape
+    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, t_max, attention_mask)
+    rc = _native.entry("helm_paged_attn_seqs")(
+        _engine.get_engine(device), q.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
+        addrs[0], addrs[1], addrs[2], page_tokens, 1 if aligned else 0, float(scale),
+        float(softcap) if softcap is not None else 0.0, *margs, int(causal),
+        _native.dtype_code(kv_dtype), _native.dtype_code(q.dtype), _engine.stream_ptr(device))
+    if rc:
+        _native.check("helm_paged_attn_seqs", rc)
     return out if out.dtype == query.dtype else out.to(query.dtype)
 
 
