@@ -82,6 +82,38 @@ def _require_hip(t: torch.Tensor, what: str) -> None:
         raise RuntimeError(f"{what}: tensors must be on a HIP device (no CPU attention path)")
 
 
+def _own_append(kvcm) -> bool:
+    """True when `kvcm` is a KVCacheManager whose append_decode is the class's
+    own: its token writes can then be queued and issued as one launch for the
+    batch, and its layers' page records serve attention.  Any other cache
+    object HELM's forwards accept (one that only has append_decode /
+    iterate_layer_pages / all_gpu_resident, or a manager whose append_decode
+    a caller replaced on the instance, e.g. to count calls) gets its public
+    append_decode called per item, as kv_offload.py:147 and :617 do."""
+    return (isinstance(kvcm, KVCacheManager) and "append_decode" not in kvcm.__dict__
+            and type(kvcm).append_decode is KVCacheManager.append_decode)
+
+
+def _append_decode_items(kvcms, k, v, layer_idx: int, bsz: int, residency_kwarg: bool) -> None:
+    """Each item's token into its pages, then its residency policy (HELM's
+    append_decode(..., skip_residency=False) per item); the writes of the
+    managers that allow it go out as one append launch.  `residency_kwarg`:
+    pass skip_residency=False to a foreign append_decode (kv_offload.py:147)
+    or call it with the token only (the Gemma-2 forward, :617)."""
+    queued = []
+    for i in range(bsz):
+        c = kvcms[i]
+        if _own_append(c):
+            c._append_decode_deferred(layer_idx, k[i:i + 1], v[i:i + 1])
+            c._enforce_residency_policy()
+            queued.append(c._appends)
+        elif residency_kwarg:
+            c.append_decode(layer_idx, k[i:i + 1], v[i:i + 1], skip_residency=False)
+        else:
+            c.append_decode(layer_idx, k[i:i + 1], v[i:i + 1])
+    _flush_appends(queued)
+
+
 # ── decode (kv_offload.py:86-186) ──────────────────────────────────────────────
 def _decode_batched(kvcms, q, k, v, layer_idx: int, scale: float,
                     attention_mask: Optional[torch.Tensor] = None):
@@ -96,7 +128,7 @@ def _decode_batched(kvcms, q, k, v, layer_idx: int, scale: float,
     bsz = q.shape[0]
     Hkv, D = k.shape[1], q.shape[-1]
 
-    if kvcms[0].use_contiguous:
+    if getattr(kvcms[0], "use_contiguous", False):
         if kvcms[0].cont_seq_len < kvcms[0].cont_capacity:
             _require_hip(q, "_decode_batched")
             out = _decode_contiguous(kvcms[:bsz], q, k, v, layer_idx, Hkv, scale,
@@ -109,12 +141,7 @@ def _decode_batched(kvcms, q, k, v, layer_idx: int, scale: float,
         for kvcm in kvcms:
             kvcm.migrate_contiguous_to_pages()
 
-    # each item: append then residency, as HELM's append_decode does; the
-    # token writes of all items go out as one append launch
-    for i in range(bsz):
-        kvcms[i]._append_decode_deferred(layer_idx, k[i:i + 1], v[i:i + 1])
-        kvcms[i]._enforce_residency_policy()
-    _flush_appends([kvcm._appends for kvcm in kvcms])
+    _append_decode_items(kvcms, k, v, layer_idx, bsz, True)
     return _decode_attend(kvcms, q, layer_idx, Hkv, scale, attention_mask)
 
 
@@ -153,7 +180,6 @@ def _decode_attend(kvcms, q, layer_idx: int, Hkv: int, scale: float,
     if all(kvcms[i].all_gpu_resident(layer_idx) for i in range(bsz)):
         lists = [[p for p in pages if p.used_tokens > 0] for pages in all_pages]
         if all(lists):
-            _require_hip(q, "_decode_batched")
             dtype = lists[0][0].k_tensor.dtype
             seqs = [[_page_segments(p, 0, 1, Hkv, D, dtype) for p in lst] for lst in lists]
             return _attend(q, seqs, Hkv, dtype, scale, attention_mask, None, False)
@@ -202,7 +228,8 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
     None when a layer's records are unusable, so the page-list path runs.
     """
     cpu = q.device.type != "cuda"
-    if not cpu and not _async_kv_prefetch_enabled():
+    if (not cpu and not _async_kv_prefetch_enabled()) or not all(
+            isinstance(kvcm, KVCacheManager) for kvcm in kvcms):
         return None
     layers = [kvcm.layers.get(layer_idx) for kvcm in kvcms]
     recs = []
@@ -260,7 +287,7 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
 
 def _cached_tokens(kvcm, layer_idx: int) -> int:
     """Tokens in the layer's active pages (from its records when they serve)."""
-    layer = kvcm.layers.get(layer_idx)
+    layer = kvcm.layers.get(layer_idx) if isinstance(kvcm, KVCacheManager) else None
     if layer is not None and layer.records() is not None and not layer._n_other:
         n = len(layer.pages)
         return int(layer._rec["tok_off"][n - 1]) + int(layer._rec["used"][n - 1]) if n else 0
@@ -305,7 +332,8 @@ def _prefill_from_records(kvcms, q, layer_idx: int, scale: float,
     as causal masking at its offset), from the layers' records;
     None when they cannot serve (the page-list path then runs)."""
     cpu = q.device.type != "cuda"
-    if not cpu and not _async_kv_prefetch_enabled():
+    if (not cpu and not _async_kv_prefetch_enabled()) or not all(
+            isinstance(kvcm, KVCacheManager) for kvcm in kvcms):
         return None
     B, _, S, D = q.shape
     layers = [kvcm.layers.get(layer_idx) for kvcm in kvcms[:B]]
@@ -495,6 +523,8 @@ def _gemma2_decode_from_records(attn_self, kvcms, q, layer: int, scale: float, s
     (kv_offload.py:577-613) as one call over the layers' records; None when
     the records cannot serve."""
     bsz = q.shape[0]
+    if not all(isinstance(c, KVCacheManager) for c in kvcms[:bsz]):
+        return None
     layers = [c.layers.get(layer) for c in kvcms[:bsz]]
     if any(L is None or L.records() is None or len(L.pages) == 0 for L in layers):
         return None
@@ -556,7 +586,8 @@ def _decode_front(kvcms, attn_self, arch: _Arch, qp, kp, vp, cos, sin, layer: in
     D = attn_self.head_dim
     dtype, device = qp.dtype, qp.device
     if (device.type != "cuda" or dtype not in _FRONT_DTYPES or len(kvcms) < bsz
-            or any(getattr(c, "use_contiguous", False) for c in kvcms[:bsz])
+            or not all(_own_append(c) for c in kvcms[:bsz])
+            or any(c.use_contiguous for c in kvcms[:bsz])
             or (torch.is_grad_enabled() and (qp.requires_grad or kp.requires_grad))):
         return None
     if (qp.dim() != 3 or qp.size(1) != 1 or kp.shape != vp.shape or kp.dtype != dtype
@@ -615,7 +646,8 @@ def _gemma2_decode_attend(attn_self, kvcms, q, layer: int, scale: float, softcap
     outs = []
     for i in range(q.shape[0]):
         pages = kvcms[i].iterate_layer_pages(layer)
-        key_length = sum(p.used_tokens for p in pages if p.used_tokens > 0 and p.state != "DEAD")
+        key_length = sum(p.used_tokens for p in pages
+                         if p.used_tokens > 0 and getattr(p, "state", None) != "DEAD")
         item_mask = (_gemma2_sliding_window_mask(
             attn_self, attention_mask[i:i + 1] if attention_mask is not None else None,
             cache_position, key_length, device=q.device, dtype=q.dtype)
@@ -682,10 +714,7 @@ def _make_forward(kvcms, arch: _Arch):
                                                        k.shape[-2], device=q.device, dtype=q.dtype)
                 out = _local_attention(q, k, v, scale, mask, softcap)
         elif arch.gemma:
-            for i in range(bsz):
-                kvcms[i]._append_decode_deferred(layer, k[i:i + 1], v[i:i + 1])
-                kvcms[i]._enforce_residency_policy()
-            _flush_appends([c._appends for c in kvcms])
+            _append_decode_items(kvcms, k, v, layer, bsz, False)
             out = _gemma2_decode_attend(attn_self, kvcms, q, layer, scale, softcap,
                                         attention_mask, cache_position)
         else:
