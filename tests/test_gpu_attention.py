@@ -362,6 +362,30 @@ def test_chunk32_workgroup_shapes(waves, pps, variant, monkeypatch):
     assert (err <= TOL[dtype] + np.abs(ref) * 2.0 ** -9).all()
 
 
+@pytest.mark.parametrize("scale", [0.05, -0.07, 0.0])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_chunk32_causal_scale_sign(scale, dtype):
+    """The chunk kernel under caller-chosen softmax scales: a custom one, a
+    negative one (the running max must follow the scaled logits, not the raw
+    q . k) and zero (uniform weights over each row's visible keys).  Path 1's
+    causal mask, 320 query rows per KV head, against fp64."""
+    Hq, Hkv, S = 32, 8, 80
+    g = torch.Generator().manual_seed(77 + int(scale * 100) + (dtype == torch.float16))
+    sizes = [16] * 7 + [9, 16, 16, 3]
+    ks = [torch.randn(1, Hkv, n, 128, generator=g).to(dtype) for n in sizes]
+    vs = [torch.randn(1, Hkv, n, 128, generator=g).to(dtype) for n in sizes]
+    pages, start = [], 0
+    for i, (k, v) in enumerate(zip(ks, vs)):
+        pages.append(_page(k.to(DEV), v.to(DEV), i, start))
+        start += k.size(2)
+    q = (3 * torch.randn(1, Hq, S, 128, generator=g)).to(dtype)
+    K, V = torch.cat(ks, 2).float(), torch.cat(vs, 2).float()
+    out = perform_streaming_attention(q.to(DEV), pages, scale=scale)
+    ref = A.attention_fp64(q.float(), K, V, scale=scale, causal=True)
+    err = np.abs(out.cpu().double().numpy() - ref)
+    assert (err <= TOL[dtype] + np.abs(ref) * 2.0 ** -9).all()
+
+
 def test_kernels_agree_at_full_size():
     """The matrix-core and vector-ALU kernels give the same attention (to
     fp32 rounding of their different summation orders) on the full 32k
