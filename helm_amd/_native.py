@@ -71,6 +71,10 @@ SIGNATURES = {
         ctypes.c_int, ctypes.c_int, _c_void_p, _c_void_p, _c_void_p, ctypes.c_int,
         ctypes.c_int, _f32, _f32, _c_void_p, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, _c_void_p]),
+    "helm_paged_attn_seqs_append": (ctypes.c_int, [
+        _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+        ctypes.c_int, _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, _f32, _f32, _c_void_p,
+        _i64, _i64, _i64, ctypes.c_int, _c_void_p, _c_void_p]),
     "helm_upload": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),
     "helm_host_pages_in_place": (ctypes.c_int, [_c_void_p, _c_void_p, ctypes.c_int,
                                                 ctypes.c_int, ctypes.c_int, ctypes.c_int,

@@ -359,6 +359,14 @@ struct DescSrc {
   const helm_page* seq_pages[kSeqArgs];
   int seq_n[kSeqArgs];
   int seq_tokens[kSeqArgs];
+  // decode calls that also write each sequence's new token (by_value only):
+  // for b < app_n, head h of sequence b's token (D = 128, 16-bit) is at
+  // app_k[b] / app_v[b] + h * app_hs[b] elements and goes to the last used
+  // slot of the sequence's last page (decode_mfma_kernel)
+  int app_n;
+  const char* app_k[kSeqArgs];
+  const char* app_v[kSeqArgs];
+  int64_t app_hs[kSeqArgs];
 
   __device__ __forceinline__ const helm_page* base(int b) const {
     return by_value ? seq_pages[b] : pages + sload(seq_off + b);

@@ -33,6 +33,8 @@
 // the splits.
 #pragma once
 
+#include <type_traits>
+
 #include "attn_kernel.h"
 
 namespace helm {
@@ -381,6 +383,27 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   const int split = p.split_base + split_local;
   const int pg0 = lo + split_local * p.pps;
   const int npg = min(pg0 + p.pps, hi) - pg0;  // 1..kMfmaMaxPps
+  if constexpr (std::is_same<Src, DescSrc>::value) {
+    // a call that carries the sequences' new tokens: each workgroup whose
+    // split holds the sequence's last page writes its head's token into that
+    // page's last used slot (16 lanes K, 16 lanes V, 16 bytes each), and the
+    // stores are complete before any wave of the workgroup reads the page.
+    // Workgroups of other query tiles of the same head write the same bytes.
+    if (b < src.app_n && pg0 + npg == np) {
+      if (wave == 0) {
+        const PageView tv = src.page(b, np - 1, hk);
+        if (lane < 32 && tv.used > 0) {
+          const int c = lane & 15;
+          const bool isv = lane >= 16;
+          const char* from = (isv ? src.app_v[b] : src.app_k[b]) + hk * src.app_hs[b] * 2 + 16 * c;
+          char* to = const_cast<char*>(isv ? tv.v : tv.k) + (int64_t)(tv.used - 1) * kRow + 16 * c;
+          *reinterpret_cast<uint4*>(to) = *reinterpret_cast<const uint4*>(from);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+      __syncthreads();
+    }
+  }
 
   const float* mrow = nullptr;
   if constexpr (kMask)

@@ -1203,14 +1203,14 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   return engine_mark_upload_consumed(eng, st);
 }
 
-int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
-                         int Hq, int Hkv, int q_len, int D,
-                         const uint64_t* seq_pages, const int32_t* seq_npages,
-                         const int32_t* seq_tokens, int page_tokens,
-                         int aligned16, float scale, float softcap,
-                         const float* mask, int64_t mask_bstride,
-                         int64_t mask_hstride, int64_t mask_qstride, int causal,
-                         int kv_dtype, int q_dtype, void* stream) {
+// helm_paged_attn_seqs, and with `app` (one new token per sequence) the
+// decode call that also writes those tokens (helm_paged_attn_seqs_append).
+static int paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B, int Hq, int Hkv,
+                    int q_len, int D, const uint64_t* seq_pages, const int32_t* seq_npages,
+                    const int32_t* seq_tokens, int page_tokens, int aligned16, float scale,
+                    float softcap, const float* mask, int64_t mask_bstride,
+                    int64_t mask_hstride, int64_t mask_qstride, int causal, int kv_dtype,
+                    int q_dtype, const helm_append_seg* app, void* stream) {
   if (!eng || !q || !out || !seq_pages || !seq_npages || !seq_tokens)
     return fail(HELM_E_INVALID, "null pointer argument");
   if (B <= 0 || Hkv <= 0 || D <= 0 || page_tokens <= 0)
@@ -1239,6 +1239,19 @@ int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
   int rc = make_plan(pl, kv_dtype, q_dtype, B, Hq, Hkv, q_len, D, page_tokens,
                      std::max(max_pages, 1), (double)all_pages / B, 0, al);
   if (rc != HELM_OK) return rc;
+  if (app) {
+    // the token writes run inside the matrix-core decode kernel only
+    if (!(pl.mfma && !pl.row_waves && q_len == 1 && D == 128 && eb == 2))
+      return fail(HELM_E_UNSUPPORTED, "token writes need the matrix-core decode kernel");
+    for (int b = 0; b < B; ++b) {
+      const helm_append_seg& a = app[b];
+      if (a.n_tok != 1 || seq_npages[b] < 1 || seq_tokens[b] < 1 || !a.src_k || !a.src_v)
+        return fail(HELM_E_INVALID, "bad token write for sequence " + std::to_string(b));
+      if ((a.src_k | a.src_v) % 16 != 0 || (a.src_head_stride * eb) % 16 != 0)
+        return fail(HELM_E_UNSUPPORTED, "token source of sequence " + std::to_string(b) +
+                                            " is not 16-byte aligned");
+    }
+  }
   pl.max_splits = std::max(1, (max_pages + pl.pps - 1) / pl.pps);
   pl.fused = fused_merge(pl.max_splits);
   size_plan(pl, B, Hkv, D);
@@ -1258,6 +1271,14 @@ int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
     s.desc.seq_n[b] = seq_npages[b];
     s.desc.seq_tokens[b] = seq_tokens[b];
   }
+  if (app) {
+    s.desc.app_n = B;
+    for (int b = 0; b < B; ++b) {
+      s.desc.app_k[b] = reinterpret_cast<const char*>(app[b].src_k);
+      s.desc.app_v[b] = reinterpret_cast<const char*>(app[b].src_v);
+      s.desc.app_hs[b] = app[b].src_head_stride;
+    }
+  }
   s.kv_dtype = kv_dtype;
   s.q_dtype = q_dtype;
   s.epl = pl.epl;
@@ -1273,6 +1294,33 @@ int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
   e = launch_merge(s, B, Hkv, st);
   if (e != hipSuccess) return hip_fail(e, "merge launch");
   return HELM_OK;
+}
+
+int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
+                         int Hq, int Hkv, int q_len, int D,
+                         const uint64_t* seq_pages, const int32_t* seq_npages,
+                         const int32_t* seq_tokens, int page_tokens,
+                         int aligned16, float scale, float softcap,
+                         const float* mask, int64_t mask_bstride,
+                         int64_t mask_hstride, int64_t mask_qstride, int causal,
+                         int kv_dtype, int q_dtype, void* stream) {
+  return paged_attn_seqs(eng, q, out, B, Hq, Hkv, q_len, D, seq_pages, seq_npages, seq_tokens,
+                         page_tokens, aligned16, scale, softcap, mask, mask_bstride,
+                         mask_hstride, mask_qstride, causal, kv_dtype, q_dtype, nullptr,
+                         stream);
+}
+
+int helm_paged_attn_seqs_append(helm_engine* eng, const void* q, void* out, int B,
+                                int Hq, int Hkv, int D, const uint64_t* seq_pages,
+                                const int32_t* seq_npages, const int32_t* seq_tokens,
+                                int page_tokens, int aligned16, float scale, float softcap,
+                                const float* mask, int64_t mask_bstride,
+                                int64_t mask_hstride, int64_t mask_qstride, int kv_dtype,
+                                const helm_append_seg* tokens, void* stream) {
+  if (!tokens) return fail(HELM_E_INVALID, "null pointer argument");
+  return paged_attn_seqs(eng, q, out, B, Hq, Hkv, 1, D, seq_pages, seq_npages, seq_tokens,
+                         page_tokens, aligned16, scale, softcap, mask, mask_bstride,
+                         mask_hstride, mask_qstride, 0, kv_dtype, kv_dtype, tokens, stream);
 }
 
 int helm_upload(helm_engine* eng, void* dst, const void* src, size_t bytes,

@@ -1035,10 +1035,15 @@ def _seq_args(B: int):
 
 def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Sequence[int],
                    Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
-                   softcap: Optional[float], causal: int) -> torch.Tensor:
+                   softcap: Optional[float], causal: int, tokens_app: Optional[int] = None):
     """One helm_paged_attn_seqs call: sequence b is layers[b]'s pages, read
     through the layer's device-resident records (uploaded only where they
-    changed); lens[b] tokens.  Every page must be device-resident."""
+    changed); lens[b] tokens.  Every page must be device-resident.
+
+    tokens_app: host address of B helm_append_seg rows, each sequence's new
+    decode token, which the call then also writes into the last page
+    (helm_paged_attn_seqs_append); returns None, with nothing launched, when
+    that call cannot take them (the caller writes them and calls again)."""
     device = query.device
     eng = _engine.get_engine(device)
     stream = _engine.stream_ptr(device)
@@ -1062,6 +1067,13 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
     page_tokens = max(layer._page_tokens for layer in layers)
     aligned = all(layer._aligned16 for layer in layers)
     B = len(layers)
+    if tokens_app is not None:
+        if (B > _MAX_SEQS or causal or query.size(2) != 1 or query.size(3) != 128
+                or query.dtype != kv_dtype):
+            return None
+        t_max = int(tokens[0]) if B == 1 else int(tokens.max())
+        return _launch_seqs(query, addrs, t_max, page_tokens, aligned, Hkv, kv_dtype, scale,
+                            attention_mask, softcap, causal, tokens_app=tokens_app)
     if B <= _MAX_SEQS:
         t_max = int(tokens[0]) if B == 1 else int(tokens.max())
         return _launch_seqs(query, addrs, t_max, page_tokens, aligned, Hkv, kv_dtype, scale,
@@ -1106,12 +1118,26 @@ _MAX_SEQS = 16     # sequences one helm_paged_attn_seqs call carries
 
 def _launch_seqs(query: torch.Tensor, addrs, t_max: int, page_tokens: int, aligned: bool,
                  Hkv: int, kv_dtype, scale: float, attention_mask: Optional[torch.Tensor],
-                 softcap: Optional[float], causal: int, _keep_args=None) -> torch.Tensor:
+                 softcap: Optional[float], causal: int, _keep_args=None,
+                 tokens_app: Optional[int] = None):
     """The helm_paged_attn_seqs call itself: `addrs` = host addresses of the
-    B record pointers, page counts and token counts (B <= 16)."""
+    B record pointers, page counts and token counts (B <= 16).  With
+    tokens_app (decode, q in the KV dtype) helm_paged_attn_seqs_append, or
+    None when it does not take the call (nothing launched)."""
     device = query.device
     B, Hq, S, D = query.shape
     q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, t_max, attention_mask)
+    if tokens_app is not None:
+        rc = _native.entry("helm_paged_attn_seqs_append")(
+            _engine.get_engine(device), q.data_ptr(), out.data_ptr(), B, Hq, Hkv, D, addrs[0],
+            addrs[1], addrs[2], page_tokens, 1 if aligned else 0, float(scale),
+            float(softcap) if softcap is not None else 0.0, *margs,
+            _native.dtype_code(kv_dtype), tokens_app, _engine.stream_ptr(device))
+        if rc == _native.HELM_E_UNSUPPORTED:
+            return None
+        if rc:
+            _native.check("helm_paged_attn_seqs_append", rc)
+        return out
     rc = _native.entry("helm_paged_attn_seqs")(
         _engine.get_engine(device), q.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
         addrs[0], addrs[1], addrs[2], page_tokens, 1 if aligned else 0, float(scale),

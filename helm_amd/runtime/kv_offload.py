@@ -23,6 +23,7 @@ from __future__ import annotations
 import importlib
 import math
 import os
+import threading
 import weakref
 from dataclasses import dataclass
 from types import MethodType
@@ -94,12 +95,16 @@ def _own_append(kvcm) -> bool:
             and type(kvcm).append_decode is KVCacheManager.append_decode)
 
 
-def _append_decode_items(kvcms, k, v, layer_idx: int, bsz: int, residency_kwarg: bool) -> None:
+def _append_decode_items(kvcms, k, v, layer_idx: int, bsz: int, residency_kwarg: bool,
+                         flush: bool = True) -> list:
     """Each item's token into its pages, then its residency policy (HELM's
     append_decode(..., skip_residency=False) per item); the writes of the
     managers that allow it go out as one append launch.  `residency_kwarg`:
     pass skip_residency=False to a foreign append_decode (kv_offload.py:147)
-    or call it with the token only (the Gemma-2 forward, :617)."""
+    or call it with the token only (the Gemma-2 forward, :617).  flush=False
+    leaves those writes queued and returns the queues, one per such manager
+    in item order: the caller issues them (or has the attention call write
+    the tokens) before anything reads the pages."""
     queued = []
     for i in range(bsz):
         c = kvcms[i]
@@ -111,7 +116,9 @@ def _append_decode_items(kvcms, k, v, layer_idx: int, bsz: int, residency_kwarg:
             c.append_decode(layer_idx, k[i:i + 1], v[i:i + 1], skip_residency=False)
         else:
             c.append_decode(layer_idx, k[i:i + 1], v[i:i + 1])
-    _flush_appends(queued)
+    if flush:
+        _flush_appends(queued)
+    return queued
 
 
 # ── decode (kv_offload.py:86-186) ──────────────────────────────────────────────
@@ -141,8 +148,11 @@ def _decode_batched(kvcms, q, k, v, layer_idx: int, scale: float,
         for kvcm in kvcms:
             kvcm.migrate_contiguous_to_pages()
 
-    _append_decode_items(kvcms, k, v, layer_idx, bsz, True)
-    return _decode_attend(kvcms, q, layer_idx, Hkv, scale, attention_mask)
+    queued = _append_decode_items(kvcms, k, v, layer_idx, bsz, True, flush=False)
+    if len(queued) != bsz:
+        _flush_appends(queued)
+        queued = None
+    return _decode_attend(kvcms, q, layer_idx, Hkv, scale, attention_mask, queued)
 
 
 def _decode_contiguous(kvcms, q, k, v, layer_idx: int, Hkv: int, scale: float,
@@ -166,14 +176,18 @@ def _decode_contiguous(kvcms, q, k, v, layer_idx: int, Hkv: int, scale: float,
 
 
 def _decode_attend(kvcms, q, layer_idx: int, Hkv: int, scale: float,
-                   attention_mask: Optional[torch.Tensor]):
+                   attention_mask: Optional[torch.Tensor], pending=None):
     """The attention of a decode step once every item's token is in its pages:
     from the layers' records, else HELM's batched or per-item page-list path
-    (kv_offload.py:116-186)."""
+    (kv_offload.py:116-186).  pending: the items' queued token writes, one
+    queue per item, not yet issued (the records call may write them itself)."""
     bsz, D = q.shape[0], q.shape[-1]
-    out = _decode_from_records(kvcms, q, layer_idx, Hkv, D, scale, attention_mask)
+    out = _decode_from_records(kvcms, q, layer_idx, Hkv, D, scale, attention_mask,
+                               pending=pending)
     if out is not None:
         return out
+    if pending:
+        _flush_appends(pending)
 
     all_pages = [kvcms[i].iterate_layer_pages(layer_idx) for i in range(bsz)]
 
@@ -215,17 +229,40 @@ def _flush_appends(queues) -> None:
 
 
 _MAX_SEQ_ARGS = 16     # sequences one helm_paged_attn_seqs call carries
+_tls = threading.local()
+
+
+def _fused_tokens(pending, kv_dtype, device) -> Optional[int]:
+    """Host address of the items' token rows (helm_append_seg, item order) for
+    helm_paged_attn_seqs_append, or None unless every queue holds exactly one
+    one-token write of the KV dtype on `device`.  HELM_AMD_FUSED_APPEND=0
+    keeps the separate append launch."""
+    if os.environ.get("HELM_AMD_FUSED_APPEND") == "0":
+        return None
+    n = len(pending)
+    rows = getattr(_tls, "token_rows", None)
+    if rows is None or len(rows) < n:
+        rows = _tls.token_rows = np.zeros(max(n, _MAX_SEQ_ARGS), dtype=_native.APPEND_DTYPE)
+    for b, queue in enumerate(pending):
+        if (len(queue.rows) != 1 or queue.dtype != kv_dtype or queue.device != device
+                or queue.rows[0][8] != 1):
+            return None
+        rows[b] = queue.rows[0]
+    return rows.ctypes.data
 
 
 def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: float,
                          attention_mask: Optional[torch.Tensor],
-                         softcap: Optional[float] = None):
+                         softcap: Optional[float] = None, pending=None):
     """The decode attention of `_decode_batched` from the layers' page records.
 
     Same outcome as the page-list path below (one batched call when every
     item is GPU-resident, else per-item streaming attention that counts the
     prefetched host pages), without touching each page in Python.  Returns
-    None when a layer's records are unusable, so the page-list path runs.
+    None when a layer's records are unusable, so the page-list path runs
+    (its caller then issues `pending`).  pending: one queue per item holding
+    that item's new token, not yet written; every page on the device, the
+    attention call writes the tokens itself, else they are issued first.
     """
     cpu = q.device.type != "cuda"
     if (not cpu and not _async_kv_prefetch_enabled()) or not all(
@@ -252,9 +289,23 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
             for layer in layers:
                 _record_prefetch(layer._n_host, layer._host_bytes)
         elif bsz <= _MAX_SEQ_ARGS:
-            # every page on the device: the layers' device-resident records
+            # every page on the device: the layers' device-resident records,
+            # each item's new token written by the same launch where it can
+            if pending:
+                app = _fused_tokens(pending, kv_dtype, q.device)
+                if app is not None:
+                    out = _attend_layers(q, layers, lens, Hkv, kv_dtype, scale, attention_mask,
+                                         softcap, False, tokens_app=app)
+                    if out is not None:
+                        for queue in pending:
+                            queue.rows.clear()
+                            queue.keep.clear()
+                        return out
+                _flush_appends(pending)
             return _attend_layers(q, layers, lens, Hkv, kv_dtype, scale, attention_mask,
                                   softcap, False)
+    if pending:
+        _flush_appends(pending)
     # (concatenated as raw 8-byte words: numpy's structured-dtype
     # concatenate is ~15x slower)
     arr = recs[0] if bsz == 1 else np.concatenate(

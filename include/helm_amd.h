@@ -220,6 +220,28 @@ int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
                          int64_t mask_hstride, int64_t mask_qstride, int causal,
                          int kv_dtype, int q_dtype, void* stream);
 
+/* One decode step of _decode_batched (helm/runtime/kv_offload.py:145-174):
+ * each sequence's new token written into its pages (KVCacheManager.
+ * append_decode's copy_, kv_cache.py:164-165) and the attention over every
+ * page, in one kernel.  Arguments as helm_paged_attn_seqs with q_len = 1
+ * and q in the KV dtype; tokens[b] is sequence b's token:
+ * src_k / src_v its head-0 K / V (16-byte aligned), src_head_stride elements
+ * between heads, n_tok = 1 — the destination is the last used slot of the
+ * sequence's last record (the bookkeeping has counted the token in
+ * seq_tokens[b]), so the dst_* fields are not read.  The split that holds the
+ * last page writes the token before reading it.  Returns HELM_E_UNSUPPORTED,
+ * launching nothing, when the call's shape does not run on the matrix-core
+ * decode kernel (16-bit KV, D = 128) or a token source is not 16-byte
+ * aligned: write the tokens
+ * with helm_page_append and call helm_paged_attn_seqs then. */
+int helm_paged_attn_seqs_append(helm_engine* eng, const void* q, void* out, int B,
+                                int Hq, int Hkv, int D, const uint64_t* seq_pages,
+                                const int32_t* seq_npages, const int32_t* seq_tokens,
+                                int page_tokens, int aligned16, float scale, float softcap,
+                                const float* mask, int64_t mask_bstride,
+                                int64_t mask_hstride, int64_t mask_qstride, int kv_dtype,
+                                const helm_append_seg* tokens, void* stream);
+
 /* Copies `bytes` from host memory `src` to device memory `dst` in the order
  * of `stream`, through the engine's pinned staging ring (src may be reused
  * as soon as the call returns).  Keeps device-resident page records current

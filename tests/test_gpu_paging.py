@@ -1234,3 +1234,59 @@ def test_record_validation_mode_checks_the_device_copy(monkeypatch):
     with pytest.raises(RuntimeError, match="device record 0 differs"):
         perform_streaming_attention(q, mgr.iterate_layer_pages(0))
     mgr.clear()
+
+
+@pytest.mark.parametrize("Hq,Hkv,dtype", [(32, 8, torch.bfloat16), (40, 2, torch.float16),
+                                          (16, 8, torch.float32)])
+def test_decode_batched_writes_tokens_inside_the_attention_call(Hq, Hkv, dtype, monkeypatch):
+    """_decode_batched over device-resident records writes each item's new
+    token inside the attention launch (helm_paged_attn_seqs_append) where the
+    matrix-core decode kernel runs (16-bit KV, D = 128; with 20 query rows per
+    KV head two query tiles write the same token) and with the separate
+    append launch otherwise (fp32).  Against the same steps with the separate
+    launch forced (HELM_AMD_FUSED_APPEND=0): outputs and every page equal bit
+    for bit, over ragged items whose tokens fill partial pages and open new
+    ones; the last step against fp64."""
+    D, P, L, B = 128, 16, 2, 3
+    g = torch.Generator(device=DEV).manual_seed(71)
+    lens = [45, 16, 31]
+    prompt = [[(torch.randn(1, Hkv, n, D, generator=g, device=DEV).to(dtype),
+                torch.randn(1, Hkv, n, D, generator=g, device=DEV).to(dtype)) for n in lens]
+              for _ in range(L)]
+    steps = [(torch.randn(B, Hq, 1, D, generator=g, device=DEV).to(dtype),
+              torch.randn(B, Hkv, 1, D, generator=g, device=DEV).to(dtype),
+              torch.randn(B, Hkv, 1, D, generator=g, device=DEV).to(dtype)) for _ in range(5)]
+
+    def run(fused):
+        monkeypatch.setenv("HELM_AMD_FUSED_APPEND", "1" if fused else "0")
+        a = KVAllocator(L, Hkv, D, page_size=P, dtype=dtype)
+        kvcms = [KVCacheManager(a, gpu_high_watermark_bytes=10 ** 12) for _ in range(B)]
+        for lid in range(L):
+            for i, m in enumerate(kvcms):
+                m.append_prefill(lid, *prompt[lid][i])
+        outs = []
+        for q, kn, vn in steps:
+            for lid in range(L):
+                outs.append(_decode_batched(kvcms, q, kn, vn, lid, 1 / math.sqrt(D)).cpu())
+        torch.cuda.synchronize()
+        pages = [_gather(m, lid) for lid in range(L) for m in kvcms]
+        for m in kvcms:
+            m.clear()
+        return outs, pages
+
+    fused_out, fused_pages = run(True)
+    sep_out, sep_pages = run(False)
+    for x, y in zip(fused_out, sep_out):
+        assert torch.equal(x, y)
+    for (k1, v1), (k2, v2) in zip(fused_pages, sep_pages):
+        assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    # the pages hold prompt + every step's token; the last step against fp64
+    q = steps[-1][0]
+    for i in range(B):
+        K = torch.cat([prompt[L - 1][i][0].cpu()] + [s[1][i:i + 1].cpu() for s in steps], 2)
+        V = torch.cat([prompt[L - 1][i][1].cpu()] + [s[2][i:i + 1].cpu() for s in steps], 2)
+        k_pages, v_pages = fused_pages[(L - 1) * B + i]
+        assert torch.equal(k_pages, K) and torch.equal(v_pages, V)
+        ref = A.attention_fp64_batched(q[i].float().cpu(), K[0].float(), V[0].float())
+        tol = 1e-2 if dtype == torch.bfloat16 else 2e-3
+        assert (fused_out[-1][i].double() - ref).abs().max().item() <= tol
