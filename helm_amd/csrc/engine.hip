@@ -179,6 +179,34 @@ int max_pps_of(const Plan& pl) {
 constexpr int kRaggedPps = 48;
 int max_splits_of(const Plan& pl) { return pl.mfma ? kMfmaMaxSplits : kMaxSplits; }
 
+// Pages per split when the split length cap (max_pps) leaves more splits
+// than one round of `target` workgroups holds: every split is the same work,
+// so the call lasts about as long as the busiest CU's share, ceil(workgroups
+// / target) splits of pps pages.  The split count is chosen to minimise that
+// (fewer splits on a tie): a sequence of 2,049 pages on 8 KV heads takes 63
+// splits of 33 pages (two per CU) instead of 33 of 64 pages, where one CU of
+// each XCD would walk two 64-page splits while the others walk one
+// (Qwen3-8B shape, 32k + a few tokens through _decode_batched: 40.9 -> 34.0
+// us per call; the Qwen3-14B B4 x 64k 40-layer step: 140.2 -> 141-142 steps/s,
+// 138.4 -> 142-143 under the decode mask).
+int balanced_pps(double pages, double units, int target, int lo_pps, int max_pps) {
+  const double P = std::max(1.0, pages);
+  const int s_min = (int)std::ceil(P / max_pps);
+  int best_pps = max_pps;
+  double best = -1.0;
+  for (int s = s_min; s <= 4 * s_min; ++s) {
+    const int pps = (int)std::ceil(P / s);
+    if (pps < lo_pps) break;
+    const double s_eff = std::ceil(P / pps);
+    const double cost = std::ceil(units * s_eff / target) * pps;
+    if (best < 0.0 || cost < best) {
+      best = cost;
+      best_pps = pps;
+    }
+  }
+  return best_pps;
+}
+
 // work_pages: pages one (sequence, head, tile) walks on average; max_pages:
 // the longest sequence (bounds the split count).
 int make_plan(Plan& pl, int kv_dtype, int q_dtype, int B, int Hq, int Hkv,
@@ -224,14 +252,18 @@ int make_plan(Plan& pl, int kv_dtype, int q_dtype, int B, int Hq, int Hkv,
     const double splits = std::max(1.0, target / units);
     pps = (int)std::ceil(std::max(1.0, avg_pages) / splits);
     pps = std::max(pps, min_pps(pl.bpp, pl.nw));
+    const bool capped = pps > max_pps_of(pl);
     pps = std::min(pps, max_pps_of(pl));
+    const bool ragged = B > 1 && max_pages > 1.5 * avg_pages;
     // ragged batches that need several rounds of workgroups end with a long
     // tail of the longest sequences' splits; shorter splits shorten it
     // (Qwen3-14B B8, 4k-32k: 146.6 us at 64 pages per split, 123.6 at 48;
     // equal-length batches are best at 64)
-    if (pl.mfma && !pl.row_waves && B > 1 && max_pages > 1.5 * avg_pages && pps > kRaggedPps &&
+    if (pl.mfma && !pl.row_waves && ragged && pps > kRaggedPps &&
         units * std::ceil(avg_pages / pps) > 2.0 * device_cus())
       pps = kRaggedPps;
+    else if (capped && !ragged)
+      pps = balanced_pps(avg_pages, units, target, min_pps(pl.bpp, pl.nw), pps);
   }
   pps = std::min(pps, max_pps_of(pl));
   pps = std::max(pps, (max_pages + max_splits_of(pl) - 1) / max_splits_of(pl));
