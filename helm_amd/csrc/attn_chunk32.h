@@ -228,28 +228,38 @@ __global__ __launch_bounds__(NW * 64, 2) void chunk32_mfma_kernel(AttnParams p, 
     const char *kb, *vb;
   };
   const int own_blk = (wave * kLoads) >> 3;
+  // (a stage never straddles two record windows: window w starts at block
+  // 64 w bpp of the split, a multiple of the stage's SB = 4 blocks, so the
+  // window is entered at a stage's first block; blocks past the split's end
+  // have no tokens and their views are never dereferenced)
+  static_assert(kRecWindow % SB == 0, "record windows start at stage boundaries");
   auto view_stage = [&](int st, int (&ntok)[SB], int (&tok0)[SB], OwnBlock& ob) {
+    if (cur_pi - win >= kRecWindow) {   // uniform: the stage lies in the next window
+      win += kRecWindow;
+      lanes = lane_pages(src, b, pg0 + win, lane);
+    }
+    int own_pi = cur_pi, own_tok_in = 0;
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
-      if (cur_pi - win >= kRecWindow) {   // uniform: the page lies in the next window
-        win += kRecWindow;
-        lanes = lane_pages(src, b, pg0 + win, lane);
-      }
-      const PageView pv = lane_page_view(src, lanes, b, pg0 + cur_pi, cur_pi - win, hk);
+      const PageMeta pm = lane_page_meta(src, lanes, b, pg0 + cur_pi, cur_pi - win);
       const int tok_in = cur_sub * kBlockTok;
-      const int nt = st * SB + j < nblk ? sclamp(pv.used - tok_in, 0, kBlockTok) : 0;
+      const int nt = st * SB + j < nblk ? sclamp(pm.used - tok_in, 0, kBlockTok) : 0;
       ntok[j] = nt;
-      tok0[j] = pv.tok_off + tok_in;
+      tok0[j] = pm.tok_off + tok_in;
       if (j == own_blk) {
         ob.ntok = nt;
-        ob.kb = pv.k + tok_in * kRow;
-        ob.vb = pv.v + tok_in * kRow;
+        own_pi = cur_pi;
+        own_tok_in = tok_in;
       }
       if (++cur_sub == bpp) {
         cur_sub = 0;
         ++cur_pi;
       }
     }
+    // the addresses of the one block this wave loads
+    const PageView pv = lane_page_view(src, lanes, b, pg0 + own_pi, own_pi - win, hk);
+    ob.kb = pv.k + own_tok_in * kRow;
+    ob.vb = pv.v + own_tok_in * kRow;
   };
 
   // this wave's loads of a stage straight from memory into LDS (no VGPRs):

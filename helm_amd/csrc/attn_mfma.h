@@ -189,7 +189,8 @@ __device__ __forceinline__ PageView lane_page_view(const DescSrc& s, const DescL
   const uint64_t v = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(L.vhi, i) << 32) |
                      (uint32_t)__builtin_amdgcn_readlane(L.vlo, i);
   const int hs = __builtin_amdgcn_readlane(L.head_stride, i);
-  const int64_t off = (int64_t)hk * hs * s.elem_bytes;
+  // (head strides are >= 0: one 32 x 32 -> 64-bit product)
+  const uint64_t off = (uint64_t)(uint32_t)hs * (uint32_t)(hk * s.elem_bytes);
   PageView pv;
   pv.k = reinterpret_cast<const char*>(k) + off;
   pv.v = reinterpret_cast<const char*>(v) + off;
@@ -197,6 +198,28 @@ __device__ __forceinline__ PageView lane_page_view(const DescSrc& s, const DescL
   pv.tok_off = __builtin_amdgcn_readlane(L.tok_off, i);
   pv.head_stride_b = 0;
   return pv;
+}
+
+// Used tokens and token offset of page i of the split (uniform), without its
+// addresses: what a walk needs for the blocks it does not load itself.
+struct PageMeta {
+  int used;
+  int tok_off;
+};
+__device__ __forceinline__ PageMeta lane_page_meta(const PoolSrc& s, const PoolLanes&, int b,
+                                                   int pg, int) {
+  const int T = sload(s.seq_lens + b);
+  PageMeta pm;
+  pm.tok_off = pg * s.page_size;
+  pm.used = min(s.page_size, T - pm.tok_off);
+  return pm;
+}
+__device__ __forceinline__ PageMeta lane_page_meta(const DescSrc&, const DescLanes& L, int, int,
+                                                   int i) {
+  PageMeta pm;
+  pm.used = __builtin_amdgcn_readlane(L.used, i);
+  pm.tok_off = __builtin_amdgcn_readlane(L.tok_off, i);
+  return pm;
 }
 
 // One 16-token block of the online-softmax recurrence on the matrix cores:
