@@ -360,11 +360,15 @@ __global__ __launch_bounds__(NW * 64, 2) void chunk32_mfma_kernel(AttnParams p, 
         mf_f32x16 sc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] = 0.f;
+        // every K operand read issued before the first MFMA (one LDS wait,
+        // then the eight MFMAs back to back)
+        mf_u32x4 ka[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const mf_u32x4 ka = cur[0][bp + kblk][ktok * 16 + ((2 * i + hh) ^ swz(ktok))];
-          sc = M32::mma(ka, qop[i], sc);
-        }
+        for (int i = 0; i < 8; ++i)
+          ka[i] = cur[0][bp + kblk][ktok * 16 + ((2 * i + hh) ^ swz(ktok))];
+        __builtin_amdgcn_sched_barrier(0);   // (keeps the reads ahead of the MFMAs)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sc = M32::mma(ka[i], qop[i], sc);
         return sc;
       };
       // steps that add exactly nothing for any row of the wave are skipped
