@@ -361,12 +361,15 @@ __global__ __launch_bounds__(NW * 64, 2) void chunk32_mfma_kernel(AttnParams p, 
 #pragma unroll
         for (int r = 0; r < 16; ++r) sc[r] = 0.f;
         // every K operand read issued before the first MFMA (one LDS wait,
-        // then the eight MFMAs back to back)
+        // then the eight MFMAs back to back), registers allowing: with a mask
+        // operand its prefetched values take them, and the compiler's order
+        // stays
         mf_u32x4 ka[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
           ka[i] = cur[0][bp + kblk][ktok * 16 + ((2 * i + hh) ^ swz(ktok))];
-        __builtin_amdgcn_sched_barrier(0);   // (keeps the reads ahead of the MFMAs)
+        if constexpr (!kMask)
+          __builtin_amdgcn_sched_barrier(0);   // (keeps the reads ahead of the MFMAs)
 #pragma unroll
         for (int i = 0; i < 8; ++i) sc = M32::mma(ka[i], qop[i], sc);
         return sc;
