@@ -984,6 +984,81 @@ __global__ __launch_bounds__(kThreads) void merge_splits_d128_kernel(AttnParams 
   }
 }
 
+// The merge for calls with many query rows and few splits (query chunks):
+// thread (r, c) = (tid / 32, tid % 32) of workgroup (tile, y) owns row
+// 8 y + r of the tile and its float4 column chunk c, and walks the splits
+// itself (no reduction across threads), eight partials in flight at a time
+// (the first eight issued before the split count arrives, bounded by the
+// workspace's split capacity).  Same arithmetic as merge_splits_d128_kernel
+// per split, in split order.
+template <typename TQ>
+__global__ __launch_bounds__(kThreads) void merge_rows_d128_kernel(AttnParams p) {
+  constexpr int QB = ElemBytes<TQ>::v;
+  const int tile = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int RS = p.rows_per_tile;
+  const int row = blockIdx.y * (kThreads / 32) + (tid >> 5);
+  const int c = tid & 31;
+  const int qt = tile % p.n_qtiles;
+  const int hk = (tile / p.n_qtiles) % p.Hkv;
+  const int b = tile / (p.n_qtiles * p.Hkv);
+  const int rr = qt * RS + row;
+  if (row >= RS || rr >= p.G * p.S) return;
+  const int total = p.counts[tile];
+  const int64_t base_part = (int64_t)tile * p.max_splits * RS + row;
+  float M = -INFINITY, L = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int bound = p.max_splits;
+  for (int s0 = 0; s0 < bound; s0 += kMergeBatch) {
+    if (s0 > 0 && s0 >= total) break;
+    float2 ml[kMergeBatch];
+    float4 v[kMergeBatch];
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const int sp = s0 + k;
+      if (sp < bound) {
+        const int64_t pi = base_part + (int64_t)sp * RS;
+        ml[k] = *reinterpret_cast<const float2*>(p.ws_ml + pi * 2);
+        v[k] = *reinterpret_cast<const float4*>(p.ws_o + pi * 128 + c * 4);
+      } else {
+        ml[k] = make_float2(-INFINITY, 0.f);
+        v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    float mb = M;
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      if (s0 + k >= total) {
+        ml[k] = make_float2(-INFINITY, 0.f);
+        v[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      mb = fmaxf(mb, ml[k].x);
+    }
+    const float base = (mb == -INFINITY) ? 0.f : mb;
+    const float a0 = fexp(M - base);
+    L *= a0;
+    acc.x *= a0; acc.y *= a0; acc.z *= a0; acc.w *= a0;
+#pragma unroll
+    for (int k = 0; k < kMergeBatch; ++k) {
+      const float wgt = fexp(ml[k].x - base);
+      L = fmaf(wgt, ml[k].y, L);
+      acc.x = fmaf(wgt, v[k].x, acc.x);
+      acc.y = fmaf(wgt, v[k].y, acc.y);
+      acc.z = fmaf(wgt, v[k].z, acc.z);
+      acc.w = fmaf(wgt, v[k].w, acc.w);
+    }
+    M = mb;
+  }
+  const float inv = 1.f / fmaxf(L, 1e-12f);
+  const RowCoord rc = row_coord(rr, p.G);
+  const int h = hk * p.G + rc.g;
+  char* orow = reinterpret_cast<char*>(p.out) + ((int64_t)(b * p.Hq + h) * p.S + rc.s) * 128 * QB;
+  store_elem<TQ>(orow + (4 * c + 0) * QB, acc.x * inv);
+  store_elem<TQ>(orow + (4 * c + 1) * QB, acc.y * inv);
+  store_elem<TQ>(orow + (4 * c + 2) * QB, acc.z * inv);
+  store_elem<TQ>(orow + (4 * c + 3) * QB, acc.w * inv);
+}
+
 template <typename TKV, typename TQ, int EPL, int GM, bool DOT2, class Src>
 __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
                                                                Src src) {

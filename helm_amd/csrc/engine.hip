@@ -353,6 +353,24 @@ hipError_t launch_merge(const LaunchSpec& s, int B, int Hkv, hipStream_t st) {
   const int chunks = (s.p.D % 4 == 0) ? s.p.D / 4 : s.p.D;
   const int groups = std::max(1, std::min(env_int("HELM_AMD_MERGE_GROUPS", 1), chunks));
   const dim3 grid(B * Hkv * s.p.n_qtiles, s.p.rows_per_tile, groups);
+  // few splits per tile (query chunks): one thread per (row, column chunk)
+  // walking the splits, eight rows per workgroup
+  if (s.p.D == 128 && groups == 1 && s.p.max_splits <= kMergeBatch &&
+      env_int("HELM_AMD_MERGE_ROWS", 1)) {
+    const dim3 rgrid(B * Hkv * s.p.n_qtiles, (s.p.rows_per_tile + 7) / 8);
+    switch (s.q_dtype) {
+      case HELM_F16:
+        hipLaunchKernelGGL(merge_rows_d128_kernel<f16_t>, rgrid, dim3(kThreads), 0, st, s.p);
+        return hipGetLastError();
+      case HELM_BF16:
+        hipLaunchKernelGGL(merge_rows_d128_kernel<bf16_t>, rgrid, dim3(kThreads), 0, st, s.p);
+        return hipGetLastError();
+      case HELM_F32:
+        hipLaunchKernelGGL(merge_rows_d128_kernel<float>, rgrid, dim3(kThreads), 0, st, s.p);
+        return hipGetLastError();
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (s.p.D == 128 && groups == 1) {
     switch (s.q_dtype) {
       case HELM_F16:
