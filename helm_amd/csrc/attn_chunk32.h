@@ -406,13 +406,13 @@ __global__ __launch_bounds__(NW * 64, 2) void chunk32_mfma_kernel(AttnParams p, 
         // the causal limit when a block's last token is past the wave's first
         // query position, the valid-token limit when a block is partial
         if constexpr (kCausal) {
-          if (max(tok0_c[bp], tok0_c[bp + 1]) + kBlockTok - 1 > s_first) {
+          if (__builtin_expect(max(tok0_c[bp], tok0_c[bp + 1]) + kBlockTok - 1 > s_first, 0)) {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
               if (tok0_c[bp + (r >> 3)] + 8 * hh + (r & 7) > s_vis) x[r] = -INFINITY;
           }
         }
-        if (nt0 < kBlockTok || nt1 < kBlockTok) {
+        if (__builtin_expect(nt0 < kBlockTok || nt1 < kBlockTok, 0)) {
 #pragma unroll
           for (int r = 0; r < 16; ++r)
             if (8 * hh + (r & 7) >= ((r >> 3) ? nt1 : nt0)) x[r] = -INFINITY;
@@ -420,7 +420,7 @@ __global__ __launch_bounds__(NW * 64, 2) void chunk32_mfma_kernel(AttnParams p, 
         float bm = x[0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) bm = fmaxf(bm, x[r]);
-        if (__builtin_amdgcn_ballot_w64(bm > m + kMfmaSlack)) {
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(bm > m + kMfmaSlack) != 0, 0)) {
           // refresh the row max (both halves of the row agree)
           const float mn = fmaxf(m, fmaxf(bm, __shfl_xor(bm, 32, 64)));
           const float a = sexp(m - ((mn == -INFINITY) ? 0.f : mn));
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(NW * 64, 2) void chunk32_mfma_kernel(AttnParams p, 
             else if (st + 1 < nstage)
               load_step_mask(vnt[K ^ 1], vt0[K ^ 1], 0);
           }
-          if (idle_step(bp)) continue;
+          if (__builtin_expect(idle_step(bp), 0)) continue;
           // masked, a step whose every mask value is <= -1e30 while every
           // row's max is already above -1e20 adds exactly nothing (each
           // weight underflows to 0 and the max stays)
