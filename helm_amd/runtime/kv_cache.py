@@ -1047,11 +1047,22 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
     device = query.device
     eng = _engine.get_engine(device)
     stream = _engine.stream_ptr(device)
-    ptrs, npages, tokens, addrs = _seq_args(len(layers))
+    B = len(layers)
+    if tokens_app is not None and (B > _MAX_SEQS or causal or query.size(2) != 1
+                                   or query.size(3) != 128 or query.dtype != kv_dtype):
+        return None
+    ptrs, npages, tokens, addrs = _seq_args(B)
+    page_tokens, aligned, t_max = 0, True, 0
     for b, layer in enumerate(layers):
         ptrs[b] = layer._device_records(device, eng, stream).data_ptr()
         npages[b] = len(layer.pages)
-        tokens[b] = lens[b]
+        n = lens[b]
+        tokens[b] = n
+        if n > t_max:
+            t_max = n
+        if layer._page_tokens > page_tokens:
+            page_tokens = layer._page_tokens
+        aligned = aligned and layer._aligned16
     if check_records_enabled():
         for layer in layers:
             layer.check_records(device)
@@ -1059,25 +1070,18 @@ def _attend_layers(query: torch.Tensor, layers: Sequence[LayerKVCache], lens: Se
         # causal c: keys from S + c - 1 on are masked for every row; the pages
         # holding only such keys are left out (records are in token order)
         limit = query.size(2) + int(causal) - 1
+        t_max = min(t_max, limit)
         for b, layer in enumerate(layers):
             if tokens[b] > limit:
                 tokens[b] = limit
                 npages[b] = int(np.searchsorted(layer._rec["tok_off"][:npages[b]], limit,
                                                 "left"))
-    page_tokens = max(layer._page_tokens for layer in layers)
-    aligned = all(layer._aligned16 for layer in layers)
-    B = len(layers)
     if tokens_app is not None:
-        if (B > _MAX_SEQS or causal or query.size(2) != 1 or query.size(3) != 128
-                or query.dtype != kv_dtype):
-            return None
-        t_max = int(tokens[0]) if B == 1 else int(tokens.max())
-        return _launch_seqs(query, addrs, t_max, page_tokens, aligned, Hkv, kv_dtype, scale,
-                            attention_mask, softcap, causal, tokens_app=tokens_app)
+        return _launch_seqs(query, addrs, int(t_max), page_tokens, aligned, Hkv, kv_dtype,
+                            scale, attention_mask, softcap, causal, tokens_app=tokens_app)
     if B <= _MAX_SEQS:
-        t_max = int(tokens[0]) if B == 1 else int(tokens.max())
-        return _launch_seqs(query, addrs, t_max, page_tokens, aligned, Hkv, kv_dtype, scale,
-                            attention_mask, softcap, causal)
+        return _launch_seqs(query, addrs, int(t_max), page_tokens, aligned, Hkv, kv_dtype,
+                            scale, attention_mask, softcap, causal)
     return _attend_device_records(query, ptrs, npages, tokens, page_tokens, aligned, Hkv,
                                   kv_dtype, scale, attention_mask, softcap, causal)
 

@@ -240,15 +240,25 @@ def _fused_tokens(pending, kv_dtype, device) -> Optional[int]:
     if os.environ.get("HELM_AMD_FUSED_APPEND") == "0":
         return None
     n = len(pending)
-    rows = getattr(_tls, "token_rows", None)
-    if rows is None or len(rows) < n:
-        rows = _tls.token_rows = np.zeros(max(n, _MAX_SEQ_ARGS), dtype=_native.APPEND_DTYPE)
+    # this thread's row array (kept between calls) as 8-byte words: the call
+    # reads src_k, src_v, src_head_stride and n_tok of each 64-byte row,
+    # words 2, 3, 4 and the low half of 7
+    kept = getattr(_tls, "token_rows", None)
+    if kept is None or len(kept[0]) < n:
+        rows = np.zeros(max(n, _MAX_SEQ_ARGS), dtype=_native.APPEND_DTYPE)
+        kept = _tls.token_rows = (rows, rows.view(np.uint64), rows.ctypes.data)
+    rows, words, addr = kept
     for b, queue in enumerate(pending):
         if (len(queue.rows) != 1 or queue.dtype != kv_dtype or queue.device != device
                 or queue.rows[0][8] != 1):
             return None
-        rows[b] = queue.rows[0]
-    return rows.ctypes.data
+        row = queue.rows[0]
+        w = 8 * b
+        words[w + 2] = row[2]
+        words[w + 3] = row[3]
+        words[w + 4] = row[4]
+        words[w + 7] = 1
+    return addr
 
 
 def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: float,
@@ -265,23 +275,29 @@ def _decode_from_records(kvcms, q, layer_idx: int, Hkv: int, D: int, scale: floa
     attention call writes the tokens itself, else they are issued first.
     """
     cpu = q.device.type != "cuda"
-    if (not cpu and not _async_kv_prefetch_enabled()) or not all(
-            isinstance(kvcm, KVCacheManager) for kvcm in kvcms):
+    if not cpu and not _async_kv_prefetch_enabled():
         return None
-    layers = [kvcm.layers.get(layer_idx) for kvcm in kvcms]
-    recs = []
-    for layer in layers:
-        r = layer.records() if layer is not None else None
-        if (r is None or len(r) == 0 or layer._n_other or layer._rec_sig is None
-                or layer._rec_sig[1:] != (Hkv, D)):
+    # one pass over the items: each a KVCacheManager whose layer has usable
+    # records of this call's shape and one KV dtype
+    layers, recs, lens = [], [], []
+    kv_dtype, host = None, False
+    for kvcm in kvcms:
+        if not isinstance(kvcm, KVCacheManager):
             return None
+        layer = kvcm.layers.get(layer_idx)
+        if layer is None:
+            return None
+        r = layer.records()
+        sig = layer._rec_sig
+        if r is None or len(r) == 0 or layer._n_other or sig is None or sig[1] != Hkv \
+                or sig[2] != D or (kv_dtype is not None and sig[0] != kv_dtype):
+            return None
+        kv_dtype = sig[0]
+        layers.append(layer)
         recs.append(r)
-    kv_dtype = layers[0]._rec_sig[0]
-    if any(layer._rec_sig[0] != kv_dtype for layer in layers):
-        return None
-    lens = [layer.total_tokens_recorded() for layer in layers]
+        lens.append(layer.total_tokens_recorded())
+        host = host or layer._n_host > 0
     bsz = len(layers)
-    host = any(layer._n_host for layer in layers)
     if not cpu:
         # HELM streams the items that hold host pages one by one and counts
         # each as a prefetch (kv_offload.py:176-186, kv_cache.py:441-447)
