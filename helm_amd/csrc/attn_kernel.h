@@ -367,6 +367,11 @@ struct DescSrc {
   const char* app_k[kSeqArgs];
   const char* app_v[kSeqArgs];
   int64_t app_hs[kSeqArgs];
+  // compact numbering (by_value, decode kernel): blockIdx.x runs over every
+  // sequence's splits in turn, sequence b's first at seq_split0[b] (b < n_seq,
+  // ascending); no workgroup lacks a split
+  int compact, n_seq;
+  int seq_split0[kSeqArgs];
 
   __device__ __forceinline__ const helm_page* base(int b) const {
     return by_value ? seq_pages[b] : pages + sload(seq_off + b);

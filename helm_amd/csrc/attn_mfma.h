@@ -345,12 +345,22 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   const int q4 = lane >> 4;
   const int n = lane & 15;
 
-  const int split_local = blockIdx.x;
+  int split_local = blockIdx.x, b = blockIdx.z;
+  if constexpr (std::is_same<Src, DescSrc>::value) {
+    if (src.compact) {
+      // the last sequence whose first split is at or before blockIdx.x
+      int bb = 0;
+#pragma unroll
+      for (int j = 1; j < kSeqArgs; ++j)
+        if (j < src.n_seq && (int)blockIdx.x >= src.seq_split0[j]) bb = j;
+      b = bb;
+      split_local = blockIdx.x - src.seq_split0[bb];
+    }
+  }
   const int hk = blockIdx.y % p.Hkv;
   // the waves share one 16-row tile and split its blocks (query chunks with
   // more tiles run in chunk_mfma_kernel)
   const int qt = blockIdx.y / p.Hkv;
-  const int b = blockIdx.z;
   const int tile = (b * p.Hkv + hk) * p.n_qtiles + qt;
   const int S = p.S;
   const int G = p.G;

@@ -179,6 +179,29 @@ int max_pps_of(const Plan& pl) {
 constexpr int kRaggedPps = 48;
 int max_splits_of(const Plan& pl) { return pl.mfma ? kMfmaMaxSplits : kMaxSplits; }
 
+// Pages per split for a batch whose page counts are known (helm_paged_attn_seqs
+// with the compact grid): the split length in [lo_pps, max_pps] that
+// minimises the busiest CU's share, ceil(units x sum_b ceil(pages_b / pps) /
+// target) x (pps + kSplitCostPages), the longer split on a tie; a split's own
+// cost (records, first loads, partial and merge) counts as kSplitCostPages
+// pages.
+constexpr int kSplitCostPages = 8;
+int batch_pps(const int32_t* pages, int B, int units, int target, int lo_pps, int max_pps) {
+  int best_pps = max_pps;
+  int64_t best = -1;
+  for (int pps = max_pps; pps >= std::max(1, lo_pps); --pps) {
+    int64_t splits = 0;
+    for (int b = 0; b < B; ++b) splits += (pages[b] + pps - 1) / pps;
+    const int64_t cost =
+        ((int64_t)units * splits + target - 1) / target * (pps + kSplitCostPages);
+    if (best < 0 || cost < best) {
+      best = cost;
+      best_pps = pps;
+    }
+  }
+  return best_pps;
+}
+
 // Pages per split when the split length cap (max_pps) leaves more splits
 // than one round of `target` workgroups holds: every split is the same work,
 // so the call lasts about as long as the busiest CU's share, ceil(workgroups
@@ -1302,6 +1325,16 @@ static int paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B, in
                                             " is not 16-byte aligned");
     }
   }
+  // a batch on the decode kernel whose sequences all hold pages: the grid
+  // numbers exactly their splits (no workgroups of a short sequence that find
+  // no split), with the split length chosen from every sequence's page count
+  bool compact = pl.mfma && !pl.row_waves && B > 1 && env_int("HELM_AMD_COMPACT", 1);
+  for (int b = 0; b < B && compact; ++b) compact = seq_npages[b] > 0;
+  if (compact && env_int("HELM_AMD_PPS", 0) <= 0) {
+    const int cand = batch_pps(seq_npages, B, Hkv * pl.qblocks(), device_cus(),
+                               min_pps(pl.bpp, pl.nw), max_pps_of(pl));
+    if ((max_pages + cand - 1) / cand <= max_splits_of(pl)) pl.pps = cand;
+  }
   pl.max_splits = std::max(1, (max_pages + pl.pps - 1) / pl.pps);
   pl.fused = fused_merge(pl.max_splits);
   size_plan(pl, B, Hkv, D);
@@ -1316,10 +1349,17 @@ static int paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B, in
   s.mode = 1;
   s.desc.elem_bytes = eb;
   s.desc.by_value = 1;
+  int all_splits = 0;
   for (int b = 0; b < B; ++b) {
     s.desc.seq_pages[b] = reinterpret_cast<const helm_page*>(seq_pages[b]);
     s.desc.seq_n[b] = seq_npages[b];
     s.desc.seq_tokens[b] = seq_tokens[b];
+    s.desc.seq_split0[b] = all_splits;
+    all_splits += (seq_npages[b] + pl.pps - 1) / pl.pps;
+  }
+  if (compact) {
+    s.desc.compact = 1;
+    s.desc.n_seq = B;
   }
   if (app) {
     s.desc.app_n = B;
@@ -1338,7 +1378,8 @@ static int paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B, in
   s.nw = pl.nw;
   s.feat = (mask ? kFeatMask : 0) | (softcap > 0.f ? kFeatCap : 0) |
            (causal ? kFeatCausal : 0);
-  s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.qblocks(), B);
+  s.grid = compact ? dim3(all_splits, Hkv * pl.qblocks(), 1)
+                  : dim3(std::max(1, pl.max_splits), Hkv * pl.qblocks(), B);
   hipError_t e = dispatch(s, st);
   if (e != hipSuccess) return hip_fail(e, "paged_attn_seqs launch");
   e = launch_merge(s, B, Hkv, st);
