@@ -509,6 +509,9 @@ struct helm_engine {
   size_t chunk_bytes = 0;
   int ring_slots = 0;
   int next_slot = 0;
+  // per ring slot: its copies are complete (recorded on `copy`) / the launch
+  // that reads it is complete (recorded on the caller's stream)
+  std::vector<hipEvent_t> slot_ready, slot_free;
   // descriptor uploads (pinned host -> device), a ring so the host can run ahead
   static constexpr int kUp = 8;
   char* up_host[kUp] = {};
@@ -610,6 +613,21 @@ int host_read_mode() {
 }
 
 bool host_read_in_place() { return host_read_mode() != 0; }
+
+// Where a call's staging copies go.  On the engine's side stream they run
+// while the device pages' launch runs on the caller's stream, but the two
+// joins (side stream after the caller's earlier work, chunk launch after its
+// copies) cost tens of microseconds per call here, so the side stream pays
+// only when that launch is long: Llama-2-13B 128k with 75% in host (671 MB
+// resident) 36.96 -> 36.66 ms per call, Qwen3-8B 32k with 50% in host (67 MB
+// resident) 1.271 -> 1.286 ms.  HELM_AMD_STAGE_STREAM=side|one forces either.
+constexpr size_t kSideStreamMinResident = (size_t)256 << 20;
+bool stage_on_side_stream(size_t resident_bytes) {
+  const char* e = std::getenv("HELM_AMD_STAGE_STREAM");
+  if (e && std::strcmp(e, "one") == 0) return false;
+  if (e && std::strcmp(e, "side") == 0) return true;
+  return resident_bytes >= kSideStreamMinResident;
+}
 
 // The staging copies reach the link's rate only in large runs: hipMemcpyAsync
 // costs ~9 us per call here, so host pages that coalesce (adjacent in host
@@ -845,6 +863,12 @@ int helm_engine_create(int device, size_t chunk_bytes, int ring_slots,
       "hipEventCreate");
   chk(hipEventCreateWithFlags(&e->ev_b, hipEventDisableTiming),
       "hipEventCreate");
+  e->slot_ready.assign(e->ring_slots, nullptr);
+  e->slot_free.assign(e->ring_slots, nullptr);
+  for (int i = 0; i < e->ring_slots; ++i) {
+    chk(hipEventCreateWithFlags(&e->slot_ready[i], hipEventDisableTiming), "hipEventCreate");
+    chk(hipEventCreateWithFlags(&e->slot_free[i], hipEventDisableTiming), "hipEventCreate");
+  }
   if (rc != HELM_OK) {
     helm_engine_destroy(e);
     return rc;
@@ -867,6 +891,10 @@ int helm_engine_destroy(helm_engine* e) {
   }
   if (e->ev_a) (void)hipEventDestroy(e->ev_a);
   if (e->ev_b) (void)hipEventDestroy(e->ev_b);
+  for (hipEvent_t ev : e->slot_ready)
+    if (ev) (void)hipEventDestroy(ev);
+  for (hipEvent_t ev : e->slot_free)
+    if (ev) (void)hipEventDestroy(ev);
   if (e->copy) (void)hipStreamDestroy(e->copy);
   delete e;
   return HELM_OK;
@@ -1245,13 +1273,41 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   }
 
   // ---- mixed residency (B == 1) ---------------------------------------------
-  // Every launch and copy of the call is queued on `st`, in order: the device
-  // pages' launch, then per staged chunk its hipMemcpyAsync and the launch
-  // that reads it, then the split merge.  Stream order alone covers the
-  // copy -> kernel dependency and the reuse of a ring slot.  (Splitting the
-  // device pages onto a second stream, joined by event waits, measured
-  // slower here: every cross-stream event wait stalls the host thread for
-  // milliseconds on this runtime, starving the queue.)
+  // Staged chunks are copied on the engine's side stream while the caller's
+  // stream runs the device pages' launch and then, chunk by chunk, the launch
+  // that reads each one: chunk c's launch waits for chunk c's copies only, so
+  // the host link stays busy while the kernels run.  The side stream first
+  // waits for everything queued on the caller's stream before this call (the
+  // evictions that wrote the host pages, and the earlier calls' readers of
+  // the ring), and a slot's next copy waits for the launch that read it.
+  // Events carry no timestamps.  Without the side stream (short device-page
+  // launch, or HELM_AMD_STAGE_STREAM=one) every copy is queued on the
+  // caller's stream in launch order.
+  size_t resident_bytes = 0;
+  for (const Launch& L : launches)
+    if (L.chunk < 0)
+      for (int i = L.lo; i < L.hi; ++i) resident_bytes += 2 * page_extent(desc[i], Hkv, D, eb);
+  const bool side = stage_on_side_stream(resident_bytes);
+  const int n_chunks = (int)chunk_runs.size();
+  auto issue_copies = [&](int c) -> int {
+    const int slot = chunk_slot[c];
+    char* dst = eng->ring + (size_t)slot * eng->chunk_bytes;
+    hipStream_t cs = side ? eng->copy : st;
+    for (const Run& r : chunk_runs[c])
+      HELM_HIP(hipMemcpyAsync(dst + r.dst_off, reinterpret_cast<const void*>(r.src), r.bytes,
+                              hipMemcpyHostToDevice, cs));
+    if (side) HELM_HIP(hipEventRecord(eng->slot_ready[slot], eng->copy));
+    return HELM_OK;
+  };
+  int issued = 0;
+  if (side) {
+    HELM_HIP(hipEventRecord(eng->ev_a, st));
+    HELM_HIP(hipStreamWaitEvent(eng->copy, eng->ev_a, 0));
+    for (; issued < n_chunks && issued < eng->ring_slots; ++issued) {
+      rc = issue_copies(issued);
+      if (rc != HELM_OK) return rc;
+    }
+  }
   s.p.total_splits = total_splits;
   for (size_t li = 0; li < launches.size(); ++li) {
     const Launch& L = launches[li];
@@ -1260,16 +1316,24 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
     s.p.split_base = split_base[li];
     const int nsp = (L.hi - L.lo + pl.pps - 1) / pl.pps;
     s.grid = dim3(std::max(1, nsp), Hkv * pl.qblocks(), 1);
+    const int slot = L.chunk >= 0 ? chunk_slot[L.chunk] : -1;
     if (L.chunk >= 0) {
-      const int slot = chunk_slot[L.chunk];
-      char* dst = eng->ring + (size_t)slot * eng->chunk_bytes;
-      for (const Run& r : chunk_runs[L.chunk])
-        HELM_HIP(hipMemcpyAsync(dst + r.dst_off,
-                                reinterpret_cast<const void*>(r.src), r.bytes,
-                                hipMemcpyHostToDevice, st));
+      if (side) {
+        HELM_HIP(hipStreamWaitEvent(st, eng->slot_ready[slot], 0));
+      } else {
+        rc = issue_copies(L.chunk);
+        if (rc != HELM_OK) return rc;
+      }
     }
     hipError_t e = dispatch(s, st);
     if (e != hipSuccess) return hip_fail(e, "stream_attn chunk launch");
+    if (side && L.chunk >= 0 && issued < n_chunks) {
+      // the next chunk for this slot (chunks take the slots in turn)
+      HELM_HIP(hipEventRecord(eng->slot_free[slot], st));
+      HELM_HIP(hipStreamWaitEvent(eng->copy, eng->slot_free[slot], 0));
+      rc = issue_copies(issued++);
+      if (rc != HELM_OK) return rc;
+    }
   }
   hipError_t e = launch_merge(s, 1, Hkv, st);
   if (e != hipSuccess) return hip_fail(e, "merge launch");
