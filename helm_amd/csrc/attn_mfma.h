@@ -43,10 +43,14 @@ constexpr int kMfmaRows = 16;     // query rows per tile (MFMA M dimension)
 constexpr int kMfmaMaxPps = 64;   // pages per split: page records live one per lane
 constexpr int kMfmaMaxSplits = 4096;
 constexpr float kMfmaSlack = 8.f;
+// Register buffers of the block pipeline: with two, one block's loads are in
+// flight while the wave computes the other (8 KiB per wave, 32 KiB per CU).
+// Measured on the Qwen3-8B 32k call: 2 buffers 26.4-26.5 us, 3 buffers
+// 26.7-27.0, 4 buffers 27.2-27.4 per call.
 #ifndef HELM_MFMA_NBUF
-#define HELM_MFMA_NBUF 3
+#define HELM_MFMA_NBUF 2
 #endif
-constexpr int kMfmaBufs = HELM_MFMA_NBUF;  // register buffers of the block pipeline
+constexpr int kMfmaBufs = HELM_MFMA_NBUF;
 
 enum MfmaFeat { kFeatMask = 1, kFeatCap = 2, kFeatCausal = 4 };
 
