@@ -107,8 +107,11 @@ int mfma_waves() { return env_int("HELM_AMD_WAVES", 4) == 8 ? 8 : 4; }
 // many workgroups; merging in-kernel (the last split of a tile to arrive
 // reads every partial) saves that launch but is bound by one CU's load
 // latency, so it is used only for tiles of at most kFusedMaxSplits splits.
-// HELM_AMD_MERGE = fused | kernel forces one.
-constexpr int kFusedMaxSplits = 8;
+// Measured per call (bf16, B = 1, D = 128, merge kernel vs in-kernel merge):
+// Qwen3-8B shape 1k 8.6 vs 7.9 us, 2k (16 splits) 9.7 vs 8.7, Qwen3-0.6B 2k
+// 9.7 vs 8.7; at 32 splits of 8-32 pages (4k-16k) the kernel wins, 10.5 vs
+// 11.3, 12.7 vs 13.4, 17.4 vs 17.8.  HELM_AMD_MERGE = fused | kernel forces one.
+constexpr int kFusedMaxSplits = 16;
 int fused_merge(int max_splits) {
   const char* v = std::getenv("HELM_AMD_MERGE");
   if (v && !std::strcmp(v, "kernel")) return 0;
