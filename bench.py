@@ -5,7 +5,12 @@ decode attention — batch 1, 32 query / 8 KV heads, head_dim 128, bf16 KV,
 32,768-token context in 2,048 pages of 16 tokens under a seeded random page
 table, q/K/V ~ N(0,1), scale 1/sqrt(128), all pages resident.  A step is one
 attention call over the whole context.  Eight independent 128 MiB pools are
-rotated so the 256 MB Infinity Cache cannot serve the KV.
+rotated so the 256 MB Infinity Cache cannot serve the KV.  `value` is the
+algorithmic bytes of one call over its time (decode kernel + split merge,
+HIP events around the calls); `roofline` is the dominant kernel's: the same
+bytes over the decode kernel's own duration, from HIP events recorded around
+its launch in a second pass of the same calls (helm_profile_split_kernels),
+with the whole-call figures beside it under `roofline.per_call`.
 
 Also measured (extra keys of the one JSON line):
 * the same workload with the oldest 50% of pages in pinned host RAM (host
@@ -92,8 +97,30 @@ def parse():
     return ap.parse_args()
 
 
+def split_kernel_us(torch, step, steps):
+    """HIP-event durations (us) of the attention (split) kernel of `steps`
+    calls of `step`, the split merge after it excluded: events recorded on
+    the call's stream just before and after that launch
+    (helm_profile_split_kernels).  Mean and median."""
+    from helm_amd import _native
+    lib = _native.load()
+    _native.call("helm_profile_split_kernels", steps)
+    try:
+        for i in range(steps):
+            step(i)
+        torch.cuda.synchronize()
+        buf = np.zeros(steps, dtype=np.float32)
+        n = lib.helm_profile_split_read(_native.ptr(buf), steps)
+        if n != steps:
+            raise RuntimeError(f"split-kernel timing read {n} of {steps} calls: "
+                               f"{_native.load().helm_last_error_string()}")
+    finally:
+        _native.call("helm_profile_split_kernels", 0)
+    return float(buf.mean()), float(np.median(buf))
+
+
 def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=None, steps=None,
-                 masked=False):
+                 masked=False, kernel_timing=False):
     """Pool-layout decode attention of one workload, all pages resident.
     Pools are rotated so that at least 1 GiB of KV passes between two reads
     of the same pool (the 256 MB Infinity Cache cannot serve it).  masked:
@@ -137,7 +164,10 @@ def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=Non
     wall = time.perf_counter() - t0
     ms_events = e0.elapsed_time(e1)
     per_call_s = ms_events / 1e3 / steps
+    # a second pass of the same calls, the attention kernel timed alone
+    kern = split_kernel_us(torch, step, steps) if kernel_timing else (None, None)
     return {
+        "split_kernel_us_mean": kern[0], "split_kernel_us_median": kern[1],
         "w": w, "case": case, "alg_bytes": alg, "kv_bytes": W.kv_bytes(w, lens),
         "per_call_s": per_call_s, "wall_ms_per_step": wall * 1e3 / steps,
         "host_issue_us_per_call": (t_issued - t0) * 1e6 / steps,
@@ -200,30 +230,44 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
 
     steps = steps or args.offload_steps
 
-    def timed():
-        for _ in range(3):
-            call()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(steps):
-            call()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / 1e3 / steps
+    def timed(**env):
+        """Seconds per call under `env` (engine switches, read per call): the
+        best of three timed runs, so that a rare host stall of a few
+        milliseconds in one run does not stand for the steady state."""
+        saved = {k: os.environ.pop(k, None)
+                 for k in ("HELM_AMD_HOST_READ", "HELM_AMD_STAGE_STREAM")}
+        os.environ.update(env)
+        try:
+            for _ in range(3):
+                call()
+            torch.cuda.synchronize()
+            best = None
+            for _ in range(3):
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(steps):
+                    call()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                t = e0.elapsed_time(e1) / 1e3 / steps
+                best = t if best is None else min(best, t)
+            return best
+        finally:
+            for k in env:
+                os.environ.pop(k, None)
+            os.environ.update({k: v for k, v in saved.items() if v is not None})
 
-    # host pages staged through the device ring by hipMemcpyAsync, read in
-    # place by the kernel over the host link, and the engine's default (it
-    # picks per call: pages in long address runs are staged)
-    prev = os.environ.pop("HELM_AMD_HOST_READ", None)
-    os.environ["HELM_AMD_HOST_READ"] = "copy"
-    per_staged = timed()
-    os.environ["HELM_AMD_HOST_READ"] = "direct"
-    per_direct = timed()
-    del os.environ["HELM_AMD_HOST_READ"]
+    # host pages staged through the device ring by hipMemcpyAsync (copies on
+    # the engine's side stream overlapped with the device pages' launch, or
+    # on the caller's stream after it), read in place by the kernel over the
+    # host link, and the engine's default (per call: pages in long address
+    # runs are staged; the side stream when the device pages are >= 256 MiB)
+    per_staged = timed(HELM_AMD_HOST_READ="copy")
+    per_side = timed(HELM_AMD_HOST_READ="copy", HELM_AMD_STAGE_STREAM="side")
+    per_one = timed(HELM_AMD_HOST_READ="copy", HELM_AMD_STAGE_STREAM="one")
+    per_direct = timed(HELM_AMD_HOST_READ="direct")
     per = timed()
-    if prev is not None:
-        os.environ["HELM_AMD_HOST_READ"] = prev
     host_bytes = n_host * slot_b
     peak = h2d_peak(torch)
     # parity spot check of this exact configuration against the oracle
@@ -242,9 +286,14 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
         "pcie5_x16_theoretical_GBs": PCIE5_X16_GBS, "max_abs_err_vs_fp64": err,
         "resident_bytes": (n - n_host) * slot_b,
         "host_read": "engine default (staged when the host pages form long address runs, "
-                     "else read in place)",
+                     "else read in place; staging copies on the side stream when the device "
+                     "pages are >= 256 MiB)",
         "staged_ms_per_call": per_staged * 1e3,
         "staged_host_link_GBs": host_bytes / per_staged / 1e9,
+        "staged_side_stream_ms_per_call": per_side * 1e3,
+        "staged_side_stream_frac_of_measured_h2d": host_bytes / per_side / 1e9 / peak,
+        "staged_one_stream_ms_per_call": per_one * 1e3,
+        "timing": f"best of 3 runs of {steps} calls after 3 warm-up calls",
         "in_place_ms_per_call": per_direct * 1e3,
         "in_place_host_link_GBs": host_bytes / per_direct / 1e9,
     }
@@ -789,9 +838,12 @@ def main():
     log(json.dumps(dprof))
 
     log("headline: qwen3-8b-32k all resident")
-    h = gpu_headline(args, torch, W, paged)
+    h = gpu_headline(args, torch, W, paged, kernel_timing=True)
     value = h["alg_bytes"] / h["per_call_s"] / 1e9
-    log(f"per call {h['per_call_s'] * 1e6:.2f} us, {value:.1f} GB/s")
+    kern_us = h["split_kernel_us_mean"]
+    kern_gbs = h["alg_bytes"] / (kern_us * 1e-6) / 1e9
+    log(f"per call {h['per_call_s'] * 1e6:.2f} us, {value:.1f} GB/s; decode kernel "
+        f"{kern_us:.2f} us, {kern_gbs:.1f} GB/s")
 
     if args.copy_calibration:
         n = 1 << 30
@@ -871,11 +923,15 @@ def main():
         cpu, threads = cpu_baseline(args, torch, W)
         log(json.dumps(cpu))
 
-    traffic = None
+    # HBM bytes per launch from the committed FETCH_SIZE / WRITE_SIZE counters:
+    # the decode kernel's own (the roofline's kernel), and the whole call's
+    traffic = call_traffic = None
     tpath = os.path.join(ROOT, "profiles", "paged_decode_qwen3-8b-32k_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            tj = json.load(f)
+        traffic = tj.get("decode_hbm_bytes_per_launch")
+        call_traffic = tj.get("hbm_bytes_per_launch")
     # the rocprofv3 kernel durations of the same call (decode + merge kernels),
     # from the committed profile: the live call time above should agree
     prof = None
@@ -902,13 +958,25 @@ def main():
                    "global_batch": 1, "seq_len": 32768, "page_size": 16},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "decode_steps_per_s_32k": round(1.0 / (QWEN3_8B_LAYERS * h["per_call_s"]), 2),
-        "roofline": {"bound": "hbm", "achieved": round(value, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic,
                      "alg_bytes_per_launch": h["alg_bytes"],
-                     "avg_launch_us": round(h["per_call_s"] * 1e6, 3),
-                     "launch": "one helm_paged_decode_attn call = decode_mfma_kernel + "
-                               "merge_splits_d128_kernel, timed with HIP events on its stream",
+                     "avg_launch_us": round(kern_us, 3),
+                     "median_launch_us": round(h["split_kernel_us_median"], 3),
+                     "launch": "decode_mfma_kernel<bf16, PoolSrc, 0, 4>, the dominant kernel "
+                               "of one helm_paged_decode_attn call (256 workgroups: 32 splits "
+                               "of 64 pages x 8 KV heads; it reads all K/V, q and the page "
+                               "table), timed with HIP events recorded on the call's stream "
+                               "around its launch (helm_profile_split_kernels), mean of "
+                               f"{args.steps} calls; the split merge after it is outside",
+                     "per_call": {"us": round(h["per_call_s"] * 1e6, 3),
+                                  "GBs": round(value, 2),
+                                  "frac": round(value / HBM_PEAK_GBS, 4),
+                                  "traffic": call_traffic,
+                                  "launch": "one whole helm_paged_decode_attn call: the "
+                                            "decode kernel + the split merge kernel, HIP "
+                                            "events around the calls"},
                      "rocprof_kernel_us": prof,
                      "host_issue_us_per_call": round(h["host_issue_us_per_call"], 2)},
         "decode_masked_32k": masked_c2,

@@ -85,6 +85,8 @@ SIGNATURES = {
         _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, ctypes.c_int, _f32,
         _c_void_p, _c_void_p, _i64, ctypes.c_int, _c_void_p, _c_void_p, ctypes.c_int,
         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
+    "helm_profile_split_kernels": (ctypes.c_int, [ctypes.c_int]),
+    "helm_profile_split_read": (ctypes.c_int, [_c_void_p, ctypes.c_int]),
     "helm_measure_bandwidth": (ctypes.c_int, [ctypes.c_int, _u64, _u64, ctypes.c_int,
                                               _c_void_p]),
     "helm_evict_pages": (ctypes.c_int, [_c_void_p, ctypes.c_int, _c_void_p, _c_void_p,

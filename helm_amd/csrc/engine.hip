@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -369,6 +370,44 @@ hipError_t dispatch(const LaunchSpec& s, hipStream_t st) {
     case HELM_F32: return launch_attn_f32(s, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+// ---- split-kernel timing (helm_profile_split_kernels) ---------------------------
+// Events around the split kernel launch of the next armed calls: pair i =
+// (before, after) of the i-th timed call.  g_prof_left > 0 only while armed,
+// so an unarmed launch reads one atomic.
+std::mutex g_prof_mu;
+std::vector<hipEvent_t> g_prof_ev;
+int g_prof_used = 0;
+std::atomic<int> g_prof_left{0};
+
+void prof_free_locked() {
+  for (hipEvent_t ev : g_prof_ev)
+    if (ev) (void)hipEventDestroy(ev);
+  g_prof_ev.clear();
+  g_prof_used = 0;
+  g_prof_left.store(0);
+}
+
+// dispatch() with the armed timing events recorded around the launch
+hipError_t dispatch_timed(const LaunchSpec& s, hipStream_t st) {
+  hipEvent_t before = nullptr, after = nullptr;
+  if (g_prof_left.load(std::memory_order_relaxed) > 0) {
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    if (g_prof_left.load() > 0) {
+      before = g_prof_ev[2 * g_prof_used];
+      after = g_prof_ev[2 * g_prof_used + 1];
+      ++g_prof_used;
+      g_prof_left.fetch_sub(1);
+    }
+  }
+  if (before) {
+    const hipError_t e = hipEventRecord(before, st);
+    if (e != hipSuccess) return e;
+  }
+  hipError_t e = dispatch(s, st);
+  if (after && e == hipSuccess) e = hipEventRecord(after, st);
+  return e;
 }
 
 // Combines the split partials of every tile into the output (after the
@@ -880,6 +919,36 @@ int helm_engine_create(int device, size_t chunk_bytes, int ring_slots,
   return HELM_OK;
 }
 
+int helm_profile_split_kernels(int n) {
+  if (n < 0) return fail(HELM_E_INVALID, "negative call count");
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  prof_free_locked();
+  if (n == 0) return HELM_OK;
+  g_prof_ev.assign(2 * (size_t)n, nullptr);
+  for (hipEvent_t& ev : g_prof_ev) {
+    const hipError_t e = hipEventCreate(&ev);
+    if (e != hipSuccess) {
+      prof_free_locked();
+      return hip_fail(e, "hipEventCreate");
+    }
+  }
+  g_prof_left.store(n);
+  return HELM_OK;
+}
+
+int helm_profile_split_read(float* us_out, int max_n) {
+  if (!us_out || max_n < 0) return fail(HELM_E_INVALID, "bad output array");
+  std::lock_guard<std::mutex> lock(g_prof_mu);
+  const int n = std::min(g_prof_used, max_n);
+  for (int i = 0; i < n; ++i) {
+    HELM_HIP(hipEventSynchronize(g_prof_ev[2 * i + 1]));
+    float ms = 0.f;
+    HELM_HIP(hipEventElapsedTime(&ms, g_prof_ev[2 * i], g_prof_ev[2 * i + 1]));
+    us_out[i] = ms * 1e3f;
+  }
+  return n;
+}
+
 int helm_engine_destroy(helm_engine* e) {
   if (!e) return HELM_OK;
   // teardown: report nothing, release everything that was created
@@ -986,7 +1055,7 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
   s.feat = (mask ? kFeatMask : 0) | (softcap > 0.f ? kFeatCap : 0);
   s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.qblocks(), B);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e = dispatch(s, st);
+  hipError_t e = dispatch_timed(s, st);
   if (e != hipSuccess) return hip_fail(e, "paged_attn launch");
   e = launch_merge(s, B, Hkv, st);
   if (e != hipSuccess) return hip_fail(e, "merge launch");
@@ -1447,7 +1516,7 @@ static int paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B, in
            (causal ? kFeatCausal : 0);
   s.grid = compact ? dim3(all_splits, Hkv * pl.qblocks(), 1)
                   : dim3(std::max(1, pl.max_splits), Hkv * pl.qblocks(), B);
-  hipError_t e = dispatch(s, st);
+  hipError_t e = dispatch_timed(s, st);
   if (e != hipSuccess) return hip_fail(e, "paged_attn_seqs launch");
   e = launch_merge(s, B, Hkv, st);
   if (e != hipSuccess) return hip_fail(e, "merge launch");

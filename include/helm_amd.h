@@ -329,6 +329,23 @@ typedef struct helm_bandwidth {
 int helm_measure_bandwidth(int device, uint64_t stream_bytes, uint64_t link_bytes,
                            int iters, helm_bandwidth* out);
 
+/* ---- split-kernel timing ----------------------------------------------------- */
+
+/* No counterpart in HELM: a profiling hook for callers that time the
+ * attention kernel itself (the bench's roofline) rather than the whole call.
+ * Arms HIP-event timing of the split (attention) kernel launches of the next
+ * n calls of helm_paged_decode_attn, helm_paged_decode_attn_static and
+ * helm_paged_attn_seqs[_append] in this process: an event is recorded on the
+ * call's stream just before the launch and one just after it, so the split
+ * merge that follows is outside the interval.  n = 0 disarms and frees the
+ * events.  Process-wide; arm, run and read from one thread. */
+int helm_profile_split_kernels(int n);
+
+/* Waits for the armed calls' events and writes the split-kernel durations of
+ * the calls timed so far (microseconds, call order) to us_out[0 .. max_n);
+ * returns how many were written (>= 0), or an error (< 0 / HIP code). */
+int helm_profile_split_read(float* us_out, int max_n);
+
 #ifdef __cplusplus
 }
 #endif

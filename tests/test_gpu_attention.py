@@ -417,3 +417,28 @@ def test_merge_kernel_column_groups(groups, monkeypatch):
                                  case["lens"], max_pages=case["max_pages"], pages_per_split=8)
     torch.cuda.synchronize()
     _check_pool(w, case, out)
+
+
+def test_split_kernel_timing_hook():
+    """helm_profile_split_kernels times the attention kernel of exactly the
+    next n calls (positive, below each call's whole time) and changes no
+    output bit; n = 0 disarms."""
+    from helm_amd import _native
+    w = W.Workload("t", 1, 32, 8, 128, torch.bfloat16, T=8192)
+    case = W.make_pool_case(w, seed=23, device=DEV)
+    args = (case["q"], case["k_pool"], case["v_pool"], case["table"], case["lens"])
+    ref = paged_decode_attention(*args, max_pages=case["max_pages"])
+    lib = _native.load()
+    _native.call("helm_profile_split_kernels", 3)
+    try:
+        outs = [paged_decode_attention(*args, max_pages=case["max_pages"]) for _ in range(5)]
+        torch.cuda.synchronize()
+        buf = np.zeros(8, dtype=np.float32)
+        n = lib.helm_profile_split_read(_native.ptr(buf), 8)
+    finally:
+        _native.call("helm_profile_split_kernels", 0)
+    assert n == 3                                 # only the armed calls
+    assert (buf[:3] > 0).all() and (buf[:3] < 10_000).all() and (buf[3:] == 0).all()
+    for out in outs:
+        assert torch.equal(out, ref)
+    assert lib.helm_profile_split_read(_native.ptr(buf), 8) == 0   # disarmed: nothing timed
