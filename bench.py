@@ -262,7 +262,7 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
     # the engine's side stream overlapped with the device pages' launch, or
     # on the caller's stream after it), read in place by the kernel over the
     # host link, and the engine's default (per call: pages in long address
-    # runs are staged; the side stream when the device pages are >= 256 MiB)
+    # runs are staged, copies on the caller's stream)
     per_staged = timed(HELM_AMD_HOST_READ="copy")
     per_side = timed(HELM_AMD_HOST_READ="copy", HELM_AMD_STAGE_STREAM="side")
     per_one = timed(HELM_AMD_HOST_READ="copy", HELM_AMD_STAGE_STREAM="one")
@@ -286,8 +286,7 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
         "pcie5_x16_theoretical_GBs": PCIE5_X16_GBS, "max_abs_err_vs_fp64": err,
         "resident_bytes": (n - n_host) * slot_b,
         "host_read": "engine default (staged when the host pages form long address runs, "
-                     "else read in place; staging copies on the side stream when the device "
-                     "pages are >= 256 MiB)",
+                     "else read in place; staging copies on the caller's stream)",
         "staged_ms_per_call": per_staged * 1e3,
         "staged_host_link_GBs": host_bytes / per_staged / 1e9,
         "staged_side_stream_ms_per_call": per_side * 1e3,

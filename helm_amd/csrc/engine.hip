@@ -656,19 +656,17 @@ int host_read_mode() {
 
 bool host_read_in_place() { return host_read_mode() != 0; }
 
-// Where a call's staging copies go.  On the engine's side stream they run
-// while the device pages' launch runs on the caller's stream, but the two
-// joins (side stream after the caller's earlier work, chunk launch after its
-// copies) cost tens of microseconds per call here, so the side stream pays
-// only when that launch is long: Llama-2-13B 128k with 75% in host (671 MB
-// resident) 36.96 -> 36.66 ms per call, Qwen3-8B 32k with 50% in host (67 MB
-// resident) 1.271 -> 1.286 ms.  HELM_AMD_STAGE_STREAM=side|one forces either.
-constexpr size_t kSideStreamMinResident = (size_t)256 << 20;
-bool stage_on_side_stream(size_t resident_bytes) {
+// Where a call's staging copies go.  On the engine's side stream
+// (HELM_AMD_STAGE_STREAM=side) they run while the device pages' launch runs
+// on the caller's stream, but the two joins (side stream after the caller's
+// earlier work, chunk launch after its copies) cost more than that overlap
+// wins here: Qwen3-8B 32k with 50% in host (67 MB of device pages) 1.25 ms
+// per call on one stream, 1.29-1.38 with the side stream (1.86 in one run);
+// Llama-2-13B 128k with 75% in host (671 MB) 36.4-37.0 ms on one stream,
+// 36.7-37.4 with the side stream.  So the default is the caller's stream.
+bool stage_on_side_stream() {
   const char* e = std::getenv("HELM_AMD_STAGE_STREAM");
-  if (e && std::strcmp(e, "one") == 0) return false;
-  if (e && std::strcmp(e, "side") == 0) return true;
-  return resident_bytes >= kSideStreamMinResident;
+  return e && std::strcmp(e, "side") == 0;
 }
 
 // The staging copies reach the link's rate only in large runs: hipMemcpyAsync
@@ -1345,21 +1343,16 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   }
 
   // ---- mixed residency (B == 1) ---------------------------------------------
-  // Staged chunks are copied on the engine's side stream while the caller's
-  // stream runs the device pages' launch and then, chunk by chunk, the launch
-  // that reads each one: chunk c's launch waits for chunk c's copies only, so
+  // With HELM_AMD_STAGE_STREAM=side, staged chunks are copied on the engine's
+  // side stream while the caller's stream runs the device pages' launch and
+  // then, chunk by chunk, the launch that reads each one: chunk c's launch waits for chunk c's copies only, so
   // the host link stays busy while the kernels run.  The side stream first
   // waits for everything queued on the caller's stream before this call (the
   // evictions that wrote the host pages, and the earlier calls' readers of
   // the ring), and a slot's next copy waits for the launch that read it.
-  // Events carry no timestamps.  Without the side stream (short device-page
-  // launch, or HELM_AMD_STAGE_STREAM=one) every copy is queued on the
-  // caller's stream in launch order.
-  size_t resident_bytes = 0;
-  for (const Launch& L : launches)
-    if (L.chunk < 0)
-      for (int i = L.lo; i < L.hi; ++i) resident_bytes += 2 * page_extent(desc[i], Hkv, D, eb);
-  const bool side = stage_on_side_stream(resident_bytes);
+  // Events carry no timestamps.  Without the side stream (the default) every
+  // copy is queued on the caller's stream in launch order.
+  const bool side = stage_on_side_stream();
   const int n_chunks = (int)chunk_runs.size();
   auto issue_copies = [&](int c) -> int {
     const int slot = chunk_slot[c];

@@ -210,8 +210,8 @@ def _ring_engine(chunk, slots):
 @pytest.fixture(params=["side", "one"])
 def stage_stream(request, monkeypatch):
     """Staging copies on the engine's side stream joined by events
-    (HELM_AMD_STAGE_STREAM=side; the default for calls whose device pages
-    are >= 256 MiB), or queued on the caller's stream (=one)."""
+    (HELM_AMD_STAGE_STREAM=side), or queued on the caller's stream (=one,
+    the same as the default)."""
     monkeypatch.setenv("HELM_AMD_STAGE_STREAM", request.param)
     return request.param
 
