@@ -505,6 +505,84 @@ def pool_error(torch, h, heads):
     return worst
 
 
+def gpu_records_decode(torch, W, h, steps=100):
+    """The pool leg's batch (`h`, same data) through helm_paged_attn_seqs, the
+    entry point _decode_batched takes for a batch whose pages are all on the
+    device (kv_offload.py:152-174): one device-resident helm_page record
+    array per sequence, the grid numbering exactly the sequences' splits (the
+    pool entry point's grid also holds workgroups that find no split of a
+    short sequence).  The same number of pool copies rotated, HIP events
+    around `steps` calls; max |error| against fp64 on the first and last KV
+    heads of every sequence."""
+    from helm_amd import _native
+    from helm_amd.runtime import engine
+    from oracle.attention import attention_fp64_batched
+    w, case = h["w"], h["case"]
+    dev = case["q"].device
+    pool0 = case["pool"]
+    pools = [pool0] + [torch.empty_like(pool0).copy_(pool0) for _ in range(h["pools"] - 1)]
+    P, es = w.page_size, pool0.element_size()
+    lens = case["lens_list"]
+    keep, sets = [], []
+    for pool in pools:
+        ptrs = []
+        for b, n in enumerate(case["n_pages"]):
+            slots = case["table_cpu"][b, :n].numpy().astype(np.uint64)
+            rec = np.zeros(n, dtype=_native.PAGE_DTYPE)
+            rec["k"] = pool.data_ptr() + slots * np.uint64(pool.stride(0) * es)
+            rec["v"] = rec["k"] + np.uint64(pool.stride(1) * es)
+            rec["used"] = P                      # the kernel caps by seq_tokens
+            rec["tok_off"] = np.arange(n, dtype=np.int32) * P
+            rec["head_stride"] = pool.stride(2)
+            t = torch.from_numpy(rec.view(np.uint8).copy()).to(dev)
+            keep.append(t)
+            ptrs.append(t.data_ptr())
+        sets.append(np.array(ptrs, dtype=np.uint64))
+    npages = np.array(case["n_pages"], dtype=np.int32)
+    tokens = np.array(lens, dtype=np.int32)
+    eng = engine.get_engine(dev)
+    stream = torch.cuda.current_stream(dev)
+    out = torch.empty_like(case["q"])
+    kcode = _native.dtype_code(w.dtype)
+    fn = _native.load().helm_paged_attn_seqs
+    args_of = [(eng, case["q"].data_ptr(), out.data_ptr(), w.B, w.Hq, w.Hkv, 1, w.D,
+                _native.ptr(st), _native.ptr(npages), _native.ptr(tokens), P, 1,
+                case["scale"], 0.0, None, 0, 0, 0, 0, kcode, kcode, stream.cuda_stream)
+               for st in sets]
+
+    def call(i):
+        rc = fn(*args_of[i % len(args_of)])
+        if rc:
+            _native.check("helm_paged_attn_seqs", rc)
+
+    for i in range(10):
+        call(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        call(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    per = e0.elapsed_time(e1) / 1e3 / steps
+    G = w.Hq // w.Hkv
+    worst = 0.0
+    for b, t in enumerate(lens):
+        slots = case["table_cpu"][b, :case["n_pages"][b]].long().to(dev)
+        for kvh in (0, w.Hkv - 1):
+            K = pool0[slots, 0, kvh].reshape(-1, w.D)[:t][None].cpu()
+            V = pool0[slots, 1, kvh].reshape(-1, w.D)[:t][None].cpu()
+            hs = slice(kvh * G, (kvh + 1) * G)
+            ref = attention_fp64_batched(case["q"][b, hs].cpu(), K, V)
+            worst = max(worst, (out[b, hs].double().cpu() - ref).abs().max().item())
+    gbs = h["alg_bytes"] / per / 1e9
+    del pools, keep
+    return {"entry": "helm_paged_attn_seqs (device-resident page records per sequence, the "
+                     "batched decode of _decode_batched)",
+            "us_per_call": round(per * 1e6, 3), "GBs": round(gbs, 1),
+            "roofline_frac": round(gbs / HBM_PEAK_GBS, 4), "max_abs_err_vs_fp64": worst}
+
+
 def gpu_configs(args, torch, W, paged):
     """The other configurations of the benchmark set, each at its stated
     shape: Qwen3-0.6B 2k (fp16) and Qwen3-14B B8 ragged 4k-32k (bf16) through
@@ -524,6 +602,8 @@ def gpu_configs(args, torch, W, paged):
             "us_per_call": round(h["per_call_s"] * 1e6, 3), "GBs": round(gbs, 1),
             "roofline_frac": round(gbs / HBM_PEAK_GBS, 4), "alg_bytes": h["alg_bytes"],
             "max_abs_err_vs_fp64": pool_error(torch, h, [0, w.Hkv - 1]), "tolerance": tol}
+        if w.B > 1:
+            res[name]["records_entry"] = gpu_records_decode(torch, W, h)
         log(json.dumps(res[name]))
         del h
         torch.cuda.empty_cache()
