@@ -1345,13 +1345,14 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   // ---- mixed residency (B == 1) ---------------------------------------------
   // With HELM_AMD_STAGE_STREAM=side, staged chunks are copied on the engine's
   // side stream while the caller's stream runs the device pages' launch and
-  // then, chunk by chunk, the launch that reads each one: chunk c's launch waits for chunk c's copies only, so
-  // the host link stays busy while the kernels run.  The side stream first
-  // waits for everything queued on the caller's stream before this call (the
-  // evictions that wrote the host pages, and the earlier calls' readers of
-  // the ring), and a slot's next copy waits for the launch that read it.
-  // Events carry no timestamps.  Without the side stream (the default) every
-  // copy is queued on the caller's stream in launch order.
+  // then, chunk by chunk, the launch that reads each one: chunk c's launch
+  // waits for chunk c's copies only, so the host link stays busy while the
+  // kernels run.  The side stream first waits for everything queued on the
+  // caller's stream before this call (the evictions that wrote the host
+  // pages, and the earlier calls' readers of the ring), and a slot's next
+  // copy waits for the launch that read it.  Events carry no timestamps.
+  // Without the side stream (the default) every copy is queued on the
+  // caller's stream in launch order.
   const bool side = stage_on_side_stream();
   const int n_chunks = (int)chunk_runs.size();
   auto issue_copies = [&](int c) -> int {
