@@ -2,8 +2,8 @@
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
 import this module, and only as the checker (or, in bench.py, as the timed
-CPU baseline).  The product (helm_amd) never imports it and has no CPU
-attention path.
+CPU baseline).  The product (helm_amd) never imports it: its own host-CPU
+attention (helm_cpu_stream_attn in libhelm_cpu.so) is checked against it.
 
 Three independent statements of the same arithmetic:
 
