@@ -366,11 +366,13 @@ def gpu_full_step(args, torch, W, budget_gb, steps, name="qwen3-14b-40l-b4-64k",
     stats = KC.get_paging_stats()
     masked = None
     if masked_steps:
-        zeros = torch.zeros(B, 1, 1, w.T + warmup + steps + masked_steps + 2, device=dev)
         torch.cuda.synchronize()
         tm = time.perf_counter()
         for s in range(masked_steps):
-            mask = zeros[..., :kvcms[0].layers[0].total_tokens + 1]
+            # HELM's decode mask: built once per step in the model's dtype and
+            # handed to every layer (pipeline_runtime.py:79-92, :217)
+            mask = torch.zeros((B, 1, 1, kvcms[0].layers[0].total_tokens + 1), device=dev,
+                               dtype=w.dtype)
             for layer in range(L):
                 out = _decode_batched(kvcms, q[layer], kn[layer], vn[layer], layer, scale, mask)
         torch.cuda.synchronize()
@@ -379,7 +381,8 @@ def gpu_full_step(args, torch, W, budget_gb, steps, name="qwen3-14b-40l-b4-64k",
         kv_m = L * B * (ctx_m - (masked_steps - 1) / 2) * w.token_bytes()
         masked = {"steps": masked_steps, "steps_per_s": masked_steps / wm,
                   "ms_per_step": wm * 1e3 / masked_steps, "kv_GBs": kv_m * masked_steps / wm / 1e9,
-                  "mask": "zeros [B, 1, 1, T] (HELM's decode mask)"}
+                  "mask": "zeros [B, 1, 1, T] in bf16, built once per step and passed to "
+                          "every layer (HELM's decode mask)"}
     # spot check: the last layer's output of the last step against the oracle
     from oracle.attention import attention_fp64_batched
     pages = kvcms[0].layers[L - 1].pages
@@ -622,8 +625,10 @@ def gpu_runtime_decode(args, torch, W, layers=8, steps=25, seed=11):
     """HELM's production decode call on the Qwen3-8B 32k shape: the per-layer
     ``_decode_batched`` of the patched forwards (append the token, residency,
     attention over the layer's records) under the pipeline's decode mask,
-    zeros [1, 1, 1, T] (pipeline_runtime.py:79-92, :217), and without a mask
-    for comparison.  Eight layers of 32k tokens are rotated (1 GiB of KV, so
+    zeros [1, 1, 1, T] in bf16 built once per step and handed to every layer
+    (pipeline_runtime.py:79-92, :217; its allocation is in the timed steps, as
+    in HELM's decode loop), and without a mask for comparison.  Eight layers
+    of 32k tokens are rotated (1 GiB of KV, so
     the Infinity Cache cannot serve a layer twice).  Wall time per layer call
     (host issue included) and the GPU time between events around the loop."""
     import random
@@ -648,7 +653,6 @@ def gpu_runtime_decode(args, torch, W, layers=8, steps=25, seed=11):
     q = torch.randn((layers, 1, w.Hq, 1, w.D), generator=g, device=dev, dtype=w.dtype)
     kn = torch.randn((layers, 1, w.Hkv, 1, w.D), generator=g, device=dev, dtype=w.dtype)
     vn = torch.randn((layers, 1, w.Hkv, 1, w.D), generator=g, device=dev, dtype=w.dtype)
-    zeros = torch.zeros(1, 1, 1, w.T + 4 * steps + 8, device=dev)
     scale = 1.0 / math.sqrt(w.D)
     stream = torch.cuda.current_stream(dev)
     out = None
@@ -656,10 +660,12 @@ def gpu_runtime_decode(args, torch, W, layers=8, steps=25, seed=11):
     def run(n, masked):
         nonlocal out
         for _ in range(n):
+            # HELM's decode mask: one per step in the model's dtype, handed to
+            # every layer (pipeline_runtime.py:79-92, :217)
+            mask = (torch.zeros((1, 1, 1, m.layers[0].total_tokens + 1), device=dev,
+                                dtype=w.dtype) if masked else None)
             for lid in range(layers):
-                t = m.layers[lid].total_tokens + 1
-                out = _decode_batched([m], q[lid], kn[lid], vn[lid], lid, scale,
-                                      zeros[..., :t] if masked else None)
+                out = _decode_batched([m], q[lid], kn[lid], vn[lid], lid, scale, mask)
 
     res = {"workload": f"qwen3-8b-32k through _decode_batched: {layers} layers of {w.T} "
                        "tokens rotated, B=1, bf16, one call per layer per step"}

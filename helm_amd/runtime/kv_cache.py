@@ -24,6 +24,7 @@ import heapq
 import math
 import os
 import threading
+import weakref
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
@@ -941,6 +942,29 @@ def _attend(query: torch.Tensor, seqs: Sequence[Sequence[_Segment]], Hkv: int, k
                            softcap, causal)
 
 
+# fp32 copies of additive masks given in another dtype or on another device,
+# one per mask object: HELM's pipeline builds one decode mask per step in the
+# model's dtype (pipeline_runtime.py:79-92) and hands that object to every
+# layer, so it is converted once per step, not once per layer.  An entry is
+# dropped when its mask is freed; it is used only while the mask's address,
+# shape, strides, dtype, version counter and the target device are unchanged.
+_F32_MASKS: dict = {}
+_F32_MASK_MAX_ELEMS = 1 << 22      # larger masks (prompt chunks) convert per call
+
+
+def _mask_fp32(m: torch.Tensor, device: torch.device) -> torch.Tensor:
+    if m.numel() > _F32_MASK_MAX_ELEMS:
+        return m.to(device=device, dtype=torch.float32)
+    key = id(m)
+    sig = (m.data_ptr(), tuple(m.shape), tuple(m.stride()), m.dtype, m._version, device)
+    ent = _F32_MASKS.get(key)
+    if ent is not None and ent[0]() is m and ent[1] == sig:
+        return ent[2]
+    f = m.to(device=device, dtype=torch.float32)
+    _F32_MASKS[key] = (weakref.ref(m, lambda _r, k=key: _F32_MASKS.pop(k, None)), sig, f)
+    return f
+
+
 def _query_and_mask(query: torch.Tensor, Hkv: int, kv_dtype, t_max: int,
                     attention_mask: Optional[torch.Tensor]):
     """The query in a kernel dtype, its output buffer and the mask arguments
@@ -960,7 +984,7 @@ def _query_and_mask(query: torch.Tensor, Hkv: int, kv_dtype, t_max: int,
     if attention_mask is not None:
         m = attention_mask
         if m.dtype != torch.float32 or m.device != device:
-            m = m.to(device=device, dtype=torch.float32)
+            m = _mask_fp32(m, device)
         if m.dim() != 4:
             raise ValueError("attention_mask must be 4-D [B, H, q_len, kv_len]")
         Bm, Hm, Sm, Tm = m.shape

@@ -543,3 +543,27 @@ def test_causal_mask_offset_cache_follows_the_tensor_object():
     fresh = torch.from_numpy(arr).view(1, 1, S, T)
     assert fresh.data_ptr() == ptr and fresh._version == 0
     assert KO._causal_mask_offset(fresh, S) is None
+
+
+def test_mask_fp32_converted_once_per_object_and_version():
+    """A decode mask in the model's dtype is converted to fp32 once per mask
+    object (HELM hands one mask to every layer of a step); an in-place change
+    or a new object converts again, and a freed mask's entry goes away."""
+    import gc
+    from helm_amd.runtime import kv_cache as KC
+    cpu = torch.device("cpu")
+    m = torch.zeros(1, 1, 1, 40, dtype=torch.bfloat16)
+    a = KC._mask_fp32(m, cpu)
+    b = KC._mask_fp32(m, cpu)
+    assert a is b and a.dtype == torch.float32 and torch.equal(a, m.float())
+    m[..., 7] = -3.0                      # in place: version bump, converted anew
+    c = KC._mask_fp32(m, cpu)
+    assert c is not a and c[0, 0, 0, 7].item() == -3.0 and torch.equal(c, m.float())
+    m2 = m.clone()                        # another object with equal values
+    assert KC._mask_fp32(m2, cpu) is not c
+    key = id(m)
+    del m, a, b, c
+    gc.collect()
+    assert key not in KC._F32_MASKS
+    big = torch.zeros(1, 1, 1, KC._F32_MASK_MAX_ELEMS + 1, dtype=torch.float16)
+    assert KC._mask_fp32(big, cpu) is not KC._mask_fp32(big, cpu)   # not kept
