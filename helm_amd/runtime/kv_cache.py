@@ -948,8 +948,12 @@ def _attend(query: torch.Tensor, seqs: Sequence[Sequence[_Segment]], Hkv: int, k
 # layer, so it is converted once per step, not once per layer.  An entry is
 # dropped when its mask is freed; it is used only while the mask's address,
 # shape, strides, dtype, version counter and the target device are unchanged.
+# (A prompt chunk's padded mask, which is not recognised as causal, is also
+# handed to every layer of the chunk's forward.)  The copies kept at once are
+# bounded; past the bound a mask converts per call.
 _F32_MASKS: dict = {}
-_F32_MASK_MAX_ELEMS = 1 << 22      # larger masks (prompt chunks) convert per call
+_F32_MASK_MAX_ELEMS = 1 << 26      # one mask
+_F32_MASK_MAX_TOTAL = 1 << 28      # all copies kept (elements, 1 GiB of fp32)
 
 
 def _mask_fp32(m: torch.Tensor, device: torch.device) -> torch.Tensor:
@@ -961,7 +965,10 @@ def _mask_fp32(m: torch.Tensor, device: torch.device) -> torch.Tensor:
     if ent is not None and ent[0]() is m and ent[1] == sig:
         return ent[2]
     f = m.to(device=device, dtype=torch.float32)
-    _F32_MASKS[key] = (weakref.ref(m, lambda _r, k=key: _F32_MASKS.pop(k, None)), sig, f)
+    if ent is not None:
+        del _F32_MASKS[key]
+    if sum(e[2].numel() for e in _F32_MASKS.values()) + f.numel() <= _F32_MASK_MAX_TOTAL:
+        _F32_MASKS[key] = (weakref.ref(m, lambda _r, k=key: _F32_MASKS.pop(k, None)), sig, f)
     return f
 
 

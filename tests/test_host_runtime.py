@@ -565,5 +565,18 @@ def test_mask_fp32_converted_once_per_object_and_version():
     del m, a, b, c
     gc.collect()
     assert key not in KC._F32_MASKS
-    big = torch.zeros(1, 1, 1, KC._F32_MASK_MAX_ELEMS + 1, dtype=torch.float16)
-    assert KC._mask_fp32(big, cpu) is not KC._mask_fp32(big, cpu)   # not kept
+    saved = KC._F32_MASK_MAX_ELEMS, KC._F32_MASK_MAX_TOTAL
+    KC._F32_MASKS.clear()
+    try:
+        KC._F32_MASK_MAX_ELEMS, KC._F32_MASK_MAX_TOTAL = 64, 100
+        big = torch.zeros(1, 1, 1, 65, dtype=torch.float16)
+        assert KC._mask_fp32(big, cpu) is not KC._mask_fp32(big, cpu)   # above one mask's cap
+        keep = [torch.zeros(1, 1, 1, 40, dtype=torch.float16) for _ in range(3)]
+        conv = [KC._mask_fp32(x, cpu) for x in keep]
+        assert KC._mask_fp32(keep[0], cpu) is conv[0]        # 40 + 40 elements kept
+        assert KC._mask_fp32(keep[1], cpu) is conv[1]
+        assert KC._mask_fp32(keep[2], cpu) is not conv[2]    # past the total: per call
+        assert torch.equal(KC._mask_fp32(keep[2], cpu), keep[2].float())
+    finally:
+        KC._F32_MASK_MAX_ELEMS, KC._F32_MASK_MAX_TOTAL = saved
+        KC._F32_MASKS.clear()
