@@ -2,8 +2,11 @@
 
 Each test below checks the behaviour one of HELM's own unit tests checks
 (tests/unit/runtime/test_streaming_attention.py, test_kv_cache.py,
-test_kv_allocator.py, test_batch_kv_offload.py, test_kv_offload.py; the test
-names are kept), through ``helm_amd.runtime`` instead of ``helm.runtime``, so
+test_kv_allocator.py, test_batch_kv_offload.py, test_kv_offload.py; where a
+test here covers one HELM case it has that case's name, and neighbouring cases
+are merged, each of them also under its own HELM name in
+tests/test_helm_unit_names.py), through ``helm_amd.runtime`` instead of
+``helm.runtime``, so
 that a HELM user who swaps the modules finds the cases they rely on green.
 HELM runs these on the CPU; so do they here: a query and pages on the CPU go
 to the host-CPU attention of libhelm_cpu.so (no torch fallback).  The
