@@ -105,7 +105,9 @@ def _generate(model, ids):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("disable_async", [False, True])
-def test_hybrid_cpu_gpu_layers_match_hf_greedy_with_eviction(disable_async, monkeypatch):
+def test_hybrid_eviction_matches_reference_across_requests(disable_async, monkeypatch):
+    """HELM's test of this name (tests/integration/test_kv_eviction_e2e.py:12): a CPU +
+    GPU split with forced eviction generates HF's greedy tokens for two requests."""
     monkeypatch.setenv("HELM_DISABLE_ASYNC_KV", "1" if disable_async else "")
     ref, model = _models()
     prompts = [torch.tensor([[2 + i % 30 for i in range(L)]]) for L in (513, 17)]
