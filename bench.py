@@ -919,7 +919,8 @@ def main():
              "pinned_h2d_GBs": round(dprof["h2d_bytes_per_s"] / 1e9, 2),
              "pinned_d2h_GBs": round(dprof["d2h_bytes_per_s"] / 1e9, 2),
              "probe": "helm_measure_bandwidth: 256 MB streaming copy (read + write), "
-                      "64 MB pinned copies each way, 8 timed repetitions"}
+                      "64 MB pinned copies each way, 8 timed repetitions after >= 20 ms of "
+                      "untimed ones"}
     log(json.dumps(dprof))
 
     log("headline: qwen3-8b-32k all resident")

@@ -5,6 +5,8 @@
 // and the device, timed with HIP events on a stream of the probe's own.
 #include <hip/hip_runtime.h>
 
+#include <chrono>
+
 #include <string>
 
 #include "helm_amd.h"
@@ -100,9 +102,20 @@ extern "C" int helm_measure_bandwidth(int device, uint64_t stream_bytes, uint64_
       int cus = 0;
       PROBE_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
       const dim3 grid(8 * (cus > 0 ? cus : 256)), block(256);
-      // op() issues one copy and returns its launch status
+      // op() issues one copy and returns its launch status.  Untimed copies
+      // first: at least three (HELM's two warm-ups and its probe call,
+      // device_profiler.py:94-107) and at least 20 ms of them — the host link
+      // reads well below its rate for the first milliseconds of a process
+      // (23-37 GB/s against 57 GB/s in the same run on the same box).
       auto timed = [&](auto&& op, double* secs) -> int {
-        PROBE_HIP(op());   // warm-up
+        const auto w0 = std::chrono::steady_clock::now();
+        for (int w = 0;; ++w) {
+          PROBE_HIP(op());
+          PROBE_HIP(hipStreamSynchronize(pr.st));
+          const double el = std::chrono::duration<double>(std::chrono::steady_clock::now() -
+                                                          w0).count();
+          if (w >= 2 && el >= 0.02) break;
+        }
         PROBE_HIP(hipEventRecord(pr.e0, pr.st));
         for (int i = 0; i < iters; ++i) PROBE_HIP(op());
         PROBE_HIP(hipEventRecord(pr.e1, pr.st));

@@ -314,7 +314,9 @@ int helm_prefetch_pages(helm_engine* eng, int n, const uint64_t* src_host,
  * planner (helm/compiler/optimization/device_profiler.py:188-240: _bench_gpu's
  * stream copy, counted as 2 x bytes per copy; _bench_pcie's pinned H2D / D2H
  * copies), in bytes per second, each the mean of `iters` timed repetitions
- * after one warm-up on a stream of the probe's own. */
+ * on a stream of the probe's own, after untimed ones (at least three, and at
+ * least 20 ms of them: the host link reads low for the first milliseconds of
+ * a process). */
 typedef struct helm_bandwidth {
   double device_copy_bytes_per_s; /* HBM: a streaming-copy kernel, read + write */
   double h2d_bytes_per_s;         /* pinned host -> device, hipMemcpyAsync       */
