@@ -8,8 +8,8 @@ attention call over the whole context.  Eight independent 128 MiB pools are
 rotated so the 256 MB Infinity Cache cannot serve the KV.  `value` is the
 algorithmic bytes of one call over its time (decode kernel + split merge,
 HIP events around the calls); `roofline` is the dominant kernel's: the same
-bytes over the decode kernel's own duration, from HIP events recorded around
-its launch in a second pass of the same calls (helm_profile_split_kernels),
+bytes over the decode kernel's own duration, from HIP events attached to its
+launch in a second pass of the same calls (helm_profile_split_kernels),
 with the whole-call figures beside it under `roofline.per_call`.
 
 Also measured (extra keys of the one JSON line):
@@ -99,9 +99,8 @@ def parse():
 
 def split_kernel_us(torch, step, steps):
     """HIP-event durations (us) of the attention (split) kernel of `steps`
-    calls of `step`, the split merge after it excluded: events recorded on
-    the call's stream just before and after that launch
-    (helm_profile_split_kernels).  Mean and median."""
+    calls of `step`, the split merge after it excluded: start / stop events
+    attached to that launch (helm_profile_split_kernels).  Mean and median."""
     from helm_amd import _native
     lib = _native.load()
     _native.call("helm_profile_split_kernels", steps)
@@ -1053,8 +1052,8 @@ def main():
                      "launch": "decode_mfma_kernel<bf16, PoolSrc, 0, 4>, the dominant kernel "
                                "of one helm_paged_decode_attn call (256 workgroups: 32 splits "
                                "of 64 pages x 8 KV heads; it reads all K/V, q and the page "
-                               "table), timed with HIP events recorded on the call's stream "
-                               "around its launch (helm_profile_split_kernels), mean of "
+                               "table), timed with HIP start / stop events attached to its "
+                               "launch (helm_profile_split_kernels), mean of "
                                f"{args.steps} calls; the split merge after it is outside",
                      "per_call": {"us": round(h["per_call_s"] * 1e6, 3),
                                   "GBs": round(value, 2),

@@ -7,17 +7,22 @@
 #include "attn_mfma.h"
 #include "attn_chunk32.h"
 
+#include <hip/hip_ext.h>
+
 namespace helm {
 namespace {
 
+// Every attention launch goes through hipExtLaunchKernelGGL with the spec's
+// start / stop events (null unless helm_profile_split_kernels armed them): a
+// timed launch's events carry the kernel's own start and end.
 template <typename TKV, typename TQ, int EPL, int GM, bool DOT2>
 hipError_t launch_one(const LaunchSpec& s, hipStream_t st) {
   if (s.mode == 0) {
-    hipLaunchKernelGGL((paged_attn_kernel<TKV, TQ, EPL, GM, DOT2, PoolSrc>),
-                       s.grid, dim3(kThreads), 0, st, s.p, s.pool);
+    hipExtLaunchKernelGGL((paged_attn_kernel<TKV, TQ, EPL, GM, DOT2, PoolSrc>), s.grid,
+                          dim3(kThreads), 0, st, s.ev_start, s.ev_stop, 0, s.p, s.pool);
   } else {
-    hipLaunchKernelGGL((paged_attn_kernel<TKV, TQ, EPL, GM, DOT2, DescSrc>),
-                       s.grid, dim3(kThreads), 0, st, s.p, s.desc);
+    hipExtLaunchKernelGGL((paged_attn_kernel<TKV, TQ, EPL, GM, DOT2, DescSrc>), s.grid,
+                          dim3(kThreads), 0, st, s.ev_start, s.ev_stop, 0, s.p, s.desc);
   }
   return hipGetLastError();
 }
@@ -41,17 +46,20 @@ template <typename T, class Src, int FEAT>
 hipError_t launch_mfma_feat(const LaunchSpec& s, const Src& src, hipStream_t st) {
   if (s.p.row_waves == 2) {
     if (s.nw == 8)
-      hipLaunchKernelGGL((chunk32_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), 0, st, s.p, src);
+      hipExtLaunchKernelGGL((chunk32_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), 0, st,
+                            s.ev_start, s.ev_stop, 0, s.p, src);
     else
-      hipLaunchKernelGGL((chunk32_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), 0, st, s.p, src);
+      hipExtLaunchKernelGGL((chunk32_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), 0, st,
+                            s.ev_start, s.ev_stop, 0, s.p, src);
   } else if (s.p.row_waves)
-    hipLaunchKernelGGL((chunk_mfma_kernel<T, Src, FEAT>), s.grid, dim3(256), 0, st, s.p, src);
+    hipExtLaunchKernelGGL((chunk_mfma_kernel<T, Src, FEAT>), s.grid, dim3(256), 0, st,
+                          s.ev_start, s.ev_stop, 0, s.p, src);
   else if (s.nw == 8)
-    hipLaunchKernelGGL((decode_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), 0, st, s.p,
-                       src);
+    hipExtLaunchKernelGGL((decode_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), 0, st,
+                          s.ev_start, s.ev_stop, 0, s.p, src);
   else
-    hipLaunchKernelGGL((decode_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), 0, st, s.p,
-                       src);
+    hipExtLaunchKernelGGL((decode_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), 0, st,
+                          s.ev_start, s.ev_stop, 0, s.p, src);
   return hipGetLastError();
 }
 

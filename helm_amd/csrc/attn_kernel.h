@@ -1423,6 +1423,8 @@ struct LaunchSpec {
   int feat;           // its feature bits (MfmaFeat)
   int nw;             // its waves per workgroup (4 or 8)
   dim3 grid;
+  hipEvent_t ev_start = nullptr;   // events of the launch (helm_profile_split_kernels)
+  hipEvent_t ev_stop = nullptr;
 };
 
 // Implemented per KV dtype in attn_f16.hip / attn_bf16.hip / attn_f32.hip.

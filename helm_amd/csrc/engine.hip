@@ -389,25 +389,24 @@ void prof_free_locked() {
   g_prof_left.store(0);
 }
 
-// dispatch() with the armed timing events recorded around the launch
+// dispatch() with the armed timing events attached to the launch itself
+// (hipExtLaunchKernelGGL's start / stop events: the kernel's own start and
+// end, no queue gap before it)
 hipError_t dispatch_timed(const LaunchSpec& s, hipStream_t st) {
-  hipEvent_t before = nullptr, after = nullptr;
   if (g_prof_left.load(std::memory_order_relaxed) > 0) {
-    std::lock_guard<std::mutex> lock(g_prof_mu);
-    if (g_prof_left.load() > 0) {
-      before = g_prof_ev[2 * g_prof_used];
-      after = g_prof_ev[2 * g_prof_used + 1];
-      ++g_prof_used;
-      g_prof_left.fetch_sub(1);
+    LaunchSpec t = s;
+    {
+      std::lock_guard<std::mutex> lock(g_prof_mu);
+      if (g_prof_left.load() > 0) {
+        t.ev_start = g_prof_ev[2 * g_prof_used];
+        t.ev_stop = g_prof_ev[2 * g_prof_used + 1];
+        ++g_prof_used;
+        g_prof_left.fetch_sub(1);
+      }
     }
+    return dispatch(t, st);
   }
-  if (before) {
-    const hipError_t e = hipEventRecord(before, st);
-    if (e != hipSuccess) return e;
-  }
-  hipError_t e = dispatch(s, st);
-  if (after && e == hipSuccess) e = hipEventRecord(after, st);
-  return e;
+  return dispatch(s, st);
 }
 
 // Combines the split partials of every tile into the output (after the

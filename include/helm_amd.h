@@ -337,10 +337,10 @@ int helm_measure_bandwidth(int device, uint64_t stream_bytes, uint64_t link_byte
  * attention kernel itself (the bench's roofline) rather than the whole call.
  * Arms HIP-event timing of the split (attention) kernel launches of the next
  * n calls of helm_paged_decode_attn, helm_paged_decode_attn_static and
- * helm_paged_attn_seqs[_append] in this process: an event is recorded on the
- * call's stream just before the launch and one just after it, so the split
- * merge that follows is outside the interval.  n = 0 disarms and frees the
- * events.  Process-wide; arm, run and read from one thread. */
+ * helm_paged_attn_seqs[_append] in this process: a start and a stop event are
+ * attached to that launch (hipExtLaunchKernelGGL), so the interval is the
+ * kernel's own and the split merge that follows is outside it.  n = 0 disarms
+ * and frees the events.  Process-wide; arm, run and read from one thread. */
 int helm_profile_split_kernels(int n);
 
 /* Waits for the armed calls' events and writes the split-kernel durations of
