@@ -373,8 +373,8 @@ hipError_t dispatch(const LaunchSpec& s, hipStream_t st) {
 }
 
 // ---- split-kernel timing (helm_profile_split_kernels) ---------------------------
-// Events around the split kernel launch of the next armed calls: pair i =
-// (before, after) of the i-th timed call.  g_prof_left > 0 only while armed,
+// Start / stop events of the split kernel launch of the next armed calls:
+// pair i belongs to the i-th timed call.  g_prof_left > 0 only while armed,
 // so an unarmed launch reads one atomic.
 std::mutex g_prof_mu;
 std::vector<hipEvent_t> g_prof_ev;
@@ -660,7 +660,8 @@ bool host_read_in_place() { return host_read_mode() != 0; }
 // on the caller's stream, but the two joins (side stream after the caller's
 // earlier work, chunk launch after its copies) cost more than that overlap
 // wins here: Qwen3-8B 32k with 50% in host (67 MB of device pages) 1.25 ms
-// per call on one stream, 1.29-1.38 with the side stream (1.86 in one run);
+// per call on one stream, 1.29-1.38 with the side stream (1.86-1.96 inside
+// full bench runs);
 // Llama-2-13B 128k with 75% in host (671 MB) 36.4-37.0 ms on one stream,
 // 36.7-37.4 with the side stream.  So the default is the caller's stream.
 bool stage_on_side_stream() {
