@@ -12,17 +12,26 @@
 namespace helm {
 namespace {
 
-// Every attention launch goes through hipExtLaunchKernelGGL with the spec's
-// start / stop events (null unless helm_profile_split_kernels armed them): a
-// timed launch's events carry the kernel's own start and end.
+// A launch timed by helm_profile_split_kernels goes through
+// hipExtLaunchKernelGGL with the spec's start / stop events, which then carry
+// the kernel's own start and end; every other launch is a plain launch.
+#define HELM_ATTN_LAUNCH(KERNEL, GRID, BLOCK, ...)                                       \
+  do {                                                                                   \
+    if (s.ev_start)                                                                      \
+      hipExtLaunchKernelGGL(KERNEL, GRID, BLOCK, 0, st, s.ev_start, s.ev_stop, 0,        \
+                            __VA_ARGS__);                                                \
+    else                                                                                 \
+      hipLaunchKernelGGL(KERNEL, GRID, BLOCK, 0, st, __VA_ARGS__);                       \
+  } while (0)
+
 template <typename TKV, typename TQ, int EPL, int GM, bool DOT2>
 hipError_t launch_one(const LaunchSpec& s, hipStream_t st) {
   if (s.mode == 0) {
-    hipExtLaunchKernelGGL((paged_attn_kernel<TKV, TQ, EPL, GM, DOT2, PoolSrc>), s.grid,
-                          dim3(kThreads), 0, st, s.ev_start, s.ev_stop, 0, s.p, s.pool);
+    HELM_ATTN_LAUNCH((paged_attn_kernel<TKV, TQ, EPL, GM, DOT2, PoolSrc>), s.grid, dim3(kThreads),
+                     s.p, s.pool);
   } else {
-    hipExtLaunchKernelGGL((paged_attn_kernel<TKV, TQ, EPL, GM, DOT2, DescSrc>), s.grid,
-                          dim3(kThreads), 0, st, s.ev_start, s.ev_stop, 0, s.p, s.desc);
+    HELM_ATTN_LAUNCH((paged_attn_kernel<TKV, TQ, EPL, GM, DOT2, DescSrc>), s.grid, dim3(kThreads),
+                     s.p, s.desc);
   }
   return hipGetLastError();
 }
@@ -46,20 +55,15 @@ template <typename T, class Src, int FEAT>
 hipError_t launch_mfma_feat(const LaunchSpec& s, const Src& src, hipStream_t st) {
   if (s.p.row_waves == 2) {
     if (s.nw == 8)
-      hipExtLaunchKernelGGL((chunk32_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), 0, st,
-                            s.ev_start, s.ev_stop, 0, s.p, src);
+      HELM_ATTN_LAUNCH((chunk32_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), s.p, src);
     else
-      hipExtLaunchKernelGGL((chunk32_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), 0, st,
-                            s.ev_start, s.ev_stop, 0, s.p, src);
+      HELM_ATTN_LAUNCH((chunk32_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), s.p, src);
   } else if (s.p.row_waves)
-    hipExtLaunchKernelGGL((chunk_mfma_kernel<T, Src, FEAT>), s.grid, dim3(256), 0, st,
-                          s.ev_start, s.ev_stop, 0, s.p, src);
+    HELM_ATTN_LAUNCH((chunk_mfma_kernel<T, Src, FEAT>), s.grid, dim3(256), s.p, src);
   else if (s.nw == 8)
-    hipExtLaunchKernelGGL((decode_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), 0, st,
-                          s.ev_start, s.ev_stop, 0, s.p, src);
+    HELM_ATTN_LAUNCH((decode_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), s.p, src);
   else
-    hipExtLaunchKernelGGL((decode_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), 0, st,
-                          s.ev_start, s.ev_stop, 0, s.p, src);
+    HELM_ATTN_LAUNCH((decode_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), s.p, src);
   return hipGetLastError();
 }
 

@@ -442,3 +442,47 @@ def test_split_kernel_timing_hook():
     for out in outs:
         assert torch.equal(out, ref)
     assert lib.helm_profile_split_read(_native.ptr(buf), 8) == 0   # disarmed: nothing timed
+
+
+@pytest.mark.parametrize("T", [2048, 4096], ids=["merge-in-kernel", "merge-kernel"])
+def test_static_decode_replays_from_a_hip_graph(T):
+    """The decode entry point that allocates nothing, captured in a HIP graph
+    (torch.cuda.CUDAGraph): every replay, with eager work and synchronizations
+    between the replays, equals the eager call bit for bit — with the split
+    merge in the decode kernel (16 splits: its tickets, left zero by every
+    call) and in a second kernel (32 splits)."""
+    from helm_amd import _native, paged
+    w = W.Workload("graph", 1, 32, 8, 128, torch.bfloat16, T=T)
+    case = W.make_pool_case(w, seed=29, device=DEV)
+
+    def static_call(out):
+        # the C-ABI arguments on torch's current stream (the capture stream
+        # inside the graph context)
+        args, keep = paged._decode_args(case["q"], case["k_pool"], case["v_pool"], case["table"],
+                                        case["lens"], case["max_pages"], sum(case["n_pages"]),
+                                        None, None, None, out, 0)
+        _native.call("helm_paged_decode_attn_static", *(list(args[:-3]) + [args[-1]]))
+        return keep
+
+    eager = torch.empty_like(case["q"])
+    keep = [static_call(eager)]
+    torch.cuda.synchronize()
+    out = torch.empty_like(case["q"])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):            # a warm-up call on a side stream first
+        keep.append(static_call(out))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        keep.append(static_call(out))
+    x = torch.randn(1024, 1024, device=DEV)
+    for i in range(4):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs from the eager call"
+        x = (x @ x).clamp_(-1, 1)            # eager work between the replays
+        torch.cuda.synchronize()
