@@ -93,7 +93,9 @@ def parse():
     ap.add_argument("--no-runtime", action="store_true",
                     help="skip the _decode_batched production-call leg")
     ap.add_argument("--all", action="store_true",
-                    help="also measure every benchmark configuration (gpurun_out/bench_all.json)")
+                    help="also measure every benchmark configuration (one line each on stderr)")
+    ap.add_argument("--all-json", default=None, metavar="PATH",
+                    help="with --all, also write the configurations' rows to PATH as JSON")
     return ap.parse_args()
 
 
@@ -464,7 +466,7 @@ def gpu_prefill(args, torch, T=32768, S=512, reps=20, seed=6):
 
 def all_configs(args, torch, W, paged):
     """Every decode-attention configuration of the benchmark set, one line
-    each on stderr and all of them in gpurun_out/bench_all.json."""
+    each on stderr and, with --all-json PATH, all of them in PATH."""
     rows = []
     for name, seed in (("qwen3-0.6b-2k", 0), ("qwen3-8b-32k", 1), ("qwen3-14b-ragged-b8", 3)):
         h = gpu_headline(args, torch, W, paged, name=name, seed=seed, steps=100)
@@ -482,9 +484,10 @@ def all_configs(args, torch, W, paged):
         rows.append(o)
         log(json.dumps(o))
         torch.cuda.empty_cache()
-    os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
-    with open(os.path.join(ROOT, "gpurun_out", "bench_all.json"), "w") as f:
-        json.dump(rows, f, indent=1)
+    if args.all_json:
+        os.makedirs(os.path.dirname(os.path.abspath(args.all_json)), exist_ok=True)
+        with open(args.all_json, "w") as f:
+            json.dump(rows, f, indent=1)
     return rows
 
 
@@ -730,7 +733,7 @@ def cpu_info():
 
 def cpu_threads():
     """Threads for the host-CPU legs: one per physical core this process may
-    use, at most the OpenMP thread count the box sets (its CPU share)."""
+    use, at most the OpenMP thread count the machine sets (its CPU share)."""
     info = cpu_info()
     cap = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
     return max(1, min(info["physical_cores_allowed"], cap)), info
@@ -900,7 +903,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the paged decode "
-              "attention shards by sequence / KV head with no exchange, see DESIGN.md",
+              "attention shards by sequence / KV head with no exchange between GPUs",
               file=sys.stderr)
         sys.exit(2)
     import torch

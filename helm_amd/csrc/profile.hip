@@ -106,7 +106,7 @@ extern "C" int helm_measure_bandwidth(int device, uint64_t stream_bytes, uint64_
       // first: at least three (HELM's two warm-ups and its probe call,
       // device_profiler.py:94-107) and at least 20 ms of them — the host link
       // reads well below its rate for the first milliseconds of a process
-      // (23-37 GB/s against 57 GB/s in the same run on the same box).
+      // (23-37 GB/s against 57 GB/s in the same run on the same machine).
       auto timed = [&](auto&& op, double* secs) -> int {
         const auto w0 = std::chrono::steady_clock::now();
         for (int w = 0;; ++w) {

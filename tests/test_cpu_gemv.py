@@ -22,10 +22,10 @@ needs_kernel = pytest.mark.skipif(not kernels.is_available(),
 
 
 # Every test here runs twice: in the CPU suite, and under the `gpu` marker so
-# that the GPU run exercises the host-CPU code on the GPU box's own host CPU
-# (another microarchitecture than the build machine's).
+# that the GPU run exercises the host-CPU code on the host CPU of the machine
+# that holds the GPU (another microarchitecture than the build machine's).
 @pytest.fixture(autouse=True, params=[pytest.param("host", id="host"),
-                                      pytest.param("box", id="box", marks=pytest.mark.gpu)])
+                                      pytest.param("gpu_host", id="gpu_host", marks=pytest.mark.gpu)])
 def _where(request):
     return request.param
 
