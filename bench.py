@@ -227,7 +227,7 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
     def call():
         _native.call("helm_stream_attn", eng, case["q"].data_ptr(), out.data_ptr(), 1, w.Hq,
                      w.Hkv, 1, w.D, _native.ptr(pages), _native.ptr(seq_off), case["scale"], 0.0,
-                     None, 0, 0, 0, 0, kcode, kcode, stream.cuda_stream)
+                     None, 0, 0, 0, _native.HELM_F32, 0, kcode, kcode, stream.cuda_stream)
 
     steps = steps or args.offload_steps
 
@@ -552,7 +552,8 @@ def gpu_records_decode(torch, W, h, steps=100):
     fn = _native.load().helm_paged_attn_seqs
     args_of = [(eng, case["q"].data_ptr(), out.data_ptr(), w.B, w.Hq, w.Hkv, 1, w.D,
                 _native.ptr(st), _native.ptr(npages), _native.ptr(tokens), P, 1,
-                case["scale"], 0.0, None, 0, 0, 0, 0, kcode, kcode, stream.cuda_stream)
+                case["scale"], 0.0, None, 0, 0, 0, _native.HELM_F32, 0, kcode, kcode,
+                stream.cuda_stream)
                for st in sets]
 
     def call(i):

@@ -56,25 +56,25 @@ SIGNATURES = {
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, ctypes.c_int,
         _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32, _f32, _c_void_p, _i64, _i64, _i64,
-        ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p, _sz, _c_void_p]),
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p, _sz, _c_void_p]),
     "helm_paged_decode_attn_static": (ctypes.c_int, [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, ctypes.c_int,
         _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32, _f32, _c_void_p, _i64, _i64, _i64,
-        ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
     "helm_stream_attn": (ctypes.c_int, [
         _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_int, _c_void_p, _c_void_p, _f32, _f32, _c_void_p, _i64, _i64,
-        _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
+        _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
     "helm_paged_attn_seqs": (ctypes.c_int, [
         _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_int, _c_void_p, _c_void_p, _c_void_p, ctypes.c_int,
         ctypes.c_int, _f32, _f32, _c_void_p, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int,
-        ctypes.c_int, _c_void_p]),
+        ctypes.c_int, ctypes.c_int, _c_void_p]),
     "helm_paged_attn_seqs_append": (ctypes.c_int, [
         _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, _f32, _f32, _c_void_p,
-        _i64, _i64, _i64, ctypes.c_int, _c_void_p, _c_void_p]),
+        _i64, _i64, _i64, ctypes.c_int, ctypes.c_int, _c_void_p, _c_void_p]),
     "helm_upload": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),
     "helm_host_pages_in_place": (ctypes.c_int, [_c_void_p, _c_void_p, ctypes.c_int,
                                                 ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -96,6 +96,7 @@ SIGNATURES = {
 }
 
 _lib = None
+ABI_VERSION = 2   # HELM_AMD_ABI_VERSION of include/helm_amd.h
 
 
 class HelmNativeError(RuntimeError):
@@ -120,8 +121,9 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.helm_abi_version() != 1:
-        raise ImportError(f"{LIB_PATH}: ABI version {lib.helm_abi_version()} != 1")
+    if lib.helm_abi_version() != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH}: ABI version {lib.helm_abi_version()} != {ABI_VERSION}"
+                          " (rebuild with `python -m helm_amd.build`)")
     _lib = lib
     return lib
 

@@ -178,10 +178,8 @@ __global__ __launch_bounds__(NW * 64, 2) void chunk32_mfma_kernel(AttnParams p, 
       qop[i] = row_ok ? mf_u32x4{v.x, v.y, v.z, v.w} : mf_u32x4{0u, 0u, 0u, 0u};
     }
   }
-  const float* mrow = nullptr;
-  if constexpr (kMask)
-    mrow = p.mask + (int64_t)b * p.mask_bstride + (int64_t)(hk * G + rc.g) * p.mask_hstride +
-           (int64_t)s_row * p.mask_qstride;
+  MaskRow mrow{nullptr, HELM_F32};
+  if constexpr (kMask) mrow = mask_row(p, b, hk * G + rc.g, s_row);
   const float scale = p.scale;
   const float cap = p.softcap;
   const float inv_cap = kCap ? 1.f / cap : 0.f;
@@ -309,7 +307,7 @@ __global__ __launch_bounds__(NW * 64, 2) void chunk32_mfma_kernel(AttnParams p, 
       for (int u = 0; u < 2; ++u) {
         const int nt = ntok[bp + u];
         const int last = max(nt - 1, 0);
-        const float* mb = mrow + tok0[bp + u];
+        const MaskRow mb = mrow + tok0[bp + u];
 #pragma unroll
         for (int i = 0; i < 8; ++i) mk_next[8 * u + i] = nt > 0 ? mb[min(8 * hh + i, last)] : 0.f;
       }

@@ -404,8 +404,9 @@ struct AttnParams {
   int n_qtiles;
   float scale;
   float softcap;      // <= 0: off
-  const float* mask;  // may be null
+  const void* mask;   // may be null; additive, in the element type mask_dt
   int64_t mask_bstride, mask_hstride, mask_qstride;
+  int mask_dt;        // HELM_F32, HELM_BF16 or HELM_F16
   int causal;         // 0: off; c > 0: position s sees tokens 0 .. s + c - 1
                       // (1: top-left causal)
   int pps;            // pages per split
@@ -424,6 +425,33 @@ struct AttnParams {
   int direct_out;     // 1: the call has one split; the chunk kernel writes the output
   int bpp_log2;       // log2 of bpp when bpp is a power of two, else -1
 };
+
+// One row of the additive mask, in the element type the caller built it in
+// (HELM's pipeline builds its masks in the model's dtype and adds them to the
+// fp32 scores after .to(float32), kv_cache.py:519, :535): a 16-bit element
+// widens to fp32 exactly, so reading it here equals converting the mask
+// first.  The element type is uniform, so the branch is a scalar one.
+struct MaskRow {
+  const char* base;  // element 0 of the row
+  int dt;            // HELM_F32, HELM_BF16 or HELM_F16
+
+  __device__ __forceinline__ float operator[](int64_t i) const {
+    if (dt == HELM_F32) return reinterpret_cast<const float*>(base)[i];
+    const uint32_t h = reinterpret_cast<const uint16_t*>(base)[i];
+    if (dt == HELM_BF16) return __uint_as_float(h << 16);
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+  }
+  __device__ __forceinline__ MaskRow operator+(int64_t i) const {
+    return MaskRow{base + i * (dt == HELM_F32 ? 4 : 2), dt};
+  }
+};
+
+// Row (b, h, s) of the call's mask.
+__device__ __forceinline__ MaskRow mask_row(const AttnParams& p, int b, int h, int s) {
+  return MaskRow{reinterpret_cast<const char*>(p.mask), p.mask_dt} +
+         ((int64_t)b * p.mask_bstride + (int64_t)h * p.mask_hstride +
+          (int64_t)s * p.mask_qstride);
+}
 
 // Per-workgroup LDS: per-wave online-softmax states of the tile's rows, and
 // the cross-thread reduction of the in-kernel split merge.
@@ -1223,13 +1251,27 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
       }
     }
     if (mask_shared) {
-      const float* mb = reinterpret_cast<const float*>(uniform64(
-          reinterpret_cast<uint64_t>(p.mask + mrow[0] + pv.tok_off + tok0)));
-      const auto rm = make_rsrc(mb, ntok * 4);
+      const MaskRow mr = MaskRow{reinterpret_cast<const char*>(p.mask), p.mask_dt} +
+                         (mrow[0] + pv.tok_off + tok0);
+      const char* mb = reinterpret_cast<const char*>(
+          uniform64(reinterpret_cast<uint64_t>(mr.base)));
+      if (p.mask_dt == HELM_F32) {
+        const auto rm = make_rsrc(mb, ntok * 4);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        B.mk[j] = __uint_as_float(
-            __builtin_amdgcn_raw_buffer_load_b32(rm, (4 * j + row) * 4, 0, 0));
+        for (int j = 0; j < 4; ++j)
+          B.mk[j] = __uint_as_float(
+              __builtin_amdgcn_raw_buffer_load_b32(rm, (4 * j + row) * 4, 0, 0));
+      } else {
+        // 16-bit mask: zero past the block's tokens, as the fp32 loads
+        const auto rm = make_rsrc(mb, ntok * 2);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(rm, (4 * j + row) * 2, 0, 0);
+          B.mk[j] = p.mask_dt == HELM_BF16
+                        ? __uint_as_float(h << 16)
+                        : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+        }
+      }
     }
   };
 
@@ -1291,8 +1333,8 @@ __global__ __launch_bounds__(kThreads) void paged_attn_kernel(AttnParams p,
       for (int g = 0; g < GM; ++g)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          sc[g][j] += p.mask[mrow[g] + tok_base +
-                             min(B.tok0 + 4 * j + row, used - 1)];
+          sc[g][j] += MaskRow{reinterpret_cast<const char*>(p.mask), p.mask_dt}
+              [mrow[g] + tok_base + min(B.tok0 + 4 * j + row, used - 1)];
     }
     if (p.causal) {
 #pragma unroll

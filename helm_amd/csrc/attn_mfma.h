@@ -442,10 +442,8 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
     }
   }
 
-  const float* mrow = nullptr;
-  if constexpr (kMask)
-    mrow = p.mask + (int64_t)b * p.mask_bstride + (int64_t)(hk * G + g_row) * p.mask_hstride +
-           (int64_t)s_row * p.mask_qstride;
+  MaskRow mrow{nullptr, HELM_F32};
+  if constexpr (kMask) mrow = mask_row(p, b, hk * G + g_row, s_row);
 
   const float scale = p.scale;
   const float cap = p.softcap;
@@ -631,10 +629,8 @@ __global__ __launch_bounds__(256) void chunk_mfma_kernel(AttnParams p, Src src) 
       qop[i] = row_ok ? mf_u32x4{v.x, v.y, v.z, v.w} : mf_u32x4{0u, 0u, 0u, 0u};
     }
   }
-  const float* mrow = nullptr;
-  if constexpr (kMask)
-    mrow = p.mask + (int64_t)b * p.mask_bstride + (int64_t)(hk * G + g_row) * p.mask_hstride +
-           (int64_t)s_row * p.mask_qstride;
+  MaskRow mrow{nullptr, HELM_F32};
+  if constexpr (kMask) mrow = mask_row(p, b, hk * G + g_row, s_row);
   const float scale = p.scale;
   const float cap = p.softcap;
   const float inv_cap = kCap ? 1.f / cap : 0.f;

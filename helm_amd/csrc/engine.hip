@@ -47,6 +47,11 @@ int elem_bytes(int dt) {
   }
 }
 
+// A mask's element type: HELM_F32, HELM_BF16 or HELM_F16 (read when mask != NULL).
+bool mask_dtype_ok(const void* mask, int mask_dtype) {
+  return !mask || mask_dtype == HELM_F32 || mask_dtype == HELM_BF16 || mask_dtype == HELM_F16;
+}
+
 int device_cus() {
   static int cus = 0;
   static std::once_flag once;
@@ -324,8 +329,8 @@ bool aligned(const void* p, size_t a) {
 
 void fill_params(AttnParams& a, const Plan& pl, const void* q, void* out,
                  int B, int Hq, int Hkv, int q_len, int D, float scale,
-                 float softcap, const float* mask, int64_t mbs, int64_t mhs,
-                 int64_t mqs, int causal, char* ws) {
+                 float softcap, const void* mask, int64_t mbs, int64_t mhs,
+                 int64_t mqs, int mask_dt, int causal, char* ws) {
   a.q = q;
   a.out = out;
   a.B = B;
@@ -344,6 +349,7 @@ void fill_params(AttnParams& a, const Plan& pl, const void* q, void* out,
   a.mask_bstride = mbs;
   a.mask_hstride = mhs;
   a.mask_qstride = mqs;
+  a.mask_dt = mask_dt;
   a.causal = causal;
   a.pps = pl.pps;
   a.bpp = pl.bpp;
@@ -1005,9 +1011,9 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
                            int table_stride, const int32_t* seq_lens, int B,
                            int Hq, int Hkv, int q_len, int D, int page_size,
                            int max_pages, int total_pages, float scale,
-                           float softcap, const float* mask,
+                           float softcap, const void* mask,
                            int64_t mask_bstride, int64_t mask_hstride,
-                           int64_t mask_qstride, int kv_dtype, int q_dtype,
+                           int64_t mask_qstride, int mask_dtype, int kv_dtype, int q_dtype,
                            int pages_per_split, void* workspace,
                            size_t ws_bytes, void* stream) {
   if (!q || !out || !k_pool || !v_pool || !page_table || !seq_lens ||
@@ -1015,6 +1021,7 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
     return fail(HELM_E_INVALID, "null pointer argument");
   if (page_size <= 0 || max_pages < 0 || table_stride < max_pages)
     return fail(HELM_E_INVALID, "bad page_size / max_pages / table_stride");
+  if (!mask_dtype_ok(mask, mask_dtype)) return fail(HELM_E_INVALID, "unknown mask dtype");
   const int eb = elem_bytes(kv_dtype);
   const int qb = elem_bytes(q_dtype);
   const bool al = aligned(q, 16) && aligned(out, 16) && aligned(k_pool, 16) &&
@@ -1030,7 +1037,7 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
                 "workspace too small: need " + std::to_string(pl.total()));
   LaunchSpec s{};
   fill_params(s.p, pl, q, out, B, Hq, Hkv, q_len, D, scale, softcap, mask,
-              mask_bstride, mask_hstride, mask_qstride, 0,
+              mask_bstride, mask_hstride, mask_qstride, mask_dtype, 0,
               reinterpret_cast<char*>(workspace));
   s.p.full_d = (al && D == 16 * pl.epl) ? 1 : 0;
   s.mode = 0;
@@ -1066,9 +1073,9 @@ int helm_paged_decode_attn_static(const void* q, void* out, const void* k_pool,
                                   int table_stride, const int32_t* seq_lens, int B,
                                   int Hq, int Hkv, int q_len, int D, int page_size,
                                   int max_pages, int total_pages, float scale,
-                                  float softcap, const float* mask,
+                                  float softcap, const void* mask,
                                   int64_t mask_bstride, int64_t mask_hstride,
-                                  int64_t mask_qstride, int kv_dtype, int q_dtype,
+                                  int64_t mask_qstride, int mask_dtype, int kv_dtype, int q_dtype,
                                   int pages_per_split, void* stream) {
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   int dev = -1;
@@ -1078,7 +1085,7 @@ int helm_paged_decode_attn_static(const void* q, void* out, const void* k_pool,
   rc = helm_paged_decode_attn(q, out, k_pool, v_pool, slot_stride, head_stride, page_table,
                               table_stride, seq_lens, B, Hq, Hkv, q_len, D, page_size,
                               max_pages, total_pages, scale, softcap, mask, mask_bstride,
-                              mask_hstride, mask_qstride, kv_dtype, q_dtype, pages_per_split,
+                              mask_hstride, mask_qstride, mask_dtype, kv_dtype, q_dtype, pages_per_split,
                               ws, HELM_STATIC_SCRATCH_BYTES, stream);
   if (rc > 0) {
     // a launch failed part-way: the tickets may not be back at zero
@@ -1096,14 +1103,15 @@ int helm_paged_decode_attn_static(const void* q, void* out, const void* k_pool,
 int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
                      int Hq, int Hkv, int q_len, int D, const helm_page* pages,
                      const int32_t* seq_off, float scale, float softcap,
-                     const float* mask, int64_t mask_bstride,
-                     int64_t mask_hstride, int64_t mask_qstride, int causal,
+                     const void* mask, int64_t mask_bstride,
+                     int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int causal,
                      int kv_dtype, int q_dtype, void* stream) {
   if (!eng || !q || !out || !seq_off)
     return fail(HELM_E_INVALID, "null pointer argument");
   if (B <= 0) return fail(HELM_E_INVALID, "B must be positive");
   if (Hkv <= 0 || D <= 0) return fail(HELM_E_INVALID, "bad Hkv / D");
   if (causal < 0) return fail(HELM_E_INVALID, "causal must be >= 0");
+  if (!mask_dtype_ok(mask, mask_dtype)) return fail(HELM_E_INVALID, "unknown mask dtype");
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int eb = elem_bytes(kv_dtype);
   const int qb = elem_bytes(q_dtype);
@@ -1316,7 +1324,7 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
 
   LaunchSpec s{};
   fill_params(s.p, pl, q, out, B, Hq, Hkv, q_len, D, scale, softcap, mask,
-              mask_bstride, mask_hstride, mask_qstride, causal, eng->ws);
+              mask_bstride, mask_hstride, mask_qstride, mask_dtype, causal, eng->ws);
   s.p.full_d = (al && D == 16 * pl.epl) ? 1 : 0;
   s.mode = 1;
   s.desc.pages = reinterpret_cast<const helm_page*>(dev_blob);
@@ -1411,14 +1419,15 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
 static int paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B, int Hq, int Hkv,
                     int q_len, int D, const uint64_t* seq_pages, const int32_t* seq_npages,
                     const int32_t* seq_tokens, int page_tokens, int aligned16, float scale,
-                    float softcap, const float* mask, int64_t mask_bstride,
-                    int64_t mask_hstride, int64_t mask_qstride, int causal, int kv_dtype,
+                    float softcap, const void* mask, int64_t mask_bstride,
+                    int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int causal, int kv_dtype,
                     int q_dtype, const helm_append_seg* app, void* stream) {
   if (!eng || !q || !out || !seq_pages || !seq_npages || !seq_tokens)
     return fail(HELM_E_INVALID, "null pointer argument");
   if (B <= 0 || Hkv <= 0 || D <= 0 || page_tokens <= 0)
     return fail(HELM_E_INVALID, "bad shape");
   if (causal < 0) return fail(HELM_E_INVALID, "causal must be >= 0");
+  if (!mask_dtype_ok(mask, mask_dtype)) return fail(HELM_E_INVALID, "unknown mask dtype");
   if (B > kSeqArgs)
     return fail(HELM_E_UNSUPPORTED,
                 "more than " + std::to_string(kSeqArgs) + " sequences per call");
@@ -1474,7 +1483,7 @@ static int paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B, in
 
   LaunchSpec s{};
   fill_params(s.p, pl, q, out, B, Hq, Hkv, q_len, D, scale, softcap, mask,
-              mask_bstride, mask_hstride, mask_qstride, causal, eng->ws);
+              mask_bstride, mask_hstride, mask_qstride, mask_dtype, causal, eng->ws);
   s.p.full_d = (al && D == 16 * pl.epl) ? 1 : 0;
   s.mode = 1;
   s.desc.elem_bytes = eb;
@@ -1522,12 +1531,12 @@ int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
                          const uint64_t* seq_pages, const int32_t* seq_npages,
                          const int32_t* seq_tokens, int page_tokens,
                          int aligned16, float scale, float softcap,
-                         const float* mask, int64_t mask_bstride,
-                         int64_t mask_hstride, int64_t mask_qstride, int causal,
+                         const void* mask, int64_t mask_bstride,
+                         int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int causal,
                          int kv_dtype, int q_dtype, void* stream) {
   return paged_attn_seqs(eng, q, out, B, Hq, Hkv, q_len, D, seq_pages, seq_npages, seq_tokens,
                          page_tokens, aligned16, scale, softcap, mask, mask_bstride,
-                         mask_hstride, mask_qstride, causal, kv_dtype, q_dtype, nullptr,
+                         mask_hstride, mask_qstride, mask_dtype, causal, kv_dtype, q_dtype, nullptr,
                          stream);
 }
 
@@ -1535,13 +1544,13 @@ int helm_paged_attn_seqs_append(helm_engine* eng, const void* q, void* out, int 
                                 int Hq, int Hkv, int D, const uint64_t* seq_pages,
                                 const int32_t* seq_npages, const int32_t* seq_tokens,
                                 int page_tokens, int aligned16, float scale, float softcap,
-                                const float* mask, int64_t mask_bstride,
-                                int64_t mask_hstride, int64_t mask_qstride, int kv_dtype,
+                                const void* mask, int64_t mask_bstride,
+                                int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int kv_dtype,
                                 const helm_append_seg* tokens, void* stream) {
   if (!tokens) return fail(HELM_E_INVALID, "null pointer argument");
   return paged_attn_seqs(eng, q, out, B, Hq, Hkv, 1, D, seq_pages, seq_npages, seq_tokens,
                          page_tokens, aligned16, scale, softcap, mask, mask_bstride,
-                         mask_hstride, mask_qstride, 0, kv_dtype, kv_dtype, tokens, stream);
+                         mask_hstride, mask_qstride, mask_dtype, 0, kv_dtype, kv_dtype, tokens, stream);
 }
 
 int helm_upload(helm_engine* eng, void* dst, const void* src, size_t bytes,

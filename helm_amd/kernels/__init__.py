@@ -20,7 +20,6 @@ from __future__ import annotations
 
 import logging
 import os
-from types import MethodType
 from typing import Optional
 
 import torch
@@ -130,18 +129,24 @@ def fp16_linear(input: torch.Tensor, weight: torch.Tensor,
                     bias.float() if bias is not None else None).half()
 
 
-def _bound_forward(self: nn.Linear, x: torch.Tensor) -> torch.Tensor:
-    """The forward bound onto a patched nn.Linear: the native GEMV path when
-    the weight and input are fp16 on the CPU at call time, else F.linear."""
-    return fp16_linear(x, self.weight, self.bias)
+class NativeLinear(nn.Linear):
+    """nn.Linear routed through ``fp16_linear``: the native GEMV path when the
+    weight and input are fp16 on the CPU at call time, else F.linear.
+    ``patch_cpu_linears`` changes a linear's class to this one in place, so
+    the module keeps its parameters, buffers, hooks and state_dict keys and
+    pickles (torch.save) like any module defined at module level."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return fp16_linear(x, self.weight, self.bias)
 
 
 def patch_cpu_linears(module: nn.Module, verbose: bool = False) -> int:
-    """Routes every fp16 CPU nn.Linear under `module` (itself included)
-    through ``fp16_linear`` and returns how many were newly routed
-    (helm/kernels/__init__.py:134-168).  A linear already routed is left as
-    it is.  When the native GEMV is unavailable nothing is changed, with one
-    warning per process."""
+    """Routes every fp16 CPU nn.Linear below `module` through ``fp16_linear``
+    and returns how many were newly routed (helm/kernels/__init__.py:134-168).
+    As HELM's walk, it visits `module`'s children recursively and never
+    `module` itself, so a bare nn.Linear passed in is left as it is (0).  A
+    linear already routed is left as it is.  When the native GEMV is
+    unavailable nothing is changed, with one warning per process."""
     global _warned
     if not is_available():
         if not _warned:
@@ -153,11 +158,13 @@ def patch_cpu_linears(module: nn.Module, verbose: bool = False) -> int:
                         load_error())
         return 0
     routed = 0
-    for sub in module.modules():
-        if (isinstance(sub, nn.Linear) and sub.weight.dtype == torch.float16
-                and sub.weight.device.type == "cpu"
-                and not getattr(sub, "_helm_native_gemv", False)):
-            sub.forward = MethodType(_bound_forward, sub)
-            sub._helm_native_gemv = True
-            routed += 1
+    for child in module.children():
+        if isinstance(child, NativeLinear):
+            continue
+        if isinstance(child, nn.Linear):
+            if child.weight.dtype == torch.float16 and child.weight.device.type == "cpu":
+                child.__class__ = NativeLinear
+                routed += 1
+        else:
+            routed += patch_cpu_linears(child, verbose=verbose)
     return routed

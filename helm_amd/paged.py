@@ -122,7 +122,10 @@ def _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages
     mask_ptr, mbs, mhs, mqs = None, 0, 0, 0
     m = None
     if attention_mask is not None:
-        m = attention_mask.to(device=q.device, dtype=torch.float32)
+        # fp32, bf16 and fp16 masks are read as given; others are widened
+        m = attention_mask.to(device=q.device)
+        if m.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            m = m.float()
         if m.stride(3) != 1:
             m = m.contiguous()
         mask_ptr = m.data_ptr()
@@ -137,7 +140,8 @@ def _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages
     args = [q.data_ptr(), out.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0),
             k_pool.stride(1), page_table.data_ptr(), page_table.stride(0), seq_lens.data_ptr(), B,
             Hq, Hkv, S, D, P, max_pages, total_pages, float(scale),
-            float(softcap) if softcap else 0.0, mask_ptr, mbs, mhs, mqs, kcode, qcode,
+            float(softcap) if softcap else 0.0, mask_ptr, mbs, mhs, mqs,
+            _native.dtype_code(m.dtype) if m is not None else _native.HELM_F32, kcode, qcode,
             pages_per_split, ws.data_ptr(), ws.numel(), _engine.stream_ptr(q.device)]
     keep = {"q": q, "out": out, "mask": m, "ws": ws, "table": page_table, "lens": seq_lens}
     return args, keep

@@ -942,22 +942,24 @@ def _attend(query: torch.Tensor, seqs: Sequence[Sequence[_Segment]], Hkv: int, k
                            softcap, causal)
 
 
-# fp32 copies of additive masks given in another dtype or on another device,
-# one per mask object: HELM's pipeline builds one decode mask per step in the
-# model's dtype (pipeline_runtime.py:79-92) and hands that object to every
-# layer, so it is converted once per step, not once per layer.  An entry is
-# dropped when its mask is freed; it is used only while the mask's address,
+# fp32 copies of additive masks that a kernel cannot read as given (a mask on
+# another device, or a CPU query's 16-bit mask: the host-CPU kernel reads
+# fp32), one per mask object: HELM's pipeline builds one decode mask per step
+# in the model's dtype (pipeline_runtime.py:79-92) and hands that object to
+# every layer, so it is converted once per step, not once per layer.  An entry
+# is dropped when its mask is freed; it is used only while the mask's address,
 # shape, strides, dtype, version counter and the target device are unchanged.
-# (A prompt chunk's padded mask, which is not recognised as causal, is also
-# handed to every layer of the chunk's forward.)  The copies kept at once are
-# bounded; past the bound a mask converts per call.
+# A tensor made under torch.inference_mode() has no version counter (HELM's
+# generate runs there, inference.py:747): an in-place change to it cannot be
+# seen, so such a mask is converted on every call.  The copies kept at once
+# are bounded; past the bound a mask converts per call.
 _F32_MASKS: dict = {}
 _F32_MASK_MAX_ELEMS = 1 << 26      # one mask
 _F32_MASK_MAX_TOTAL = 1 << 28      # all copies kept (elements, 1 GiB of fp32)
 
 
 def _mask_fp32(m: torch.Tensor, device: torch.device) -> torch.Tensor:
-    if m.numel() > _F32_MASK_MAX_ELEMS:
+    if m.numel() > _F32_MASK_MAX_ELEMS or m.is_inference():
         return m.to(device=device, dtype=torch.float32)
     key = id(m)
     sig = (m.data_ptr(), tuple(m.shape), tuple(m.stride()), m.dtype, m._version, device)
@@ -972,10 +974,16 @@ def _mask_fp32(m: torch.Tensor, device: torch.device) -> torch.Tensor:
     return f
 
 
+# mask element types the GPU kernels read as given (HELM_F32 / BF16 / F16)
+_MASK_NATIVE = (torch.float32, torch.bfloat16, torch.float16)
+
+
 def _query_and_mask(query: torch.Tensor, Hkv: int, kv_dtype, t_max: int,
-                    attention_mask: Optional[torch.Tensor]):
+                    attention_mask: Optional[torch.Tensor], gpu: bool = True):
     """The query in a kernel dtype, its output buffer and the mask arguments
-    (pointer, batch / head / row strides) of one attention call."""
+    (pointer, batch / head / row strides, and for a GPU call the element type)
+    of one attention call.  A GPU call reads a mask on the query's device in
+    fp32, bf16 or fp16 as given; the host-CPU kernel reads fp32."""
     device = query.device
     B, Hq, S, D = query.shape
     if Hq % Hkv != 0:
@@ -987,10 +995,12 @@ def _query_and_mask(query: torch.Tensor, Hkv: int, kv_dtype, t_max: int,
         q = q.contiguous()
     out = torch.empty_like(q)
     mask_ptr, mbs, mhs, mqs = None, 0, 0, 0
+    mdt = _native.HELM_F32
     m = None
     if attention_mask is not None:
         m = attention_mask
-        if m.dtype != torch.float32 or m.device != device:
+        if m.device != device or (m.dtype != torch.float32 and
+                                  (not gpu or m.dtype not in _MASK_NATIVE)):
             m = _mask_fp32(m, device)
         if m.dim() != 4:
             raise ValueError("attention_mask must be 4-D [B, H, q_len, kv_len]")
@@ -1008,7 +1018,9 @@ def _query_and_mask(query: torch.Tensor, Hkv: int, kv_dtype, t_max: int,
         mbs = m.stride(0) if Bm > 1 else 0
         mhs = m.stride(1) if Hm > 1 else 0
         mqs = m.stride(2) if Sm > 1 else 0
-    return q, out, (mask_ptr, mbs, mhs, mqs), m
+        mdt = _native.dtype_code(m.dtype)
+    margs = (mask_ptr, mbs, mhs, mqs, mdt) if gpu else (mask_ptr, mbs, mhs, mqs)
+    return q, out, margs, m
 
 
 def _attend_records(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarray, t_max: int,
@@ -1039,7 +1051,8 @@ def _attend_records_cpu(query: torch.Tensor, arr: np.ndarray, seq_off: np.ndarra
     call (libhelm_cpu.so) over records whose pages are in host memory, on
     torch's intra-op thread count."""
     B, Hq, S, D = query.shape
-    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, t_max, attention_mask)
+    q, out, margs, _keep = _query_and_mask(query, Hkv, kv_dtype, t_max, attention_mask,
+                                           gpu=False)
     n = int(seq_off[B])
     _cpu_native.call("helm_cpu_stream_attn", q.data_ptr(), out.data_ptr(), B, Hq, Hkv, S, D,
                      _native.ptr(arr) if n else None, _native.ptr(seq_off), float(scale),

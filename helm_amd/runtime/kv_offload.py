@@ -480,18 +480,24 @@ def _causal_mask_offset(mask: Optional[torch.Tensor], S: int) -> Optional[int]:
     layer), so the check runs once per forward and chunk.  The entry holds a
     weak reference: a later mask that reuses a freed mask's memory (same
     address, shape and a fresh version counter) is a different object and is
-    checked anew."""
+    checked anew.  A mask made under torch.inference_mode() (HELM's generate,
+    inference.py:747) has no version counter, so an in-place change to it
+    cannot be seen: it is checked on every call."""
     if (mask is None or S < 2 or mask.dim() != 4 or mask.shape[-2] != S
             or mask.shape[-1] < S
             or mask.dtype not in (torch.float32, torch.bfloat16, torch.float16)):
         return None
     T = mask.shape[-1]
-    sig = (mask.data_ptr(), tuple(mask.shape), tuple(mask.stride()), mask.dtype, mask._version)
-    ent = _CAUSAL_MASKS.get(id(mask))
+    inference = mask.is_inference()
+    sig = None if inference else (mask.data_ptr(), tuple(mask.shape), tuple(mask.stride()),
+                                  mask.dtype, mask._version)
+    ent = None if inference else _CAUSAL_MASKS.get(id(mask))
     if ent is not None and ent[0]() is mask and ent[1] == sig:
         return ent[2]
     upper = torch.ones(S, T, dtype=torch.bool, device=mask.device).triu_(1 + T - S)
     past = T - S if bool(torch.where(upper, mask <= -1e4, mask == 0).all()) else None
+    if inference:
+        return past
     if len(_CAUSAL_MASKS) > 64:
         _CAUSAL_MASKS.clear()
     _CAUSAL_MASKS[id(mask)] = (weakref.ref(mask), sig, past)

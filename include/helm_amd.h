@@ -21,8 +21,13 @@
  *                    HELM's KVPage.k_tensor / v_tensor hold.  head_stride is the
  *                    element distance between consecutive KV heads of a page
  *                    (= page capacity * D for a dense page).
- *   mask             additive fp32, element (b, h, s, t) at
- *                    mask + b*mask_bstride + h*mask_hstride + s*mask_qstride + t
+ *   mask             additive, of element type mask_dtype (HELM_F32, HELM_BF16
+ *                    or HELM_F16: HELM's pipeline builds its masks in the
+ *                    model's dtype and widens them to fp32 before adding,
+ *                    helm/runtime/kv_cache.py:519, :535; a 16-bit element
+ *                    widens exactly, so it is read as given), element
+ *                    (b, h, s, t) at element index
+ *                    b*mask_bstride + h*mask_hstride + s*mask_qstride + t
  *                    where t is the position of the key among the sequence's
  *                    active tokens (HELM's token_cursor).
  *
@@ -38,7 +43,7 @@
 extern "C" {
 #endif
 
-#define HELM_AMD_ABI_VERSION 1
+#define HELM_AMD_ABI_VERSION 2
 
 enum helm_dtype { HELM_F16 = 0, HELM_BF16 = 1, HELM_F32 = 2 };
 
@@ -130,8 +135,8 @@ int helm_paged_decode_attn(const void* q, void* out,
                            int B, int Hq, int Hkv, int q_len, int D,
                            int page_size, int max_pages, int total_pages,
                            float scale, float softcap,
-                           const float* mask, int64_t mask_bstride,
-                           int64_t mask_hstride, int64_t mask_qstride,
+                           const void* mask, int64_t mask_bstride,
+                           int64_t mask_hstride, int64_t mask_qstride, int mask_dtype,
                            int kv_dtype, int q_dtype, int pages_per_split,
                            void* workspace, size_t ws_bytes, void* stream);
 
@@ -157,8 +162,8 @@ int helm_paged_decode_attn_static(const void* q, void* out,
                                   int B, int Hq, int Hkv, int q_len, int D,
                                   int page_size, int max_pages, int total_pages,
                                   float scale, float softcap,
-                                  const float* mask, int64_t mask_bstride,
-                                  int64_t mask_hstride, int64_t mask_qstride,
+                                  const void* mask, int64_t mask_bstride,
+                                  int64_t mask_hstride, int64_t mask_qstride, int mask_dtype,
                                   int kv_dtype, int q_dtype, int pages_per_split,
                                   void* stream);
 
@@ -190,8 +195,8 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out,
                      int B, int Hq, int Hkv, int q_len, int D,
                      const helm_page* pages, const int32_t* seq_off,
                      float scale, float softcap,
-                     const float* mask, int64_t mask_bstride,
-                     int64_t mask_hstride, int64_t mask_qstride, int causal,
+                     const void* mask, int64_t mask_bstride,
+                     int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int causal,
                      int kv_dtype, int q_dtype, void* stream);
 
 /* Decode / chunk attention over page records that already sit in device
@@ -216,8 +221,8 @@ int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
                          const uint64_t* seq_pages, const int32_t* seq_npages,
                          const int32_t* seq_tokens, int page_tokens,
                          int aligned16, float scale, float softcap,
-                         const float* mask, int64_t mask_bstride,
-                         int64_t mask_hstride, int64_t mask_qstride, int causal,
+                         const void* mask, int64_t mask_bstride,
+                         int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int causal,
                          int kv_dtype, int q_dtype, void* stream);
 
 /* One decode step of _decode_batched (helm/runtime/kv_offload.py:145-174):
@@ -238,8 +243,8 @@ int helm_paged_attn_seqs_append(helm_engine* eng, const void* q, void* out, int 
                                 int Hq, int Hkv, int D, const uint64_t* seq_pages,
                                 const int32_t* seq_npages, const int32_t* seq_tokens,
                                 int page_tokens, int aligned16, float scale, float softcap,
-                                const float* mask, int64_t mask_bstride,
-                                int64_t mask_hstride, int64_t mask_qstride, int kv_dtype,
+                                const void* mask, int64_t mask_bstride,
+                                int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int kv_dtype,
                                 const helm_append_seg* tokens, void* stream);
 
 /* Copies `bytes` from host memory `src` to device memory `dst` in the order

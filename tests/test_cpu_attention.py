@@ -18,6 +18,7 @@ import torch
 from helm_amd import _cpu_native, _native
 from helm_amd import workloads as W
 from helm_amd.runtime import kv_cache as KC
+from helm_amd.runtime import kv_offload as KO
 from helm_amd.runtime.kv_allocator import KVAllocator
 from helm_amd.runtime.kv_cache import KVCacheManager, perform_streaming_attention
 from oracle import attention as A
@@ -332,6 +333,50 @@ def test_perform_streaming_attention_cpu_paths(dtype):
     KC.reset_paging_stats()
     perform_streaming_attention(q, pages, attention_mask=mask)
     assert KC.get_paging_stats()["prefetch_calls"] == 0
+
+
+@pytest.mark.parametrize("mdtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_masks_made_under_inference_mode(mdtype):
+    """HELM's generate runs under torch.inference_mode() (inference.py:747) and
+    builds its masks there in the model's dtype (pipeline_runtime.py:79-113):
+    such tensors have no version counter.  A CPU query under such a mask (decode
+    mask and a prompt chunk's causal mask) gives what the same mask made outside
+    inference mode gives, and an in-place change to the mask between calls is
+    seen by the next call."""
+    g = torch.Generator().manual_seed(7)
+    Hq, Hkv, D, T = 4, 2, 32, 96
+    K = torch.randn(1, Hkv, T, D, generator=g)
+    V = torch.randn(1, Hkv, T, D, generator=g)
+    q = torch.randn(1, Hq, 1, D, generator=g)
+    mgr = _mgr(Hkv, D, torch.float32)
+    mgr.append_prefill(0, K, V)
+    pages = mgr.iterate_layer_pages(0)
+    lo = torch.finfo(mdtype).min
+    plain = torch.zeros(1, 1, 1, T, dtype=mdtype)
+    plain[..., 5:40] = lo
+    want = perform_streaming_attention(q, pages, attention_mask=plain)
+    with torch.inference_mode():
+        m = torch.zeros(1, 1, 1, T, dtype=mdtype)
+        m[..., 5:40] = lo
+        assert m.is_inference()
+        got = perform_streaming_attention(q, pages, attention_mask=m)
+        assert torch.equal(got, want)
+        assert torch.equal(KC._mask_fp32(m, torch.device("cpu")), m.float())
+        m[..., 5:40] = 0          # in place: the next call sees it
+        got2 = perform_streaming_attention(q, pages, attention_mask=m)
+    assert torch.equal(got2, perform_streaming_attention(q, pages))
+    assert not torch.equal(got2, got)
+    # a prompt chunk's mask (HELM's _build_chunk_prefill_mask): recognised as
+    # causal, and a change in place is seen
+    S, past = 6, 10
+    with torch.inference_mode():
+        cm = torch.full((S, past + S), lo, dtype=mdtype).triu_(1 + past)[None, None]
+        assert KO._causal_mask_offset(cm, S) == past
+        assert KO._causal_mask_offset(cm, S) == past
+        cm[..., 0, 0] = lo
+        assert KO._causal_mask_offset(cm, S) is None
+        cm[..., 0, 0] = 0
+        assert KO._causal_mask_offset(cm, S) == past
 
 
 def test_cpu_query_edge_cases():

@@ -207,9 +207,13 @@ def test_patch_cpu_linears():
     lin0, w0 = m[0], m[0].weight
     keys = list(m.state_dict())
     assert kernels.patch_cpu_linears(m) == 2
-    assert m[0] is lin0 and type(m[0]) is nn.Linear and m[0].weight is w0
+    assert m[0] is lin0 and isinstance(m[0], nn.Linear) and m[0].weight is w0
+    assert type(m[0]) is kernels.NativeLinear and type(m[2][1]) is nn.Linear
     assert list(m.state_dict()) == keys
     assert kernels.patch_cpu_linears(m) == 0
+    # HELM walks the children only: a bare linear passed in is not patched
+    bare = nn.Linear(8, 4).half()
+    assert kernels.patch_cpu_linears(bare) == 0 and type(bare) is nn.Linear
     x = torch.randn(1, 1, 64, dtype=torch.float16)
     y = m[0](x)
     assert torch.equal(y.reshape(-1), kernels.gemv_fp16(x, m[0].weight, m[0].bias).reshape(-1))
@@ -218,6 +222,26 @@ def test_patch_cpu_linears():
     assert torch.equal(m[2][1](xf), F.linear(xf, m[2][1].weight, m[2][1].bias))
     xp = torch.randn(2, 9, 64, dtype=torch.float16)
     assert torch.equal(m[0](xp), F.linear(xp.float(), w0.float(), m[0].bias.float()).half())
+
+
+@needs_kernel
+def test_patched_model_saves_and_loads(tmp_path):
+    """A patched model goes through torch.save / torch.load (whole module and
+    state_dict) and gives the same decode outputs afterwards."""
+    torch.manual_seed(6)
+    m = nn.Sequential(nn.Linear(64, 32), nn.ReLU(), nn.Linear(32, 16)).half()
+    assert kernels.patch_cpu_linears(m) == 2
+    x = torch.randn(1, 64, dtype=torch.float16)
+    y = m(x)
+    torch.save(m, tmp_path / "m.pt")
+    torch.save(m.state_dict(), tmp_path / "sd.pt")
+    m2 = torch.load(tmp_path / "m.pt", weights_only=False)
+    assert type(m2[0]) is kernels.NativeLinear
+    assert torch.equal(m2(x), y)
+    m3 = nn.Sequential(nn.Linear(64, 32), nn.ReLU(), nn.Linear(32, 16)).half()
+    m3.load_state_dict(torch.load(tmp_path / "sd.pt", weights_only=True))
+    assert kernels.patch_cpu_linears(m3) == 2
+    assert torch.equal(m3(x), y)
 
 
 def test_fp16_linear_empty_input_takes_the_float32_branch():

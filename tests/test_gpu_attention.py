@@ -486,3 +486,35 @@ def test_static_decode_replays_from_a_hip_graph(T):
         assert torch.equal(out, eager), f"replay {i} differs from the eager call"
         x = (x @ x).clamp_(-1, 1)            # eager work between the replays
         torch.cuda.synchronize()
+
+
+# ── the committed golden fixtures through the HIP path ───────────────────────
+def _golden_cases():
+    import os
+    d = os.path.join(os.path.dirname(__file__), "golden")
+    return sorted(f[:-4] for f in os.listdir(d) if f.endswith(".npz"))
+
+
+@pytest.mark.parametrize("name", _golden_cases())
+def test_golden_fixtures_on_the_gpu(name, kernel):
+    """Each fixture of tests/golden/ (seeded inputs in the page sizes it
+    lists and their float64 output) through perform_streaming_attention on
+    the GPU, within the fixture's tolerance; every kernel and merge choice."""
+    import json
+    import os
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", f"{name}.npz"))
+    meta = json.loads(str(z["meta"]))
+    dtype = getattr(torch, meta["dtype"])
+    q = torch.from_numpy(z["q"]).to(dtype)
+    K = torch.from_numpy(z["K"]).to(dtype)
+    V = torch.from_numpy(z["V"]).to(dtype)
+    pages, t = [], 0
+    for i, n in enumerate(meta["page_sizes"]):
+        pages.append(_page(K[:, :, t:t + n].to(DEV), V[:, :, t:t + n].to(DEV), i, t))
+        t += n
+    mask = torch.from_numpy(z["mask"]).to(DEV) if "mask" in z.files else None
+    out = perform_streaming_attention(q.to(DEV), pages, scale=meta["scale"],
+                                      attention_mask=mask, softcap=meta["softcap"])
+    torch.cuda.synchronize()
+    err = (out.double().cpu() - torch.from_numpy(z["out"])).abs().max().item()
+    assert err <= meta["atol"], err

@@ -249,7 +249,7 @@ def test_staging_ring_reuse_many_chunks(host_read, stage_stream):
             out = torch.empty_like(q)
             _native.call("helm_stream_attn", eng, q.data_ptr(), out.data_ptr(), 1, 32, 8, 1, 128,
                          _native.ptr(pages), _native.ptr(seq_off), 1 / math.sqrt(128), 0.0, None,
-                         0, 0, 0, 0, _native.HELM_BF16, _native.HELM_BF16,
+                         0, 0, 0, _native.HELM_F32, 0, _native.HELM_BF16, _native.HELM_BF16,
                          torch.cuda.current_stream().cuda_stream)
             outs.append(out)
         torch.cuda.synchronize()
@@ -306,7 +306,7 @@ def test_staged_copies_follow_callers_host_writes(stage_stream, chunk_mb, slots,
             out = torch.empty_like(q)
             _native.call("helm_stream_attn", eng, q.data_ptr(), out.data_ptr(), 1, 32, 8, 1, 128,
                          _native.ptr(pages), _native.ptr(seq_off), 1 / math.sqrt(128), 0.0,
-                         None, 0, 0, 0, 0, _native.HELM_BF16, _native.HELM_BF16,
+                         None, 0, 0, 0, _native.HELM_F32, 0, _native.HELM_BF16, _native.HELM_BF16,
                          torch.cuda.current_stream().cuda_stream)
             torch.cuda.synchronize()
             outs.append(out.cpu())
@@ -364,7 +364,7 @@ def test_host_pages_in_place_and_mixed_host_memory(host_read):
         out = torch.empty_like(qd)
         _native.call("helm_stream_attn", eng, qd.data_ptr(), out.data_ptr(), B, Hq, Hkv, 1, D,
                      _native.ptr(arr), _native.ptr(off), 1 / math.sqrt(D), 0.0, None, 0, 0, 0,
-                     0, _native.HELM_BF16, _native.HELM_BF16, stream)
+                     _native.HELM_F32, 0, _native.HELM_BF16, _native.HELM_BF16, stream)
         return out
 
     qd = q.to(DEV)
@@ -404,7 +404,7 @@ def test_large_contiguous_host_runs(host_read):
     off = np.array([0, len(rec)], dtype=np.int32)
     _native.call("helm_stream_attn", engine.get_engine(DEV), qd.data_ptr(), out.data_ptr(), 1,
                  Hq, Hkv, 1, D, _native.ptr(rec), _native.ptr(off), 1 / math.sqrt(D), 0.0, None,
-                 0, 0, 0, 0, _native.HELM_BF16, _native.HELM_BF16,
+                 0, 0, 0, _native.HELM_F32, 0, _native.HELM_BF16, _native.HELM_BF16,
                  torch.cuda.current_stream().cuda_stream)
     K = torch.cat([host[:, 0].permute(1, 0, 2, 3).reshape(Hkv, -1, D).float(),
                    devp[perm, 0].permute(1, 0, 2, 3).reshape(Hkv, -1, D).cpu().float()], 1)

@@ -55,6 +55,53 @@ def test_masks_softcap_match_fp64():
     np.testing.assert_allclose(got.double().numpy(), ref, atol=1e-5)
 
 
+@pytest.mark.parametrize("scale", [1.0, 0.5])
+def test_softcap_two_keys_known_answer(scale):
+    """Soft-cap pinned by hand: with one-dimensional q = 1 and keys k_i, the
+    logits are x_i = cap * tanh(k_i * scale / cap) (HELM scales first, then
+    caps: kv_cache.py:516-517, :532-533), the weights are exp(x_i) / sum, and
+    the output is their mean of the values.  A cap applied before the scale,
+    a missing tanh or a cap applied to the weights gives another number."""
+    cap = 2.0
+    k = [3.0, -1.5]
+    v = [10.0, -4.0]
+    x = [cap * math.tanh(ki * scale / cap) for ki in k]
+    w = [math.exp(xi) for xi in x]
+    want = (w[0] * v[0] + w[1] * v[1]) / (w[0] + w[1])
+    q = torch.ones(1, 1, 1, 1)
+    K = torch.tensor(k).view(1, 1, 2, 1)
+    V = torch.tensor(v).view(1, 1, 2, 1)
+    got64 = A.attention_fp64(q, K, V, scale=scale, softcap=cap)[0, 0, 0, 0]
+    assert abs(got64 - want) <= 1e-12
+    for pages in ([(K, V)], [(K[:, :, :1], V[:, :, :1]), (K[:, :, 1:], V[:, :, 1:])]):
+        got = A.online_softmax_pages(q, pages, scale=scale, softcap=cap)[0, 0, 0, 0].item()
+        assert abs(got - want) <= 1e-5
+        got = A.streaming_attention(q, pages, scale=scale, softcap=cap)[0, 0, 0, 0].item()
+        assert abs(got - want) <= 1e-5
+    # the wrong orders give numbers far from it
+    x_wrong = [cap * math.tanh(ki / cap) * scale for ki in k]
+    w_wrong = [math.exp(xi) for xi in x_wrong]
+    wrong = (w_wrong[0] * v[0] + w_wrong[1] * v[1]) / sum(w_wrong)
+    if scale != 1.0:
+        assert abs(wrong - want) > 1e-3
+
+
+def test_softcap_large_cap_is_uncapped_sdpa():
+    """cap * tanh(x / cap) -> x as cap grows: at cap = 1e6 the capped formula
+    equals float64 SDPA without a cap (logits of order 10: the cap changes
+    them by ~x^3 / (3 cap^2) < 1e-9)."""
+    q, pages, K, V = _pages([16, 16, 5], 8, 32, seed=17, kv_heads=4)
+    q = q * 3
+    Ke = K.repeat_interleave(2, dim=1).double()
+    Ve = V.repeat_interleave(2, dim=1).double()
+    sdpa = F.scaled_dot_product_attention(q.double(), Ke, Ve).numpy()
+    np.testing.assert_allclose(A.attention_fp64(q, K, V, softcap=1e6), sdpa, atol=1e-9)
+    got = A.online_softmax_pages(q, pages, softcap=1e6)
+    np.testing.assert_allclose(got.double().numpy(), sdpa, atol=1e-5)
+    # and a small cap moves the answer (the branch is not a no-op)
+    assert np.abs(A.attention_fp64(q, K, V, softcap=1.0) - sdpa).max() > 1e-2
+
+
 def test_fp16_within_helm_tolerance():
     # HELM: fp16 accumulates in fp32, atol 2e-3 (test_streaming_attention.py:353-365)
     q, pages, K, V = _pages([16] * 8, 16, 128, seed=5, kv_heads=8, dtype=torch.float16)
