@@ -94,6 +94,9 @@ def parse():
                     help="skip the _decode_batched production-call leg")
     ap.add_argument("--all", action="store_true",
                     help="also measure every benchmark configuration (one line each on stderr)")
+    ap.add_argument("--stamps", action="store_true",
+                    help="also record per-workgroup start / page-loop-end / end times of the "
+                         "headline decode kernel (helm_profile_workgroup_stamps)")
     ap.add_argument("--all-json", default=None, metavar="PATH",
                     help="with --all, also write the configurations' rows to PATH as JSON")
     return ap.parse_args()
@@ -173,6 +176,67 @@ def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=Non
         "per_call_s": per_call_s, "wall_ms_per_step": wall * 1e3 / steps,
         "host_issue_us_per_call": (t_issued - t0) * 1e6 / steps,
         "ms_per_step": ms_events / steps, "pools": n_pools, "lens": lens, "prep": prep,
+        "step": step,
+    }
+
+
+def workgroup_stamps(torch, h, captures=5, run=40):
+    """Per-workgroup timing of the decode kernel (helm_profile_workgroup_stamps):
+    in each of `captures` runs of `run` back-to-back calls, the middle call's
+    workgroups record the s_memrealtime counter (100 MHz) at their start,
+    after their page loop and at their end, with their XCD and CU.  Returns
+    the spread of those times (us from the kernel's first workgroup start)
+    and their means per XCD and per KV head."""
+    from helm_amd import _native
+    step = h["step"]
+    nwg = 1 << 16
+    buf = torch.zeros(nwg * 4, dtype=torch.int64, device="cuda")
+    caps = []
+    for c in range(captures):
+        for i in range(run // 2):
+            step(i)
+        _native.call("helm_profile_workgroup_stamps", buf.data_ptr(), nwg)
+        for i in range(run // 2, run):
+            step(i)
+        torch.cuda.synchronize()
+        _native.call("helm_profile_workgroup_stamps", None, 0)
+        a = buf.view(-1, 4).cpu().numpy().astype(np.uint64)
+        used = a[:, 0] > 0
+        a = a[used]
+        buf.zero_()
+        t0 = a[:, 0].min()
+        rel = (a[:, :3] - t0).astype(np.float64) / 100.0           # 100 MHz -> us
+        xcd = (a[:, 3] >> np.uint64(32)).astype(np.int64)
+        hw = (a[:, 3] & np.uint64(0xffffffff)).astype(np.int64)
+        caps.append((rel, xcd, hw))
+    rel, xcd, hw = caps[-1]
+    n = len(rel)
+    splits = n // max(1, h["w"].Hkv)
+    head = np.arange(n) // splits                               # grid (split, head)
+    loop = np.stack([c[0][:, 1] for c in caps])                 # [captures, wg]
+    end = np.stack([c[0][:, 2] for c in caps])
+    start = np.stack([c[0][:, 0] for c in caps])
+
+    def stats(x):
+        return {"min": round(float(x.min()), 2), "mean": round(float(x.mean()), 2),
+                "max": round(float(x.max()), 2), "std": round(float(x.std()), 2)}
+
+    # does a workgroup's lateness repeat from call to call (a slow place) or not
+    lo = loop - loop.mean(axis=1, keepdims=True)
+    repeat = float(np.corrcoef(lo[:-1].ravel(), lo[1:].ravel())[0, 1]) if captures > 1 else None
+    return {
+        "workgroups": n, "captures": captures,
+        "start_us": stats(start), "loop_end_us": stats(loop), "end_us": stats(end),
+        "loop_end_spread_us_per_capture": [round(float(r.max() - r.min()), 2) for r in loop],
+        "last_end_us_per_capture": [round(float(r.max()), 2) for r in end],
+        "loop_end_mean_per_xcd_us": {int(x): round(float(loop[-1][xcd == x].mean()), 2)
+                                     for x in sorted(set(xcd.tolist()))},
+        "loop_end_mean_per_kv_head_us": {int(k): round(float(loop[-1][head == k].mean()), 2)
+                                         for k in sorted(set(head.tolist()))},
+        "lateness_correlation_between_calls": None if repeat is None else round(repeat, 3),
+        "how": "helm_profile_workgroup_stamps: s_memrealtime (100 MHz) at each workgroup's "
+               "start, after its page loop (all waves), and at its end, relative to the "
+               f"first start; middle call of {run} back-to-back calls, {captures} captures",
     }
 
 
@@ -934,6 +998,11 @@ def main():
     log(f"per call {h['per_call_s'] * 1e6:.2f} us, {value:.1f} GB/s; decode kernel "
         f"{kern_us:.2f} us, {kern_gbs:.1f} GB/s")
 
+    stamps = None
+    if args.stamps:
+        stamps = workgroup_stamps(torch, h)
+        log("workgroup stamps: " + json.dumps(stamps))
+
     if args.copy_calibration:
         n = 1 << 30
         a = torch.empty(n, dtype=torch.uint8, device="cuda")
@@ -1069,6 +1138,7 @@ def main():
                      "rocprof_kernel_us": prof,
                      "host_issue_us_per_call": round(h["host_issue_us_per_call"], 2)},
         "decode_masked_32k": masked_c2,
+        "workgroup_stamps": stamps,
         "configs": configs,
         "runtime_decode_32k": runtime,
         "c1_cpu_path": c1_cpu,

@@ -87,6 +87,7 @@ SIGNATURES = {
         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
     "helm_profile_split_kernels": (ctypes.c_int, [ctypes.c_int]),
     "helm_profile_split_read": (ctypes.c_int, [_c_void_p, ctypes.c_int]),
+    "helm_profile_workgroup_stamps": (ctypes.c_int, [_c_void_p, ctypes.c_int]),
     "helm_measure_bandwidth": (ctypes.c_int, [ctypes.c_int, _u64, _u64, ctypes.c_int,
                                               _c_void_p]),
     "helm_evict_pages": (ctypes.c_int, [_c_void_p, ctypes.c_int, _c_void_p, _c_void_p,

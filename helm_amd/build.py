@@ -38,6 +38,11 @@ HIPCC_FLAGS = [
     # MFMA accumulators in ordinary VGPRs: the decode kernel rescales them
     # with vector ALU ops, which cannot address AGPRs
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # atomics as written: the decode kernel's block claims are issued by one
+    # lane and their results read a step later; the atomic optimizer would
+    # broadcast each result right after the atomic, a wait on every load
+    # in flight
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
 
 

@@ -53,13 +53,15 @@ hipError_t launch_generic(const LaunchSpec& s, hipStream_t st) {
 // Matrix-core kernels: D = 128, q and KV of the same 16-bit type.
 template <typename T, class Src, int FEAT>
 hipError_t launch_mfma_feat(const LaunchSpec& s, const Src& src, hipStream_t st) {
+  // the chunk kernels read a mask's element type at run time
+  constexpr int CF = FEAT & ~kFeatMask16;
   if (s.p.row_waves == 2) {
     if (s.nw == 8)
-      HELM_ATTN_LAUNCH((chunk32_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), s.p, src);
+      HELM_ATTN_LAUNCH((chunk32_mfma_kernel<T, Src, CF, 8>), s.grid, dim3(512), s.p, src);
     else
-      HELM_ATTN_LAUNCH((chunk32_mfma_kernel<T, Src, FEAT, 4>), s.grid, dim3(256), s.p, src);
+      HELM_ATTN_LAUNCH((chunk32_mfma_kernel<T, Src, CF, 4>), s.grid, dim3(256), s.p, src);
   } else if (s.p.row_waves)
-    HELM_ATTN_LAUNCH((chunk_mfma_kernel<T, Src, FEAT>), s.grid, dim3(256), s.p, src);
+    HELM_ATTN_LAUNCH((chunk_mfma_kernel<T, Src, CF>), s.grid, dim3(256), s.p, src);
   else if (s.nw == 8)
     HELM_ATTN_LAUNCH((decode_mfma_kernel<T, Src, FEAT, 8>), s.grid, dim3(512), s.p, src);
   else
@@ -78,6 +80,10 @@ hipError_t launch_mfma_src(const LaunchSpec& s, const Src& src, hipStream_t st) 
     case 5: return launch_mfma_feat<T, Src, 5>(s, src, st);
     case 6: return launch_mfma_feat<T, Src, 6>(s, src, st);
     case 7: return launch_mfma_feat<T, Src, 7>(s, src, st);
+    case 9: return launch_mfma_feat<T, Src, 9>(s, src, st);
+    case 11: return launch_mfma_feat<T, Src, 11>(s, src, st);
+    case 13: return launch_mfma_feat<T, Src, 13>(s, src, st);
+    case 15: return launch_mfma_feat<T, Src, 15>(s, src, st);
     default: return hipErrorInvalidValue;
   }
 }

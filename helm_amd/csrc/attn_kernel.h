@@ -329,6 +329,34 @@ struct PoolSrc {
     const int T = sload(seq_lens + b);
     return T > 0 ? min((T + page_size - 1) / page_size, max_pages) : 0;
   }
+  // Dynamic claiming (decode kernel): a sequence's loop-invariant part, a
+  // page's record (its slot) fetched a step ahead, and the page's view
+  struct Ctx {
+    const int32_t* row;  // the sequence's page-table row
+    int T;               // its tokens
+  };
+  __device__ __forceinline__ Ctx ctx(int b) const {
+    return Ctx{table + (int64_t)b * table_stride, sload(seq_lens + b)};
+  }
+  struct Raw {
+    int slot;
+  };
+  __device__ __forceinline__ Raw raw(const Ctx& c, int p) const { return Raw{sload(c.row + p)}; }
+  // the record as loaded, read where it is used: the compiler then does not
+  // start computing with it (and wait for its load) where it is fetched
+  __device__ __forceinline__ static void pin(Raw& r) {
+    r.slot = __builtin_amdgcn_readfirstlane(r.slot);
+  }
+  __device__ __forceinline__ PageView view(const Ctx& c, const Raw& r, int p, int hk) const {
+    PageView pv;
+    const int64_t off = (int64_t)r.slot * slot_stride_b + hk * head_stride_b;
+    pv.k = k_pool + off;
+    pv.v = v_pool + off;
+    pv.tok_off = p * page_size;
+    pv.used = min(page_size, c.T - pv.tok_off);
+    pv.head_stride_b = 0;
+    return pv;
+  }
   __device__ __forceinline__ PageView page(int b, int p, int hk) const {
     const int slot = sload(table + (int64_t)b * table_stride + p);
     const int T = sload(seq_lens + b);
@@ -382,6 +410,35 @@ struct DescSrc {
   __device__ __forceinline__ int used_of(const helm_page& d, int b) const {
     return by_value ? min(d.used, seq_tokens[b] - d.tok_off) : d.used;
   }
+  // Dynamic claiming (decode kernel): as PoolSrc's
+  struct Ctx {
+    const helm_page* base;  // the sequence's records
+    int tokens;             // its tokens (by_value; else no cap)
+  };
+  __device__ __forceinline__ Ctx ctx(int b) const {
+    return Ctx{base(b), by_value ? seq_tokens[b] : 0x7fffffff};
+  }
+  struct Raw {
+    helm_page d;
+  };
+  __device__ __forceinline__ Raw raw(const Ctx& c, int p) const { return Raw{sload(c.base + p)}; }
+  __device__ __forceinline__ static void pin(Raw& r) {
+    r.d.k = uniform64(r.d.k);
+    r.d.v = uniform64(r.d.v);
+    r.d.used = __builtin_amdgcn_readfirstlane(r.d.used);
+    r.d.tok_off = __builtin_amdgcn_readfirstlane(r.d.tok_off);
+    r.d.head_stride = __builtin_amdgcn_readfirstlane(r.d.head_stride);
+  }
+  __device__ __forceinline__ PageView view(const Ctx& c, const Raw& r, int, int hk) const {
+    PageView pv;
+    const int64_t off = (int64_t)hk * r.d.head_stride * elem_bytes;
+    pv.k = reinterpret_cast<const char*>(r.d.k) + off;
+    pv.v = reinterpret_cast<const char*>(r.d.v) + off;
+    pv.used = min(r.d.used, c.tokens - r.d.tok_off);
+    pv.tok_off = r.d.tok_off;
+    pv.head_stride_b = 0;
+    return pv;
+  }
   __device__ __forceinline__ PageView page(int b, int p, int hk) const {
     const helm_page d = sload(base(b) + p);
     PageView pv;
@@ -424,7 +481,34 @@ struct AttnParams {
   int row_waves;      // query chunks: 16-row tiles per wave (1 or 2; 0: decode kernel)
   int direct_out;     // 1: the call has one split; the chunk kernel writes the output
   int bpp_log2;       // log2 of bpp when bpp is a power of two, else -1
+  // profiling (helm_profile_workgroup_stamps): per workgroup of the decode
+  // kernel {start, page loop end, end, XCD << 32 | HW_ID}; null: off
+  uint64_t* stamps;
+  // dynamic block claiming (decode kernel): one counter per tile at
+  // claims[tile * kClaimStride], zero before the call, zeroed again by the
+  // tile's merge (merge kernel, or the last split in fused mode)
+  int dyn;
+  uint32_t* claims;
 };
+
+// Counter spacing of the dynamic block claims (128 bytes: one tile's
+// counter per line).
+constexpr int kClaimStride = 32;
+
+// Zeroes tile's claim counter once its merge runs (every claim is done).
+__device__ __forceinline__ void reset_claims(const AttnParams& p, int tile) {
+  if (p.claims) p.claims[(int64_t)tile * kClaimStride] = 0u;
+}
+
+// The s_memrealtime counter (100 MHz) and the workgroup's XCD and HW_ID
+// (CU, SIMD, shader engine) for the profiling stamps.
+__device__ __forceinline__ uint64_t stamp_now() { return __builtin_amdgcn_s_memrealtime(); }
+__device__ __forceinline__ uint64_t stamp_place() {
+  uint32_t xcc, hw;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+  return ((uint64_t)xcc << 32) | hw;
+}
 
 // One row of the additive mask, in the element type the caller built it in
 // (HELM's pipeline builds its masks in the model's dtype and adds them to the
@@ -443,6 +527,19 @@ struct MaskRow {
   }
   __device__ __forceinline__ MaskRow operator+(int64_t i) const {
     return MaskRow{base + i * (dt == HELM_F32 ? 4 : 2), dt};
+  }
+  // element i's bits, for an element type known at compile time (K16: a
+  // 16-bit mask, zero-extended); widened where the value is used
+  template <bool K16>
+  __device__ __forceinline__ uint32_t bits(int64_t i) const {
+    if constexpr (K16) return reinterpret_cast<const uint16_t*>(base)[i];
+    return reinterpret_cast<const uint32_t*>(base)[i];
+  }
+  template <bool K16>
+  __device__ __forceinline__ float widen(uint32_t x) const {
+    if constexpr (!K16) return __uint_as_float(x);
+    return dt == HELM_BF16 ? __uint_as_float(x << 16)
+                           : static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x)));
   }
 };
 
@@ -601,7 +698,10 @@ __device__ __forceinline__ void fused_merge_tail(Smem<NW, GM, DMAX>& sm,
       for (int j = 0; j < cw; ++j) store_elem<TQ>(orow + (d0 + j) * QB, a[j] * inv);
     }
   }
-  if (tid == 0) p.tickets[tile] = 0u;
+  if (tid == 0) {
+    p.tickets[tile] = 0u;
+    reset_claims(p, tile);
+  }
 }
 
 // Shared end of a split for the vector-ALU decode kernels (NW waves per
@@ -785,7 +885,10 @@ __device__ __forceinline__ void split_epilogue_d128(Smem<NW, GM, 128>& sm, const
       store_elem<TQ>(orow + (d0 + 2) * QB, o.z * inv);
       store_elem<TQ>(orow + (d0 + 3) * QB, o.w * inv);
     }
-    if (tid == 0) p.tickets[tile] = 0u;
+    if (tid == 0) {
+      p.tickets[tile] = 0u;
+      reset_claims(p, tile);
+    }
   }
 }
 
@@ -807,6 +910,8 @@ __global__ __launch_bounds__(kThreads) void merge_splits_kernel(AttnParams p) {
   __shared__ float4 red[kThreads];
   __shared__ float2 redml[kThreads];
   const int tile = blockIdx.x;
+  // every split of the tile has finished claiming blocks
+  if (blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0) reset_claims(p, tile);
   const int row = blockIdx.y;
   const int tid = threadIdx.x;
   const int D = p.D, S = p.S, G = p.G;
@@ -928,6 +1033,8 @@ __global__ __launch_bounds__(kThreads) void merge_splits_d128_kernel(AttnParams 
   __shared__ float4 red[kThreads];
   __shared__ float2 redml[kThreads];
   const int tile = blockIdx.x;
+  // every split of the tile has finished claiming blocks
+  if (blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0) reset_claims(p, tile);
   const int row = blockIdx.y;
   const int tid = threadIdx.x;
   const int RS = p.rows_per_tile;
@@ -1028,6 +1135,8 @@ template <typename TQ>
 __global__ __launch_bounds__(kThreads) void merge_rows_d128_kernel(AttnParams p) {
   constexpr int QB = ElemBytes<TQ>::v;
   const int tile = blockIdx.x;
+  // every split of the tile has finished claiming blocks
+  if (blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0) reset_claims(p, tile);
   const int tid = threadIdx.x;
   const int RS = p.rows_per_tile;
   const int row = blockIdx.y * (kThreads / 32) + (tid >> 5);

@@ -52,7 +52,9 @@ constexpr float kMfmaSlack = 8.f;
 #endif
 constexpr int kMfmaBufs = HELM_MFMA_NBUF;
 
-enum MfmaFeat { kFeatMask = 1, kFeatCap = 2, kFeatCausal = 4 };
+// kFeatMask16: the mask is 16-bit (bf16 / fp16); only the decode kernel
+// reads it at that width (the chunk kernels read the element type at run time)
+enum MfmaFeat { kFeatMask = 1, kFeatCap = 2, kFeatCausal = 4, kFeatMask16 = 8 };
 
 typedef __bf16 mf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 mf_f16x8 __attribute__((ext_vector_type(8)));
@@ -340,6 +342,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   constexpr bool kMask = (FEAT & kFeatMask) != 0;
   constexpr bool kCap = (FEAT & kFeatCap) != 0;
   constexpr bool kCausal = (FEAT & kFeatCausal) != 0;
+  constexpr bool kMask16 = (FEAT & kFeatMask16) != 0;
 
   __shared__ Smem<NW, kMfmaRows, 128> sm;
 
@@ -348,6 +351,14 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   const int lane = tid & 63;
   const int q4 = lane >> 4;
   const int n = lane & 15;
+  // profiling stamps of this workgroup (helm_profile_workgroup_stamps)
+  uint64_t* const stp =
+      p.stamps ? p.stamps + 4 * (blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z))
+               : nullptr;
+  if (stp && tid == 0) {
+    stp[0] = stamp_now();
+    stp[3] = stamp_place();
+  }
 
   int split_local = blockIdx.x, b = blockIdx.z;
   if constexpr (std::is_same<Src, DescSrc>::value) {
@@ -415,6 +426,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
         store_elem<T>(reinterpret_cast<char*>(p.out) + o_off * 2, 0.f);
       }
     }
+    if (stp && tid == 0) stp[1] = stp[2] = stamp_now();
     return;
   }
   const int split = p.split_base + split_local;
@@ -426,7 +438,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
     // page's last used slot (16 lanes K, 16 lanes V, 16 bytes each), and the
     // stores are complete before any wave of the workgroup reads the page.
     // Workgroups of other query tiles of the same head write the same bytes.
-    if (b < src.app_n && pg0 + npg == np) {
+    if (!p.dyn && b < src.app_n && pg0 + npg == np) {
       if (wave == 0) {
         const PageView tv = src.page(b, np - 1, hk);
         if (lane < 32 && tv.used > 0) {
@@ -465,7 +477,7 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   struct Blk {
     mf_u32x4 k[4];
     mf_u32x4 v[4];
-    float mk[4];
+    uint32_t mk[4];  // mask elements as loaded (widened when used)
     int ntok;   // valid tokens of the block (0: past the end)
     int tok0;   // HELM token cursor of the block's first token
   };
@@ -486,19 +498,169 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
 #pragma unroll
     for (int j = 0; j < 4; ++j) B.v[j] = buf_load16_nt(rv, voff_v + 1024 * j);
     if constexpr (kMask) {
-      // token 4r + q4 of the block for row n; clamped inside the page's tokens
+      // token 4r + q4 of the block for row n; clamped inside the block's
+      // tokens (a block past its page's tokens reads the row's first key:
+      // its scores are -inf whatever the mask holds)
+      const int mbase = ntok > 0 ? B.tok0 : 0;
       const int last = max(ntok - 1, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        B.mk[r] = mrow[B.tok0 + min(4 * r + q4, last)];
+        B.mk[r] = mrow.bits<kMask16>(mbase + min(4 * r + q4, last));
     }
   };
 
   auto compute_block = [&](const Blk& B) {
-    mfma_block_step<Ops, kMask, kCap, kCausal>(B.k, B.v, B.mk, B.ntok, B.tok0, qop, m, lsum, o,
+    float mk[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mk[r] = kMask ? mrow.widen<kMask16>(B.mk[r]) : 0.f;
+    mfma_block_step<Ops, kMask, kCap, kCausal>(B.k, B.v, mk, B.ntok, B.tok0, qop, m, lsum, o,
                                                scale, cap, inv_cap, s_vis, q4);
   };
 
+  // ---- dynamic block claiming (p.dyn): the waves of every workgroup of the
+  // tile share the tile's blocks through one counter -------------------------
+  // Block k of the tile is page lo + k / bpp, 16-token block k % bpp of it.
+  // The Wt waves of the tile's workgroups take blocks w, w + Wt, w + 2 Wt
+  // first (w = the wave's index among them), then claim one block at a time
+  // (block 3 Wt + the counter's old value), so a wave that streams faster
+  // takes more blocks and every wave's last block ends at about the same
+  // time.  Per step a wave reads the result of the claim it issued one step
+  // before, issues the next claim, fetches the page record of the block two
+  // ahead (scalar load) and the K / V of the block one ahead, then computes
+  // the current block: each of the three latencies hides behind one step.
+  // Claims only grow, so a wave is done at its first block past the tile.
+  if (p.dyn) {
+    const int Wt = nsplit_launch * NW;
+    const int np_t = hi - lo;
+    const int nblk_t = np_t * bpp;
+    const int kbase = 3 * Wt;
+    uint32_t* const ctr = p.claims + (int64_t)tile * kClaimStride;
+    const int w0 = split_local * NW + wave;
+    // the block whose last slot takes the step's new token (-1: none)
+    int k_tok = -1;
+    const char* tok_from = nullptr;
+    if constexpr (std::is_same<Src, DescSrc>::value) {
+      if (b < src.app_n && np_t > 0) {
+        const PageView tv = src.page(b, hi - 1, hk);
+        if (tv.used > 0) {
+          k_tok = (np_t - 1) * bpp + (tv.used - 1) / kBlockTok;
+          tok_from = (lane >= 16 ? src.app_v[b] : src.app_k[b]) + hk * src.app_hs[b] * 2 +
+                     16 * (lane & 15);
+        }
+      }
+    }
+    // block k's page record, fetched a step before it is used (scalar loads
+    // whose wait falls in the next step), and its view; past the tile: none
+    struct Rec {
+      typename Src::Raw r;
+      int k;
+    };
+    const typename Src::Ctx sc = src.ctx(b);
+    auto fetch = [&](int k) {
+      Rec d;
+      d.k = __builtin_amdgcn_readfirstlane(k);  // uniform: scalar loads, not vector ones
+      // (past the tile: the last page's record, not used)
+      const int kk = min(d.k, nblk_t - 1);
+      const int pi = p.bpp_log2 >= 0 ? kk >> p.bpp_log2 : kk / bpp;
+      d.r = src.raw(sc, lo + pi);
+      return d;
+    };
+    auto view = [&](Rec d) {
+      PageView pv;
+      if (d.k < nblk_t) {
+        const int pi = p.bpp_log2 >= 0 ? d.k >> p.bpp_log2 : d.k / bpp;
+        Src::pin(d.r);
+        pv = src.view(sc, d.r, lo + pi, hk);
+        const int tok_in = (d.k - pi * bpp) * kBlockTok;
+        pv.k += tok_in * kRow;
+        pv.v += tok_in * kRow;
+        pv.tok_off += tok_in;
+        pv.used -= tok_in;
+      } else {
+        pv.k = pv.v = reinterpret_cast<const char*>(p.q);
+        pv.used = 0;
+        pv.tok_off = 0;
+      }
+      // (uniform; said so, so that the values stay in scalar registers)
+      pv.k = reinterpret_cast<const char*>(uniform64(reinterpret_cast<uint64_t>(pv.k)));
+      pv.v = reinterpret_cast<const char*>(uniform64(reinterpret_cast<uint64_t>(pv.v)));
+      pv.used = __builtin_amdgcn_readfirstlane(pv.used);
+      pv.tok_off = __builtin_amdgcn_readfirstlane(pv.tok_off);
+      pv.head_stride_b = 0;
+      return pv;
+    };
+    // K / V (and mask) loads of block k through its record
+    auto load_dyn = [&](int k, const PageView& pv, Blk& B) {
+      k = __builtin_amdgcn_readfirstlane(k);
+      if constexpr (std::is_same<Src, DescSrc>::value) {
+        if (k == k_tok) {
+          // this wave is the one that reads the new token's block: write the
+          // token into its slot first (16 lanes K, 16 lanes V)
+          if (lane < 32) {
+            char* to = const_cast<char*>(lane >= 16 ? pv.v : pv.k) +
+                       (int64_t)(pv.used - 1) * kRow + 16 * (lane & 15);
+            *reinterpret_cast<uint4*>(to) = *reinterpret_cast<const uint4*>(tok_from);
+          }
+          __builtin_amdgcn_s_waitcnt(0);
+        }
+      }
+      const int ntok = sclamp(pv.used, 0, kBlockTok);
+      B.ntok = ntok;
+      B.tok0 = pv.tok_off;
+      const auto rk = make_rsrc(pv.k, ntok * kRow);
+      const auto rv = make_rsrc(pv.v, ntok * kRow);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) B.k[i] = buf_load16_nt(rk, voff_k + 64 * i);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) B.v[j] = buf_load16_nt(rv, voff_v + 1024 * j);
+      if constexpr (kMask) {
+        const int mbase = ntok > 0 ? B.tok0 : 0;
+        const int last = max(ntok - 1, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) B.mk[r] = mrow.bits<kMask16>(mbase + min(4 * r + q4, last));
+      }
+    };
+    auto claim = [&]() {
+      uint32_t v = 0;
+      if (lane == 0) v = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return v;
+    };
+    bool dry = kbase >= nblk_t;  // no block left to claim
+    uint32_t cl = dry ? 0u : claim();
+    int kc = w0, kn = w0 + Wt, kr = w0 + 2 * Wt;
+    Rec rn = fetch(kn);
+    Blk buf[2];
+    load_dyn(kc, view(fetch(kc)), buf[0]);
+    auto step = [&](Blk& cur, Blk& nxt) {
+      int kq = nblk_t;
+      if (!dry) {
+        kq = kbase + (int)__builtin_amdgcn_readfirstlane(cl);
+        if (kq >= nblk_t) {
+          kq = nblk_t;
+          dry = true;
+        } else {
+          cl = claim();
+        }
+      }
+      // (the record fetch after the view of the one fetched a step before:
+      // scalar loads return out of order, so a wait for that one would also
+      // wait for this one)
+      load_dyn(kn, view(rn), nxt);
+      const Rec rr = fetch(kr);
+      compute_block(cur);
+      kc = kn;
+      kn = kr;
+      rn = rr;
+      kr = kq;
+    };
+    while (kc < nblk_t) {
+      step(buf[0], buf[1]);
+      if (kc >= nblk_t) break;
+      step(buf[1], buf[0]);
+    }
+    // the claim still in flight (its result is not needed)
+    __builtin_amdgcn_s_waitcnt(0);
+  } else
   // ---- main loop: a ring of kMfmaBufs register buffers, kMfmaBufs - 1
   // blocks' loads in flight while one block is computed ----------------------
   {
@@ -532,7 +694,9 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
     *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4][r], o[5][r], o[6][r], o[7][r]);
   }
   __syncthreads();
+  if (stp && tid == 0) stp[1] = stamp_now();
   split_epilogue_d128<T, NW, kMfmaRows>(sm, p, tid, tile, split, total, nrows, r0, b, hk);
+  if (stp && tid == 0) stp[2] = stamp_now();
 }
 
 // ---- query chunks: K/V blocks staged through LDS ----------------------------

@@ -137,7 +137,9 @@ int kernel_choice() {
 // left zero by every call, whatever shapes earlier calls had (a region sized
 // per call would grow into bytes an earlier call used for split counts or
 // partials).  A call with more tiles than it holds merges in the second kernel.
-constexpr size_t kTicketRegionBytes = 64 << 10;  // 16,384 tiles
+constexpr size_t kTicketRegionBytes = 64 << 10;
+// its second half holds the dynamic block claims' counters (256 tiles)
+constexpr size_t kClaimRegionBytes = 32 << 10;
 
 void size_plan(Plan& pl, int B, int Hkv, int D) {
   const size_t tiles = (size_t)B * Hkv * pl.n_qtiles;
@@ -151,7 +153,8 @@ void size_plan(Plan& pl, int B, int Hkv, int D) {
 // partial offsets reach every partial.
 void settle_fused(Plan& pl, int B, int Hkv) {
   const size_t tiles = (size_t)B * Hkv * pl.n_qtiles;
-  if (pl.o_bytes >= 0x7ffffff0u || tiles * 4 > kTicketRegionBytes || pl.row_waves)
+  if (pl.o_bytes >= 0x7ffffff0u || tiles * 4 > kTicketRegionBytes - kClaimRegionBytes ||
+      pl.row_waves)
     pl.fused = 0;
   pl.direct = (pl.row_waves && pl.max_splits == 1) ? 1 : 0;
 }
@@ -367,6 +370,24 @@ void fill_params(AttnParams& a, const Plan& pl, const void* q, void* out,
   a.fused = pl.fused;
   a.ws_ml = reinterpret_cast<float*>(ws + pl.ticket_bytes + pl.count_bytes);
   a.ws_o = reinterpret_cast<float*>(ws + pl.ticket_bytes + pl.count_bytes + pl.ml_bytes);
+  a.stamps = nullptr;
+  a.dyn = 0;
+  a.claims = nullptr;
+}
+
+// Dynamic block claiming for a one-launch matrix-core decode call
+// (HELM_AMD_CLAIM=1): its counters sit in the second half of the ticket
+// region (zero between calls), one 128-byte line per tile.  Which wave sums
+// which block then depends on timing, so the fp32 sums' order (and the last
+// bits of a result) can change from call to call; the static split (the
+// default) gives the same bits for the same inputs.
+void enable_claims(AttnParams& a, const Plan& pl, int B, int Hkv, char* ws) {
+  const size_t tiles = (size_t)B * Hkv * pl.n_qtiles;
+  if (!pl.mfma || pl.row_waves || tiles * kClaimStride * 4 > kClaimRegionBytes ||
+      !env_int("HELM_AMD_CLAIM", 0))
+    return;
+  a.dyn = 1;
+  a.claims = reinterpret_cast<uint32_t*>(ws + kTicketRegionBytes - kClaimRegionBytes);
 }
 
 hipError_t dispatch(const LaunchSpec& s, hipStream_t st) {
@@ -395,10 +416,27 @@ void prof_free_locked() {
   g_prof_left.store(0);
 }
 
+// ---- workgroup stamps (helm_profile_workgroup_stamps) ----------------------------
+// A caller's device buffer that the next decode-kernel launch writes its
+// workgroups' stamps into; taken (and disarmed) by that launch.
+std::atomic<uint64_t*> g_stamp_buf{nullptr};
+std::atomic<int> g_stamp_cap{0};
+
 // dispatch() with the armed timing events attached to the launch itself
 // (hipExtLaunchKernelGGL's start / stop events: the kernel's own start and
 // end, no queue gap before it)
 hipError_t dispatch_timed(const LaunchSpec& s, hipStream_t st) {
+  if (s.mfma && !s.p.row_waves && g_stamp_buf.load(std::memory_order_relaxed)) {
+    const uint64_t wgs = (uint64_t)s.grid.x * s.grid.y * s.grid.z;
+    if (wgs <= (uint64_t)g_stamp_cap.load()) {
+      uint64_t* buf = g_stamp_buf.exchange(nullptr);
+      if (buf) {
+        LaunchSpec t = s;
+        t.p.stamps = buf;
+        return dispatch(t, st);
+      }
+    }
+  }
   if (g_prof_left.load(std::memory_order_relaxed) > 0) {
     LaunchSpec t = s;
     {
@@ -940,6 +978,14 @@ int helm_profile_split_kernels(int n) {
   return HELM_OK;
 }
 
+int helm_profile_workgroup_stamps(void* dev_buf, int max_workgroups) {
+  if (max_workgroups < 0 || (max_workgroups > 0 && !dev_buf))
+    return fail(HELM_E_INVALID, "bad stamp buffer");
+  g_stamp_cap.store(max_workgroups);
+  g_stamp_buf.store(max_workgroups > 0 ? reinterpret_cast<uint64_t*>(dev_buf) : nullptr);
+  return HELM_OK;
+}
+
 int helm_profile_split_read(float* us_out, int max_n) {
   if (!us_out || max_n < 0) return fail(HELM_E_INVALID, "bad output array");
   std::lock_guard<std::mutex> lock(g_prof_mu);
@@ -1039,6 +1085,7 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
   fill_params(s.p, pl, q, out, B, Hq, Hkv, q_len, D, scale, softcap, mask,
               mask_bstride, mask_hstride, mask_qstride, mask_dtype, 0,
               reinterpret_cast<char*>(workspace));
+  enable_claims(s.p, pl, B, Hkv, reinterpret_cast<char*>(workspace));
   s.p.full_d = (al && D == 16 * pl.epl) ? 1 : 0;
   s.mode = 0;
   s.pool.k_pool = reinterpret_cast<const char*>(k_pool);
@@ -1057,7 +1104,8 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
   s.fast = pl.fast;
   s.mfma = pl.mfma;
   s.nw = pl.nw;
-  s.feat = (mask ? kFeatMask : 0) | (softcap > 0.f ? kFeatCap : 0);
+  s.feat = (mask ? kFeatMask : 0) | (mask && mask_dtype != HELM_F32 ? kFeatMask16 : 0) |
+           (softcap > 0.f ? kFeatCap : 0);
   s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.qblocks(), B);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e = dispatch_timed(s, st);
@@ -1338,7 +1386,8 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   s.fast = pl.fast;
   s.mfma = pl.mfma;
   s.nw = pl.nw;
-  s.feat = (mask ? kFeatMask : 0) | (softcap > 0.f ? kFeatCap : 0) |
+  s.feat = (mask ? kFeatMask : 0) | (mask && mask_dtype != HELM_F32 ? kFeatMask16 : 0) |
+           (softcap > 0.f ? kFeatCap : 0) |
            (causal ? kFeatCausal : 0);
 
   if (!n_host) {
@@ -1484,6 +1533,7 @@ static int paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B, in
   LaunchSpec s{};
   fill_params(s.p, pl, q, out, B, Hq, Hkv, q_len, D, scale, softcap, mask,
               mask_bstride, mask_hstride, mask_qstride, mask_dtype, causal, eng->ws);
+  enable_claims(s.p, pl, B, Hkv, eng->ws);
   s.p.full_d = (al && D == 16 * pl.epl) ? 1 : 0;
   s.mode = 1;
   s.desc.elem_bytes = eb;
@@ -1515,7 +1565,8 @@ static int paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B, in
   s.fast = pl.fast;
   s.mfma = pl.mfma;
   s.nw = pl.nw;
-  s.feat = (mask ? kFeatMask : 0) | (softcap > 0.f ? kFeatCap : 0) |
+  s.feat = (mask ? kFeatMask : 0) | (mask && mask_dtype != HELM_F32 ? kFeatMask16 : 0) |
+           (softcap > 0.f ? kFeatCap : 0) |
            (causal ? kFeatCausal : 0);
   s.grid = compact ? dim3(all_splits, Hkv * pl.qblocks(), 1)
                   : dim3(std::max(1, pl.max_splits), Hkv * pl.qblocks(), B);

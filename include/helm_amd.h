@@ -109,10 +109,11 @@ void* helm_engine_copy_stream(helm_engine* eng);
 /* ---- attention ------------------------------------------------------------ */
 
 /* Workspace (bytes) helm_paged_decode_attn needs for this shape: per-tile
- * merge tickets (a fixed region at its start, 64 KiB, used for nothing
- * else), split counts, and the split partials (m, l, o[D]) of every query
- * row.  It must be zero before its first use; every completed call leaves the
- * ticket region zero again, so one workspace serves calls of any shapes. */
+ * merge tickets and block-claim counters (a fixed region at its start,
+ * 64 KiB, used for nothing else), split counts, and the split partials
+ * (m, l, o[D]) of every query row.  It must be zero before its first use;
+ * every completed call leaves the ticket region zero again, so one workspace
+ * serves calls of any shapes. */
 size_t helm_query_workspace_bytes(int B, int Hq, int Hkv, int q_len, int D,
                                   int max_pages, int page_size,
                                   int pages_per_split);
@@ -347,6 +348,18 @@ int helm_measure_bandwidth(int device, uint64_t stream_bytes, uint64_t link_byte
  * kernel's own and the split merge that follows is outside it.  n = 0 disarms
  * and frees the events.  Process-wide; arm, run and read from one thread. */
 int helm_profile_split_kernels(int n);
+
+/* No counterpart in HELM: a profiling hook that shows how the decode
+ * kernel's workgroups share a call.  Arms the next matrix-core decode-kernel
+ * launch of helm_paged_decode_attn[_static] or helm_paged_attn_seqs[_append]
+ * whose grid has at most max_workgroups
+ * workgroups to write, for workgroup w (blockIdx.x + gridDim.x * (blockIdx.y
+ * + gridDim.y * blockIdx.z)), four uint64 at dev_buf + 32 w: the s_memrealtime
+ * counter (100 MHz) at its start, after its page loop (every wave done), at
+ * its end, and (XCD id << 32) | HW_ID (its CU, SIMD and shader engine).  The
+ * launch disarms it.  dev_buf is device memory the caller owns and reads
+ * after the launch completes.  max_workgroups = 0 disarms.  Process-wide. */
+int helm_profile_workgroup_stamps(void* dev_buf, int max_workgroups);
 
 /* Waits for the armed calls' events and writes the split-kernel durations of
  * the calls timed so far (microseconds, call order) to us_out[0 .. max_n);
