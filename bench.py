@@ -97,6 +97,9 @@ def parse():
     ap.add_argument("--stamps", action="store_true",
                     help="also record per-workgroup start / page-loop-end / end times of the "
                          "headline decode kernel (helm_profile_workgroup_stamps)")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="also time a kernel that only reads the headline call's K/V bytes "
+                         "(with and without a merge-sized second kernel): the call's floor")
     ap.add_argument("--all-json", default=None, metavar="PATH",
                     help="with --all, also write the configurations' rows to PATH as JSON")
     return ap.parse_args()
@@ -176,8 +179,39 @@ def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=Non
         "per_call_s": per_call_s, "wall_ms_per_step": wall * 1e3 / steps,
         "host_issue_us_per_call": (t_issued - t0) * 1e6 / steps,
         "ms_per_step": ms_events / steps, "pools": n_pools, "lens": lens, "prep": prep,
-        "step": step,
+        "step": step, "pool_tensors": pools,
     }
+
+
+def read_pass_floor(torch, h, iters=200):
+    """The headline call's floor (helm_profile_read_pass): a kernel that only
+    streams the call's K/V bytes out of the same rotated pools, at 256 to 2048
+    workgroups, alone and followed by a 32-workgroup kernel reading the
+    split merge's 0.53 MB of partials (the two launches of a call)."""
+    from helm_amd import _native
+    pools = h["pool_tensors"]
+    kv = h["kv_bytes"]
+    if any(p.numel() * p.element_size() < kv for p in pools):
+        raise RuntimeError("read-pass probe: a pool holds fewer bytes than the call reads")
+    ptrs = np.array([p.data_ptr() for p in pools], dtype=np.uint64)
+    stream = torch.cuda.current_stream().cuda_stream
+    tail = 32 * 4 * 8 * 130 * 4          # splits x rows x KV heads x (D + 2) x fp32
+    out = {"kv_bytes": kv, "tail_bytes": tail, "iters": iters}
+    us = np.zeros(1, dtype=np.float32)
+    for wg in (256, 512, 1024, 2048):
+        row = {}
+        for label, tb, twg in (("read", 0, 0), ("read_then_tail", tail, 32)):
+            _native.call("helm_profile_read_pass", _native.ptr(ptrs), len(pools), kv, wg, tb,
+                         twg, iters, stream, _native.ptr(us))
+            row[label + "_us"] = round(float(us[0]), 3)
+        row["read_GBs"] = round(kv / (row["read_us"] * 1e-6) / 1e9, 1)
+        out[f"workgroups_{wg}"] = row
+    out["how"] = ("helm_profile_read_pass over the headline's rotated pools: each pass reads "
+                  "the call's K/V bytes (each workgroup a contiguous run; 16-byte "
+                  "non-temporal loads, 8 in flight per thread), "
+                  "alone and followed by a 32-workgroup kernel reading the merge's partial "
+                  "bytes; HIP events around the passes")
+    return out
 
 
 def workgroup_stamps(torch, h, captures=5, run=40):
@@ -1003,6 +1037,11 @@ def main():
         stamps = workgroup_stamps(torch, h)
         log("workgroup stamps: " + json.dumps(stamps))
 
+    read_floor = None
+    if args.read_probe:
+        read_floor = read_pass_floor(torch, h)
+        log("read-pass floor: " + json.dumps(read_floor))
+
     if args.copy_calibration:
         n = 1 << 30
         a = torch.empty(n, dtype=torch.uint8, device="cuda")
@@ -1139,6 +1178,7 @@ def main():
                      "host_issue_us_per_call": round(h["host_issue_us_per_call"], 2)},
         "decode_masked_32k": masked_c2,
         "workgroup_stamps": stamps,
+        "read_pass_floor": read_floor,
         "configs": configs,
         "runtime_decode_32k": runtime,
         "c1_cpu_path": c1_cpu,

@@ -41,6 +41,20 @@ BANDWIDTH_DTYPE = np.dtype([
 ])
 assert BANDWIDTH_DTYPE.itemsize == 32
 
+# helm_decode_args (include/helm_amd.h); 744 bytes, no padding
+DECODE_MAX_SEQS = 16
+DECODE_ARGS_DTYPE = np.dtype([
+    ("q", "<u8"), ("out", "<u8"), ("mask", "<u8"), ("stream", "<u8"),
+    ("mask_bstride", "<i8"), ("mask_hstride", "<i8"), ("mask_qstride", "<i8"),
+    ("seq_pages", "<u8", (DECODE_MAX_SEQS,)), ("tok_k", "<u8", (DECODE_MAX_SEQS,)),
+    ("tok_v", "<u8", (DECODE_MAX_SEQS,)), ("tok_head_stride", "<i8", (DECODE_MAX_SEQS,)),
+    ("seq_npages", "<i4", (DECODE_MAX_SEQS,)), ("seq_tokens", "<i4", (DECODE_MAX_SEQS,)),
+    ("B", "<i4"), ("Hq", "<i4"), ("Hkv", "<i4"), ("D", "<i4"),
+    ("page_tokens", "<i4"), ("aligned16", "<i4"), ("mask_dtype", "<i4"), ("kv_dtype", "<i4"),
+    ("append", "<i4"), ("pad", "<i4"), ("scale", "<f4"), ("softcap", "<f4"),
+])
+assert DECODE_ARGS_DTYPE.itemsize == 744
+
 _c_void_p = ctypes.c_void_p
 _i32, _i64, _u64, _f32, _sz = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_float, ctypes.c_size_t
 
@@ -75,6 +89,7 @@ SIGNATURES = {
         _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, _f32, _f32, _c_void_p,
         _i64, _i64, _i64, ctypes.c_int, ctypes.c_int, _c_void_p, _c_void_p]),
+    "helm_decode_step": (ctypes.c_int, [_c_void_p, _c_void_p]),
     "helm_upload": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),
     "helm_host_pages_in_place": (ctypes.c_int, [_c_void_p, _c_void_p, ctypes.c_int,
                                                 ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -88,6 +103,9 @@ SIGNATURES = {
     "helm_profile_split_kernels": (ctypes.c_int, [ctypes.c_int]),
     "helm_profile_split_read": (ctypes.c_int, [_c_void_p, ctypes.c_int]),
     "helm_profile_workgroup_stamps": (ctypes.c_int, [_c_void_p, ctypes.c_int]),
+    "helm_profile_read_pass": (ctypes.c_int, [_c_void_p, ctypes.c_int, _u64, ctypes.c_int, _u64,
+                                              ctypes.c_int, ctypes.c_int, _c_void_p,
+                                              _c_void_p]),
     "helm_measure_bandwidth": (ctypes.c_int, [ctypes.c_int, _u64, _u64, ctypes.c_int,
                                               _c_void_p]),
     "helm_evict_pages": (ctypes.c_int, [_c_void_p, ctypes.c_int, _c_void_p, _c_void_p,

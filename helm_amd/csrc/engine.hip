@@ -1604,6 +1604,37 @@ int helm_paged_attn_seqs_append(helm_engine* eng, const void* q, void* out, int 
                          mask_hstride, mask_qstride, mask_dtype, 0, kv_dtype, kv_dtype, tokens, stream);
 }
 
+static_assert(sizeof(helm_decode_args) == 744, "helm_decode_args layout (helm_amd/_native.py)");
+
+int helm_decode_step(helm_engine* eng, const helm_decode_args* a) {
+  if (!a) return fail(HELM_E_INVALID, "null pointer argument");
+  if (a->B <= 0 || a->B > HELM_DECODE_MAX_SEQS)
+    return fail(HELM_E_UNSUPPORTED, "B must be in [1, " +
+                                        std::to_string(HELM_DECODE_MAX_SEQS) + "]");
+  const void* mask = reinterpret_cast<const void*>(a->mask);
+  void* st = reinterpret_cast<void*>(a->stream);
+  if (!a->append)
+    return paged_attn_seqs(eng, reinterpret_cast<const void*>(a->q),
+                           reinterpret_cast<void*>(a->out), a->B, a->Hq, a->Hkv, 1, a->D,
+                           a->seq_pages, a->seq_npages, a->seq_tokens, a->page_tokens,
+                           a->aligned16, a->scale, a->softcap, mask, a->mask_bstride,
+                           a->mask_hstride, a->mask_qstride, a->mask_dtype, 0, a->kv_dtype,
+                           a->kv_dtype, nullptr, st);
+  helm_append_seg app[HELM_DECODE_MAX_SEQS];
+  for (int b = 0; b < a->B; ++b) {
+    app[b] = helm_append_seg{};
+    app[b].src_k = a->tok_k[b];
+    app[b].src_v = a->tok_v[b];
+    app[b].src_head_stride = a->tok_head_stride[b];
+    app[b].n_tok = 1;
+  }
+  return helm_paged_attn_seqs_append(
+      eng, reinterpret_cast<const void*>(a->q), reinterpret_cast<void*>(a->out), a->B, a->Hq,
+      a->Hkv, a->D, a->seq_pages, a->seq_npages, a->seq_tokens, a->page_tokens, a->aligned16,
+      a->scale, a->softcap, mask, a->mask_bstride, a->mask_hstride, a->mask_qstride,
+      a->mask_dtype, a->kv_dtype, app, st);
+}
+
 int helm_upload(helm_engine* eng, void* dst, const void* src, size_t bytes,
                 void* stream) {
   if (!eng || (bytes && (!dst || !src)))

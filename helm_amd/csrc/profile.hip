@@ -47,6 +47,38 @@ __global__ void count_mismatch_kernel(const uint32_t* a, const uint32_t* b, size
   if (local) atomicAdd(bad, local);
 }
 
+// Bare read pass: every 16-byte element of src[0, n) read once with the
+// non-temporal hint and folded by XOR into one word per workgroup in sink (so
+// that no load can be removed).  Workgroup w reads its own contiguous run of
+// elements, as a decode workgroup walks its split; each thread keeps eight
+// 16-byte loads in flight (a wave reads 1 KiB contiguous per load).
+__global__ __launch_bounds__(256) void read_pass_kernel(const u32x4* __restrict__ src, size_t n,
+                                                        uint32_t* __restrict__ sink) {
+  __shared__ uint32_t red[256];
+  constexpr size_t kStep = 256 * 8;
+  const size_t per = (n + gridDim.x - 1) / gridDim.x;
+  const size_t lo = min(n, (size_t)blockIdx.x * per);
+  const size_t hi = min(n, lo + per);
+  uint32_t acc = 0;
+  for (size_t i = lo + threadIdx.x; i < hi; i += kStep) {
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const size_t e = i + 256 * j;
+      v[j] = e < hi ? __builtin_nontemporal_load(src + e) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc ^= v[j][0] ^ v[j][1] ^ v[j][2] ^ v[j][3];
+  }
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t x = 0;
+    for (int t = 0; t < 256; ++t) x ^= red[t];
+    sink[blockIdx.x] = x;
+  }
+}
+
 struct Probe {
   hipStream_t st = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
@@ -162,5 +194,51 @@ extern "C" int helm_measure_bandwidth(int device, uint64_t stream_bytes, uint64_
   const hipError_t e = hipSetDevice(prev);
   if (rc == HELM_OK && e != hipSuccess)
     return helm::report_error((int)e, std::string("hipSetDevice: ") + hipGetErrorString(e));
+  return rc;
+}
+
+extern "C" int helm_profile_read_pass(const void* const* bufs, int nbufs, uint64_t bytes,
+                                      int workgroups, uint64_t tail_bytes, int tail_workgroups,
+                                      int iters, void* stream, float* us_per_iter) {
+  if (!bufs || nbufs < 1 || !us_per_iter || iters < 1 || bytes < 16 || bytes % 16 ||
+      workgroups < 1 || tail_bytes % 16 || tail_bytes > bytes ||
+      (tail_bytes && tail_workgroups < 1))
+    return helm::report_error(HELM_E_INVALID,
+                              "need buffers, iters >= 1, byte counts multiples of 16 (tail <= "
+                              "bytes) and workgroups >= 1");
+  for (int i = 0; i < nbufs; ++i)
+    if (!bufs[i]) return helm::report_error(HELM_E_INVALID, "null buffer");
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int sink_words = workgroups > tail_workgroups ? workgroups : tail_workgroups;
+  uint32_t* sink = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  auto run = [&]() -> int {
+    PROBE_HIP(hipMalloc(&sink, (size_t)sink_words * 4));
+    PROBE_HIP(hipEventCreate(&e0));
+    PROBE_HIP(hipEventCreate(&e1));
+    auto pass = [&](int i) -> hipError_t {
+      hipLaunchKernelGGL(read_pass_kernel, dim3(workgroups), dim3(256), 0, st,
+                         static_cast<const u32x4*>(bufs[i % nbufs]), (size_t)(bytes / 16), sink);
+      if (tail_bytes)
+        hipLaunchKernelGGL(read_pass_kernel, dim3(tail_workgroups), dim3(256), 0, st,
+                           static_cast<const u32x4*>(bufs[(i + 1) % nbufs]),
+                           (size_t)(tail_bytes / 16), sink);
+      return hipGetLastError();
+    };
+    for (int i = 0; i < 3; ++i) PROBE_HIP(pass(i));
+    PROBE_HIP(hipEventRecord(e0, st));
+    for (int i = 0; i < iters; ++i) PROBE_HIP(pass(i));
+    PROBE_HIP(hipEventRecord(e1, st));
+    PROBE_HIP(hipEventSynchronize(e1));
+    float ms = 0.f;
+    PROBE_HIP(hipEventElapsedTime(&ms, e0, e1));
+    *us_per_iter = ms * 1e3f / iters;
+    return HELM_OK;
+  };
+  const int rc = run();
+  if (st) (void)hipStreamSynchronize(st);
+  if (sink) (void)hipFree(sink);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
   return rc;
 }

@@ -139,6 +139,7 @@ class LayerKVCache:
         self._dev_dirty: List[int] = []  # records changed since the last upload
         self._dev_all = False           # every record needs an upload
         self._gen = 0                   # bumped whenever the page list changes
+        self._tail_tok_off = 0          # the tail record's token offset
 
     def _reset(self) -> None:
         """Drops every page (the list is emptied in place)."""
@@ -152,6 +153,7 @@ class LayerKVCache:
         self._page_tokens, self._aligned16 = 0, True
         self._dev_dirty.clear()
         self._dev_all = True
+        self._tail_tok_off = 0
 
     def append_page(self, page: KVPage):
         self.pages.append(page)
@@ -165,6 +167,7 @@ class LayerKVCache:
         r = self._rec[n - 1:n]
         r["tok_off"] = (int(self._rec["tok_off"][n - 2]) + int(self._rec["used"][n - 2])
                         if n > 1 else 0)
+        self._tail_tok_off = int(r["tok_off"][0])
         self._tier.append((0, 0))
         self._set_record(n - 1, page)
         # the old tail's device record takes its final token count
@@ -1194,6 +1197,139 @@ def _launch_seqs(query: torch.Tensor, addrs, t_max: int, page_tokens: int, align
     if rc:
         _native.check("helm_paged_attn_seqs", rc)
     return out if out.dtype == query.dtype else out.to(query.dtype)
+
+
+# helm_decode_args word indices (include/helm_amd.h): 8-byte words, then
+# 4-byte words of the same struct
+_DA_Q, _DA_OUT, _DA_MASK, _DA_STREAM, _DA_MBS, _DA_MHS, _DA_MQS = range(7)
+_DA_PAGES, _DA_TOKK, _DA_TOKV, _DA_TOKHS = 7, 23, 39, 55
+_DA_NPAGES, _DA_TOKENS = 142, 158
+(_DA_B, _DA_HQ, _DA_HKV, _DA_D, _DA_PTOK, _DA_AL16, _DA_MDT, _DA_KVDT,
+ _DA_APPEND) = range(174, 183)
+_DA_SCALE, _DA_SOFTCAP = 184, 185
+_MASK_CODES = {torch.float32: _native.HELM_F32, torch.bfloat16: _native.HELM_BF16,
+               torch.float16: _native.HELM_F16}
+_KV16 = {torch.bfloat16: _native.HELM_BF16, torch.float16: _native.HELM_F16}
+
+
+def _decode_args():
+    """This thread's helm_decode_args block and its word views."""
+    a = getattr(_tls, "decode_args", None)
+    if a is None:
+        arr = np.zeros(1, dtype=_native.DECODE_ARGS_DTYPE)
+        raw = arr.view(np.uint8)
+        a = _tls.decode_args = (arr, raw.view(np.uint64), raw.view(np.int32),
+                                raw.view(np.float32), arr.ctypes.data)
+    return a
+
+
+def _decode_step_fast(kvcms, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      layer_idx: int, scale: float,
+                      attention_mask: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    """The common decode step of ``_decode_batched`` in one native call
+    (helm_decode_step): every item a KVCacheManager whose layer holds only
+    device pages with device-resident records that need no upload, the tail
+    page with room for the token, nothing over the watermark, 16-bit KV,
+    D = 128, q in the KV dtype.  Then HELM's append_decode bookkeeping for the
+    token is a tail count, the residency policy (kv_cache.py:224-235) cannot
+    evict anything (the evictable pages and their bytes do not change), and
+    the attention kernel writes each token itself.  Returns None, having
+    changed nothing, when any of that does not hold (the general path runs;
+    HELM_AMD_FAST_DECODE=0 always takes it)."""
+    B, Hq, S, D = q.shape
+    kv_code = _KV16.get(q.dtype)
+    if (kv_code is None or S != 1 or D != 128 or B > _native.DECODE_MAX_SEQS
+            or q.device.type != "cuda" or k.dtype is not q.dtype or v.dtype is not q.dtype
+            or not q.is_contiguous()):
+        return None
+    Hkv = k.shape[1]
+    if (k.shape[0] < B or k.shape[2] != 1 or k.stride(3) != 1 or v.stride(3) != 1
+            or k.stride(1) != v.stride(1) or (k.stride(1) * 2) % 16
+            or (k.data_ptr() | v.data_ptr() | (k.stride(0) * 2) | (v.stride(0) * 2)) % 16):
+        return None
+    env = os.environ
+    if (check_records_enabled() or not _async_kv_prefetch_enabled()
+            or env.get("HELM_AMD_FAST_DECODE") == "0" or env.get("HELM_AMD_FUSED_APPEND") == "0"
+            or env.get("HELM_AMD_KERNEL", "auto") not in ("", "auto", "mfma")
+            or q.data_ptr() % 16):
+        return None
+    device = q.device
+    sig = (q.dtype, Hkv, D)
+    layers = []
+    for kvcm in kvcms[:B]:
+        if (type(kvcm) is not KVCacheManager or "append_decode" in kvcm.__dict__
+                or kvcm.use_contiguous):
+            return None
+        layer = kvcm.layers.get(layer_idx)
+        if layer is None or layer._n_host or layer._n_other or not layer._rec_ok:
+            return None
+        tail = layer.tail_page
+        if (tail is None or tail.used_tokens >= tail.capacity_tokens or tail.state != "GPU"
+                or layer._rec_sig != sig or not layer._aligned16 or layer._dev is None
+                or layer._dev_dirty or layer._dev_all or layer._dev.device != device):
+            return None
+        kvcm._sync_layers()
+        if kvcm._ev_bytes > kvcm.gpu_high_watermark_bytes:
+            return None
+        layers.append(layer)
+    if B > 1 and len({id(layer) for layer in layers}) != B:
+        return None
+    mask_code, mbs, mhs, mqs, mptr = _native.HELM_F32, 0, 0, 0, 0
+    m = attention_mask
+    if m is not None:
+        mask_code = _MASK_CODES.get(m.dtype)
+        t_max = max(l._tail_tok_off + l.tail_page.used_tokens for l in layers) + 1
+        if (mask_code is None or m.device != device or m.dim() != 4 or m.stride(3) != 1
+                or m.shape[0] not in (1, B) or m.shape[1] not in (1, Hq) or m.shape[2] != 1
+                or m.shape[3] < t_max):
+            return None
+        mptr = m.data_ptr()
+        mbs = m.stride(0) if m.shape[0] > 1 else 0
+        mhs = m.stride(1) if m.shape[1] > 1 else 0
+    # HELM's append_decode bookkeeping (kv_cache.py:145-171): the tail gains
+    # the token
+    arr, w64, w32, f32, addr = _decode_args()
+    ks0, vs0 = k.stride(0) * 2, v.stride(0) * 2
+    kp, vp = k.data_ptr(), v.data_ptr()
+    page_tokens = 0
+    for b, layer in enumerate(layers):
+        tail = layer.tail_page
+        used = tail.used_tokens + 1
+        tail.used_tokens = used
+        layer.total_tokens += 1
+        n = len(layer.pages)
+        layer._rec["used"][n - 1] = used
+        w64[_DA_PAGES + b] = layer._dev.data_ptr()
+        w64[_DA_TOKK + b] = kp + b * ks0
+        w64[_DA_TOKV + b] = vp + b * vs0
+        w64[_DA_TOKHS + b] = k.stride(1)
+        w32[_DA_NPAGES + b] = n
+        w32[_DA_TOKENS + b] = layer._tail_tok_off + used
+        if layer._page_tokens > page_tokens:
+            page_tokens = layer._page_tokens
+    out = torch.empty_like(q)
+    w64[_DA_Q] = q.data_ptr()
+    w64[_DA_OUT] = out.data_ptr()
+    w64[_DA_MASK] = mptr
+    w64[_DA_STREAM] = _engine.stream_ptr(device)
+    w64[_DA_MBS] = mbs
+    w64[_DA_MHS] = mhs
+    w64[_DA_MQS] = mqs
+    w32[_DA_B] = B
+    w32[_DA_HQ] = Hq
+    w32[_DA_HKV] = Hkv
+    w32[_DA_D] = D
+    w32[_DA_PTOK] = page_tokens
+    w32[_DA_AL16] = 1
+    w32[_DA_MDT] = mask_code
+    w32[_DA_KVDT] = kv_code
+    w32[_DA_APPEND] = 1
+    f32[_DA_SCALE] = scale
+    f32[_DA_SOFTCAP] = 0.0
+    rc = _native.entry("helm_decode_step")(_engine.get_engine(device), addr)
+    if rc:
+        _native.check("helm_decode_step", rc)
+    return out
 
 
 def _stage_host_pages_sync(segs: List[_Segment], device: torch.device) -> List[_Segment]:

@@ -36,6 +36,7 @@ from helm_amd import _native
 from helm_amd.runtime import engine as _engine
 from helm_amd.runtime.kv_allocator import KVAllocator
 from helm_amd.runtime.kv_cache import (ContiguousKV, KVCacheManager, _async_kv_prefetch_enabled,
+                                       _decode_step_fast,
                                        _attend, _attend_device_records, _attend_layers,
                                        _attend_records, _contiguous_segments, _page_segments,
                                        _record_prefetch, perform_streaming_attention)
@@ -148,6 +149,9 @@ def _decode_batched(kvcms, q, k, v, layer_idx: int, scale: float,
         for kvcm in kvcms:
             kvcm.migrate_contiguous_to_pages()
 
+    out = _decode_step_fast(kvcms, q, k, v, layer_idx, scale, attention_mask)
+    if out is not None:
+        return out
     queued = _append_decode_items(kvcms, k, v, layer_idx, bsz, True, flush=False)
     if len(queued) != bsz:
         _flush_appends(queued)

@@ -248,6 +248,37 @@ int helm_paged_attn_seqs_append(helm_engine* eng, const void* q, void* out, int 
                                 int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int kv_dtype,
                                 const helm_append_seg* tokens, void* stream);
 
+/* One decode step of one layer for up to HELM_DECODE_MAX_SEQS sequences, its
+ * arguments in one struct (a serving loop keeps it and rewrites only what
+ * changes: q, out, token counts, mask, token sources), so that a step costs
+ * one native call.  Same call as helm_paged_attn_seqs_append (append != 0:
+ * sequence b's token at tok_k[b] / tok_v[b], heads tok_head_stride[b]
+ * elements apart, written into the last used slot of its last record) or
+ * helm_paged_attn_seqs with q_len = 1 (append == 0).  Replaces, with the
+ * runtime's slot bookkeeping, the per-layer attention of _decode_batched
+ * (helm/runtime/kv_offload.py:145-174) and its append_decode copy
+ * (helm/runtime/kv_cache.py:164-165).  Returns HELM_E_UNSUPPORTED, launching
+ * nothing, where helm_paged_attn_seqs_append would. */
+#define HELM_DECODE_MAX_SEQS 16
+typedef struct helm_decode_args {
+  uint64_t q;                 /* [B, Hq, 1, D] in the KV dtype                  */
+  uint64_t out;               /* [B, Hq, 1, D]                                  */
+  uint64_t mask;              /* additive mask of mask_dtype, or 0              */
+  uint64_t stream;            /* hipStream_t                                     */
+  int64_t mask_bstride, mask_hstride, mask_qstride;
+  uint64_t seq_pages[HELM_DECODE_MAX_SEQS];   /* device record arrays            */
+  uint64_t tok_k[HELM_DECODE_MAX_SEQS];       /* the step's tokens (append)      */
+  uint64_t tok_v[HELM_DECODE_MAX_SEQS];
+  int64_t tok_head_stride[HELM_DECODE_MAX_SEQS];
+  int32_t seq_npages[HELM_DECODE_MAX_SEQS];
+  int32_t seq_tokens[HELM_DECODE_MAX_SEQS];
+  int32_t B, Hq, Hkv, D;
+  int32_t page_tokens, aligned16, mask_dtype, kv_dtype;
+  int32_t append, pad;
+  float scale, softcap;
+} helm_decode_args;
+int helm_decode_step(helm_engine* eng, const helm_decode_args* a);
+
 /* Copies `bytes` from host memory `src` to device memory `dst` in the order
  * of `stream`, through the engine's pinned staging ring (src may be reused
  * as soon as the call returns).  Keeps device-resident page records current
@@ -336,6 +367,20 @@ typedef struct helm_bandwidth {
  * returning.  Byte counts >= 4096 and multiples of 16, iters >= 1. */
 int helm_measure_bandwidth(int device, uint64_t stream_bytes, uint64_t link_bytes,
                            int iters, helm_bandwidth* out);
+
+/* No counterpart in HELM: the floor a decode call is measured against.  Times
+ * `iters` passes on `stream` (after three untimed ones), pass i reading
+ * bufs[i % nbufs][0, bytes) once with a kernel that does nothing else
+ * (`workgroups` workgroups of 256 threads, each reading its own contiguous
+ * run with 16-byte non-temporal loads, eight in flight per thread) and,
+ * when tail_bytes > 0, then
+ * bufs[(i + 1) % nbufs][0, tail_bytes) with a second such kernel of
+ * tail_workgroups workgroups (a split merge's reads after the page walk).
+ * Writes the mean microseconds per pass to *us_per_iter.  Allocates (and
+ * frees) a small result buffer; byte counts are multiples of 16. */
+int helm_profile_read_pass(const void* const* bufs, int nbufs, uint64_t bytes, int workgroups,
+                           uint64_t tail_bytes, int tail_workgroups, int iters, void* stream,
+                           float* us_per_iter);
 
 /* ---- split-kernel timing ----------------------------------------------------- */
 
