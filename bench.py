@@ -18,7 +18,9 @@ Also measured (extra keys of the one JSON line):
 * the CPU baseline: HELM's CPU streaming attention restated by the oracle
   (torch CPU, HELM's Path 2 and masked online-softmax loop) on the same
   shape, timed on this host's cores for a bounded sample;
-* decode steps/s at 32k = 1 / (36 layers x per-layer call time);
+* decode steps/s at 32k = 1 / (36 layers x per-layer call time), for the
+  raw C-ABI call and for HELM's production call (``_decode_batched`` under
+  its decode mask, wall time per layer call);
 * the full 40-layer Qwen3-14B decode step (batch 4 x 65,536 tokens, per layer
   token append + residency policy + attention through the runtime API), with
   the 64 GB device KV budget (nothing evicted) and with a 32 GB budget that
@@ -149,7 +151,7 @@ def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=Non
     prep = paged.prepare_paged_decode(case["q"], case["k_pool"], case["v_pool"], case["table"],
                                       case["lens"], max_pages=case["max_pages"],
                                       total_pages=sum(case["n_pages"]), pages_per_split=args.pps,
-                                      attention_mask=mask)
+                                      attention_mask=mask, host_lens=lens)
     views = [(p[:, 0], p[:, 1]) for p in pools]
 
     def step(i):
@@ -778,12 +780,14 @@ def gpu_runtime_decode(args, torch, W, layers=8, steps=25, seed=11):
         e0.record(stream)
         run(steps, masked)
         e1.record(stream)
+        t_issue = time.perf_counter() - t0
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) / (steps * layers)
         gpu = e0.elapsed_time(e1) / 1e3 / (steps * layers)
         alg = W.algorithmic_bytes(w, [m.layers[0].total_tokens])
         res[label] = {"us_per_call_wall": round(wall * 1e6, 2),
                       "us_per_call_gpu_events": round(gpu * 1e6, 2),
+                      "us_per_call_host_issue": round(t_issue / (steps * layers) * 1e6, 2),
                       "GBs_wall": round(alg / wall / 1e9, 1),
                       "roofline_frac_wall": round(alg / wall / 1e9 / HBM_PEAK_GBS, 4)}
     # the last call (layer layers-1, unmasked) against the oracle on two KV heads
@@ -1155,6 +1159,11 @@ def main():
                    "global_batch": 1, "seq_len": 32768, "page_size": 16},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "decode_steps_per_s_32k": round(1.0 / (QWEN3_8B_LAYERS * h["per_call_s"]), 2),
+        # the same through HELM's production decode call (_decode_batched per
+        # layer under HELM's decode mask, wall time per layer call)
+        "decode_steps_per_s_32k_production": (
+            None if runtime is None else
+            round(1e6 / (QWEN3_8B_LAYERS * runtime["masked"]["us_per_call_wall"]), 2)),
         "roofline": {"bound": "hbm", "achieved": round(kern_gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic,

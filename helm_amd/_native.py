@@ -69,13 +69,13 @@ SIGNATURES = {
     "helm_paged_decode_attn": (ctypes.c_int, [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, ctypes.c_int,
         _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-        ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32, _f32, _c_void_p, _i64, _i64, _i64,
-        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p, _sz, _c_void_p]),
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p, _f32, _f32, _c_void_p, _i64, _i64,
+        _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p, _sz, _c_void_p]),
     "helm_paged_decode_attn_static": (ctypes.c_int, [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _c_void_p, ctypes.c_int,
         _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-        ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32, _f32, _c_void_p, _i64, _i64, _i64,
-        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p, _f32, _f32, _c_void_p, _i64, _i64,
+        _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _c_void_p]),
     "helm_stream_attn": (ctypes.c_int, [
         _c_void_p, _c_void_p, _c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_int, _c_void_p, _c_void_p, _f32, _f32, _c_void_p, _i64, _i64,

@@ -314,6 +314,10 @@ struct PageView {
 };
 
 // vLLM-style pool: slot s at base + s*slot_stride (bytes), int32 page table.
+// Sequences a call that numbers its splits compactly carries (PoolSrc,
+// DescSrc).
+constexpr int kSeqArgs = 16;
+
 struct PoolSrc {
   const char* k_pool;
   const char* v_pool;
@@ -324,6 +328,11 @@ struct PoolSrc {
   const int32_t* seq_lens;
   int page_size;
   int max_pages;  // table columns the caller declared; bounds every walk
+  // compact numbering (decode kernel, sequence lengths known on the host):
+  // blockIdx.x runs over every sequence's splits in turn, sequence b's first
+  // at seq_split0[b] (b < n_seq, ascending); no workgroup lacks a split
+  int compact, n_seq;
+  int seq_split0[kSeqArgs];
 
   __device__ __forceinline__ int n_pages(int b) const {
     const int T = sload(seq_lens + b);
@@ -377,7 +386,6 @@ struct PoolSrc {
 // in its arguments: then a page's used tokens are capped at the tokens the
 // sequence holds past the page's offset, so the last page's record may keep
 // its full capacity while tokens are appended to it.
-constexpr int kSeqArgs = 16;
 
 struct DescSrc {
   const helm_page* pages;

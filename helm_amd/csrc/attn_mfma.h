@@ -40,7 +40,8 @@
 namespace helm {
 
 constexpr int kMfmaRows = 16;     // query rows per tile (MFMA M dimension)
-constexpr int kMfmaMaxPps = 64;   // pages per split: page records live one per lane
+// pages per split: page records live one per lane, in two windows of 64
+constexpr int kMfmaMaxPps = 128;
 constexpr int kMfmaMaxSplits = 4096;
 constexpr float kMfmaSlack = 8.f;
 // Register buffers of the block pipeline: with two, one block's loads are in
@@ -361,16 +362,14 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   }
 
   int split_local = blockIdx.x, b = blockIdx.z;
-  if constexpr (std::is_same<Src, DescSrc>::value) {
-    if (src.compact) {
-      // the last sequence whose first split is at or before blockIdx.x
-      int bb = 0;
+  if (src.compact) {
+    // the last sequence whose first split is at or before blockIdx.x
+    int bb = 0;
 #pragma unroll
-      for (int j = 1; j < kSeqArgs; ++j)
-        if (j < src.n_seq && (int)blockIdx.x >= src.seq_split0[j]) bb = j;
-      b = bb;
-      split_local = blockIdx.x - src.seq_split0[bb];
-    }
+    for (int j = 1; j < kSeqArgs; ++j)
+      if (j < src.n_seq && (int)blockIdx.x >= src.seq_split0[j]) bb = j;
+    b = bb;
+    split_local = blockIdx.x - src.seq_split0[bb];
   }
   const int hk = blockIdx.y % p.Hkv;
   // the waves share one 16-row tile and split its blocks (query chunks with
@@ -386,6 +385,9 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   // (pg0 below equals this whenever the workgroup has pages to process)
   const typename LanesOf<Src>::type lanes =
       lane_pages(src, b, p.lo + split_local * p.pps, lane);
+  // a split of more than 64 pages: the records of its pages 64 .. 127
+  typename LanesOf<Src>::type lanes_hi{};
+  if (p.pps > 64 && !p.dyn) lanes_hi = lane_pages(src, b, p.lo + split_local * p.pps + 64, lane);
   // ---- query operand: row n of the tile at dim chunks 4i + q4 ---------------
   const bool row_ok = n < nrows;
   const int rr = r0 + (row_ok ? n : 0);
@@ -486,7 +488,8 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
     const bool valid = bi < nblk;
     const int pi = valid ? (p.bpp_log2 >= 0 ? bi >> p.bpp_log2 : bi / bpp) : 0;
     const int sub = valid ? bi - pi * bpp : 0;
-    const PageView pv = lane_page_view(src, lanes, b, pg0 + pi, pi, hk);
+    const PageView pv = pi < 64 ? lane_page_view(src, lanes, b, pg0 + pi, pi, hk)
+                                : lane_page_view(src, lanes_hi, b, pg0 + pi, pi - 64, hk);
     const int tok_in = sub * kBlockTok;
     const int ntok = valid ? sclamp(pv.used - tok_in, 0, kBlockTok) : 0;
     B.ntok = ntok;

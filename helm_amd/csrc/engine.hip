@@ -1056,8 +1056,8 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
                            int64_t head_stride, const int32_t* page_table,
                            int table_stride, const int32_t* seq_lens, int B,
                            int Hq, int Hkv, int q_len, int D, int page_size,
-                           int max_pages, int total_pages, float scale,
-                           float softcap, const void* mask,
+                           int max_pages, int total_pages, const int32_t* seq_lens_host,
+                           float scale, float softcap, const void* mask,
                            int64_t mask_bstride, int64_t mask_hstride,
                            int64_t mask_qstride, int mask_dtype, int kv_dtype, int q_dtype,
                            int pages_per_split, void* workspace,
@@ -1078,6 +1078,29 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
   int rc = make_plan(pl, kv_dtype, q_dtype, B, Hq, Hkv, q_len, D, page_size,
                      max_pages, avg, pages_per_split, al);
   if (rc != HELM_OK) return rc;
+  // the sequences' lengths on the host (a batch on the decode kernel): the
+  // split length from every sequence's page count and a grid of exactly
+  // their splits, as helm_paged_attn_seqs numbers them; the partial buffers
+  // keep the stride of the declared table width
+  int32_t seq_np[kSeqArgs];
+  bool compact = seq_lens_host && pl.mfma && !pl.row_waves && B > 1 && B <= kSeqArgs &&
+                 env_int("HELM_AMD_COMPACT", 1);
+  for (int b = 0; b < B && compact; ++b) {
+    const int64_t np = ((int64_t)seq_lens_host[b] + page_size - 1) / page_size;
+    seq_np[b] = (int32_t)std::min<int64_t>(np, max_pages);
+    compact = seq_lens_host[b] > 0;
+  }
+  if (compact) {
+    if (pages_per_split <= 0 && env_int("HELM_AMD_PPS", 0) <= 0) {
+      const int cand = batch_pps(seq_np, B, Hkv * pl.qblocks(), device_cus(),
+                                 min_pps(pl.bpp, pl.nw), max_pps_of(pl));
+      if ((max_pages + cand - 1) / cand <= max_splits_of(pl)) pl.pps = cand;
+    }
+    pl.max_splits = std::max(1, (max_pages + pl.pps - 1) / pl.pps);
+    pl.fused = fused_merge(pl.max_splits);
+    size_plan(pl, B, Hkv, D);
+    settle_fused(pl, B, Hkv);
+  }
   if (ws_bytes < pl.total())
     return fail(HELM_E_WORKSPACE,
                 "workspace too small: need " + std::to_string(pl.total()));
@@ -1107,6 +1130,16 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
   s.feat = (mask ? kFeatMask : 0) | (mask && mask_dtype != HELM_F32 ? kFeatMask16 : 0) |
            (softcap > 0.f ? kFeatCap : 0);
   s.grid = dim3(std::max(1, pl.max_splits), Hkv * pl.qblocks(), B);
+  if (compact) {
+    int all_splits = 0;
+    for (int b = 0; b < B; ++b) {
+      s.pool.seq_split0[b] = all_splits;
+      all_splits += (seq_np[b] + pl.pps - 1) / pl.pps;
+    }
+    s.pool.compact = 1;
+    s.pool.n_seq = B;
+    s.grid = dim3(all_splits, Hkv * pl.qblocks(), 1);
+  }
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t e = dispatch_timed(s, st);
   if (e != hipSuccess) return hip_fail(e, "paged_attn launch");
@@ -1120,7 +1153,8 @@ int helm_paged_decode_attn_static(const void* q, void* out, const void* k_pool,
                                   int64_t head_stride, const int32_t* page_table,
                                   int table_stride, const int32_t* seq_lens, int B,
                                   int Hq, int Hkv, int q_len, int D, int page_size,
-                                  int max_pages, int total_pages, float scale,
+                                  int max_pages, int total_pages,
+                                  const int32_t* seq_lens_host, float scale,
                                   float softcap, const void* mask,
                                   int64_t mask_bstride, int64_t mask_hstride,
                                   int64_t mask_qstride, int mask_dtype, int kv_dtype, int q_dtype,
@@ -1132,9 +1166,9 @@ int helm_paged_decode_attn_static(const void* q, void* out, const void* k_pool,
   if (rc != HELM_OK) return rc;
   rc = helm_paged_decode_attn(q, out, k_pool, v_pool, slot_stride, head_stride, page_table,
                               table_stride, seq_lens, B, Hq, Hkv, q_len, D, page_size,
-                              max_pages, total_pages, scale, softcap, mask, mask_bstride,
-                              mask_hstride, mask_qstride, mask_dtype, kv_dtype, q_dtype, pages_per_split,
-                              ws, HELM_STATIC_SCRATCH_BYTES, stream);
+                              max_pages, total_pages, seq_lens_host, scale, softcap, mask,
+                              mask_bstride, mask_hstride, mask_qstride, mask_dtype, kv_dtype,
+                              q_dtype, pages_per_split, ws, HELM_STATIC_SCRATCH_BYTES, stream);
   if (rc > 0) {
     // a launch failed part-way: the tickets may not be back at zero
     std::lock_guard<std::mutex> lock(g_scratch_mu);

@@ -10,8 +10,9 @@ the slot stride is ``2*Hkv*page*D`` elements and one page's head tile is
 from __future__ import annotations
 
 import math
-from typing import Dict, Optional, Tuple
+from typing import Dict, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from helm_amd import _native
@@ -64,12 +65,13 @@ def prepare_paged_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Te
                          scale: Optional[float] = None, softcap: Optional[float] = None,
                          out: Optional[torch.Tensor] = None,
                          pages_per_split: int = 0,
-                         attention_mask: Optional[torch.Tensor] = None) -> PreparedDecode:
+                         attention_mask: Optional[torch.Tensor] = None,
+                         host_lens: Optional[Sequence[int]] = None) -> PreparedDecode:
     """Validates the shapes once and returns a PreparedDecode bound to torch's
     current stream on q's device (same arguments as paged_decode_attention;
     the mask, if any, is read at every run)."""
     args, keep = _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages,
-                              scale, softcap, attention_mask, out, pages_per_split)
+                              scale, softcap, attention_mask, out, pages_per_split, host_lens)
     prep = PreparedDecode(args, 2, _native.load().helm_paged_decode_attn)
     prep.out = keep["out"]
     prep._keep = keep
@@ -82,21 +84,24 @@ def paged_decode_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
                            scale: Optional[float] = None, softcap: Optional[float] = None,
                            attention_mask: Optional[torch.Tensor] = None,
                            out: Optional[torch.Tensor] = None,
-                           pages_per_split: int = 0) -> torch.Tensor:
+                           pages_per_split: int = 0,
+                           host_lens: Optional[Sequence[int]] = None) -> torch.Tensor:
     """Decode attention of q [B,Hq,q_len,D] over pooled pages.
 
     k_pool / v_pool: [n_slots, Hkv, page, D] (any slot stride, dense rows);
     page_table: int32 [B, >=max_pages] slot ids; seq_lens: int32 [B] tokens
     (device).  attention_mask: additive fp32-convertible [B|1, 1|Hq, q_len|1,
-    >=max tokens].  Returns out [B,Hq,q_len,D] in q's dtype."""
+    >=max tokens].  host_lens: the same lengths as a host sequence (optional:
+    a batch then gets a grid of exactly its splits).  Returns out
+    [B,Hq,q_len,D] in q's dtype."""
     args, keep = _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages,
-                              scale, softcap, attention_mask, out, pages_per_split)
+                              scale, softcap, attention_mask, out, pages_per_split, host_lens)
     _native.call("helm_paged_decode_attn", *args)
     return keep["out"]
 
 
 def _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages, scale, softcap,
-                 attention_mask, out, pages_per_split):
+                 attention_mask, out, pages_per_split, host_lens=None):
     """Checks the operands and returns (C-ABI argument list, tensors to keep alive)."""
     if q.device.type != "cuda":
         raise RuntimeError("paged_decode_attention needs HIP tensors")
@@ -132,6 +137,11 @@ def _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages
         mbs = m.stride(0) if m.size(0) > 1 else 0
         mhs = m.stride(1) if m.size(1) > 1 else 0
         mqs = m.stride(2) if m.size(2) > 1 else 0
+    hl = None
+    if host_lens is not None:
+        hl = np.ascontiguousarray(np.asarray(host_lens, dtype=np.int32))
+        if hl.shape != (B,):
+            raise ValueError("host_lens must hold B lengths")
     kcode = _native.dtype_code(k_pool.dtype)
     qcode = _native.dtype_code(q.dtype)
     lib = _native.load()
@@ -139,9 +149,11 @@ def _decode_args(q, k_pool, v_pool, page_table, seq_lens, max_pages, total_pages
     ws = workspace(q.device, need)
     args = [q.data_ptr(), out.data_ptr(), k_pool.data_ptr(), v_pool.data_ptr(), k_pool.stride(0),
             k_pool.stride(1), page_table.data_ptr(), page_table.stride(0), seq_lens.data_ptr(), B,
-            Hq, Hkv, S, D, P, max_pages, total_pages, float(scale),
+            Hq, Hkv, S, D, P, max_pages, total_pages,
+            _native.ptr(hl) if hl is not None else None, float(scale),
             float(softcap) if softcap else 0.0, mask_ptr, mbs, mhs, mqs,
             _native.dtype_code(m.dtype) if m is not None else _native.HELM_F32, kcode, qcode,
             pages_per_split, ws.data_ptr(), ws.numel(), _engine.stream_ptr(q.device)]
-    keep = {"q": q, "out": out, "mask": m, "ws": ws, "table": page_table, "lens": seq_lens}
+    keep = {"q": q, "out": out, "mask": m, "ws": ws, "table": page_table, "lens": seq_lens,
+            "host_lens": hl}
     return args, keep

@@ -1239,6 +1239,7 @@ def _decode_step_fast(kvcms, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     B, Hq, S, D = q.shape
     kv_code = _KV16.get(q.dtype)
     if (kv_code is None or S != 1 or D != 128 or B > _native.DECODE_MAX_SEQS
+            or Hq > 16 * k.shape[1]             # more than one 16-row tile per KV head
             or q.device.type != "cuda" or k.dtype is not q.dtype or v.dtype is not q.dtype
             or not q.is_contiguous()):
         return None

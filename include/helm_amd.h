@@ -127,6 +127,11 @@ size_t helm_query_workspace_bytes(int B, int Hq, int Hkv, int q_len, int D,
  * (device array), every page but the last is full (page_size tokens).
  * pages_per_split <= 0 picks the split automatically; total_pages is an
  * optional hint (sum over b of pages, 0 = unknown) for that choice.
+ * seq_lens_host (may be NULL) holds the same B lengths as seq_lens in host
+ * memory: a batch of 2..16 sequences then gets a split length chosen from
+ * every sequence's page count and a grid of exactly its splits (no
+ * workgroup of a short sequence without a split).  Lengths that differ from
+ * seq_lens give wrong results (never an access outside the buffers).
  * softcap <= 0 disables the tanh soft-cap; mask may be NULL. */
 int helm_paged_decode_attn(const void* q, void* out,
                            const void* k_pool, const void* v_pool,
@@ -135,7 +140,7 @@ int helm_paged_decode_attn(const void* q, void* out,
                            const int32_t* seq_lens,
                            int B, int Hq, int Hkv, int q_len, int D,
                            int page_size, int max_pages, int total_pages,
-                           float scale, float softcap,
+                           const int32_t* seq_lens_host, float scale, float softcap,
                            const void* mask, int64_t mask_bstride,
                            int64_t mask_hstride, int64_t mask_qstride, int mask_dtype,
                            int kv_dtype, int q_dtype, int pages_per_split,
@@ -162,7 +167,7 @@ int helm_paged_decode_attn_static(const void* q, void* out,
                                   const int32_t* seq_lens,
                                   int B, int Hq, int Hkv, int q_len, int D,
                                   int page_size, int max_pages, int total_pages,
-                                  float scale, float softcap,
+                                  const int32_t* seq_lens_host, float scale, float softcap,
                                   const void* mask, int64_t mask_bstride,
                                   int64_t mask_hstride, int64_t mask_qstride, int mask_dtype,
                                   int kv_dtype, int q_dtype, int pages_per_split,

@@ -518,3 +518,25 @@ def test_golden_fixtures_on_the_gpu(name, kernel):
     torch.cuda.synchronize()
     err = (out.double().cpu() - torch.from_numpy(z["out"])).abs().max().item()
     assert err <= meta["atol"], err
+
+
+@pytest.mark.parametrize("merge", ["auto", "fused"])
+def test_pool_entry_with_host_lengths(merge, monkeypatch):
+    """The ragged Qwen3-14B batch through the pool entry point with the
+    lengths also given on the host: the grid holds exactly the sequences'
+    splits; every sequence within tolerance of fp64, as without them."""
+    monkeypatch.setenv("HELM_AMD_MERGE", merge)
+    w = W.WORKLOADS["qwen3-14b-ragged-b8"]
+    case = W.make_pool_case(w, seed=23, device=DEV)
+    args = dict(max_pages=case["max_pages"], total_pages=sum(case["n_pages"]))
+    out_h = paged_decode_attention(case["q"], case["k_pool"], case["v_pool"], case["table"],
+                                   case["lens"], host_lens=case["lens_list"], **args)
+    out_d = paged_decode_attention(case["q"], case["k_pool"], case["v_pool"], case["table"],
+                                   case["lens"], **args)
+    torch.cuda.synchronize()
+    G = w.Hq // w.Hkv
+    for b in range(w.B):
+        ref = _pool_reference(case, w, b)
+        for out in (out_h, out_d):
+            err = (out[b].double().cpu() - ref).abs().max().item()
+            assert err <= TOL[w.dtype], (b, err)

@@ -75,7 +75,7 @@ def test_argument_errors_raise_before_device_work():
         _native.check("helm_page_append", rc)
     # null pointers in the pool entry point are rejected
     rc = lib.helm_paged_decode_attn(None, None, None, None, 0, 0, None, 0, None, 1, 32, 8, 1,
-                                    128, 16, 1, 0, 1.0, 0.0, None, 0, 0, 0, 2, 1, 1, 0, None, 0,
+                                    128, 16, 1, 0, None, 1.0, 0.0, None, 0, 0, 0, 2, 1, 1, 0, None, 0,
                                     None)
     assert rc == _native.HELM_E_INVALID
 

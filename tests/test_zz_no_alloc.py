@@ -84,7 +84,7 @@ def test_static_scratch_call_equals_workspace_call_then_smaller_call():
     rc = lib.helm_paged_decode_attn_static(
         q.data_ptr(), out.data_ptr(), pool[:, 0].data_ptr(), pool[:, 1].data_ptr(),
         pool.stride(0), pool.stride(2), table.data_ptr(), maxp, lens.data_ptr(), Bq, Hq, Hkv,
-        1, D, 16, maxp, 0, 1.0, 0.0, None, 0, 0, 0, _native.HELM_F32, _native.HELM_BF16, _native.HELM_BF16, 0,
+        1, D, 16, maxp, 0, None, 1.0, 0.0, None, 0, 0, 0, _native.HELM_F32, _native.HELM_BF16, _native.HELM_BF16, 0,
         None)
     assert rc == _native.HELM_E_WORKSPACE
     assert b"static scratch" in lib.helm_last_error_string()
