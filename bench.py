@@ -308,7 +308,16 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
     kcode = _native.dtype_code(w.dtype)
     host = torch.empty((n_host, 2, w.Hkv, w.page_size, w.D), dtype=w.dtype).pin_memory()
     table = case["table_cpu"][0, :n].long()
-    host.copy_(case["pool"][table[:n_host].to(dev)].cpu())
+    eng = engine.get_engine(dev)
+    # the host pages are written as the runtime evicts them: one engine
+    # eviction (device -> pinned host), which the side-stream staging copies
+    # are ordered after by its event
+    cold = case["pool"][table[:n_host].to(dev)].contiguous()
+    reg = [np.array([x], dtype=np.uint64)
+           for x in (cold.data_ptr(), host.data_ptr(), cold.numel() * cold.element_size())]
+    _native.call("helm_evict_pages", eng, 1, _native.ptr(reg[0]), _native.ptr(reg[1]),
+                 _native.ptr(reg[2]), 1, torch.cuda.current_stream(dev).cuda_stream)
+    del cold
     pages = np.zeros(n, dtype=_native.PAGE_DTYPE)
     for j in range(n):
         if j < n_host:
@@ -320,7 +329,6 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
         pages[j] = (base, base + slot_b // 2, w.page_size, j * w.page_size,
                     w.page_size * w.D, flags)
     seq_off = np.array([0, n], dtype=np.int32)
-    eng = engine.get_engine(dev)
     out = torch.empty_like(case["q"])
     stream = torch.cuda.current_stream(dev)
 
@@ -331,10 +339,14 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
 
     steps = steps or args.offload_steps
 
-    def timed(**env):
+    host_calls = {}
+
+    def timed(label, **env):
         """Seconds per call under `env` (engine switches, read per call): the
         best of three timed runs, so that a rare host stall of a few
-        milliseconds in one run does not stand for the steady state."""
+        milliseconds in one run does not stand for the steady state.  The
+        host time of each call of every run (issue, including any wait
+        inside it) is kept under `label`."""
         saved = {k: os.environ.pop(k, None)
                  for k in ("HELM_AMD_HOST_READ", "HELM_AMD_STAGE_STREAM")}
         os.environ.update(env)
@@ -343,16 +355,24 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
                 call()
             torch.cuda.synchronize()
             best = None
+            host = []
             for _ in range(3):
                 e0 = torch.cuda.Event(enable_timing=True)
                 e1 = torch.cuda.Event(enable_timing=True)
                 e0.record(stream)
                 for _ in range(steps):
+                    h0 = time.perf_counter()
                     call()
+                    host.append((time.perf_counter() - h0) * 1e6)
                 e1.record(stream)
                 torch.cuda.synchronize()
                 t = e0.elapsed_time(e1) / 1e3 / steps
                 best = t if best is None else min(best, t)
+            host.sort()
+            host_calls[label] = {"median": round(host[len(host) // 2], 1),
+                                 "p90": round(host[(9 * len(host)) // 10], 1),
+                                 "max": round(host[-1], 1),
+                                 "over_5ms": sum(h > 5000 for h in host), "calls": len(host)}
             return best
         finally:
             for k in env:
@@ -360,15 +380,17 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
             os.environ.update({k: v for k, v in saved.items() if v is not None})
 
     # host pages staged through the device ring by hipMemcpyAsync (copies on
-    # the engine's side stream overlapped with the device pages' launch, or
-    # on the caller's stream after it), read in place by the kernel over the
+    # the engine's side stream, which wait only for the eviction and for the
+    # earlier readers of their ring slots, overlapped with the device pages'
+    # launch and the earlier calls' kernels; or on the caller's stream after
+    # the device pages' launch), read in place by the kernel over the
     # host link, and the engine's default (per call: pages in long address
     # runs are staged, copies on the caller's stream)
-    per_staged = timed(HELM_AMD_HOST_READ="copy")
-    per_side = timed(HELM_AMD_HOST_READ="copy", HELM_AMD_STAGE_STREAM="side")
-    per_one = timed(HELM_AMD_HOST_READ="copy", HELM_AMD_STAGE_STREAM="one")
-    per_direct = timed(HELM_AMD_HOST_READ="direct")
-    per = timed()
+    per_staged = timed("staged", HELM_AMD_HOST_READ="copy")
+    per_side = timed("staged_side_stream", HELM_AMD_HOST_READ="copy", HELM_AMD_STAGE_STREAM="side")
+    per_one = timed("staged_one_stream", HELM_AMD_HOST_READ="copy", HELM_AMD_STAGE_STREAM="one")
+    per_direct = timed("in_place", HELM_AMD_HOST_READ="direct")
+    per = timed("default")
     host_bytes = n_host * slot_b
     peak = h2d_peak(torch)
     # parity spot check of this exact configuration against the oracle
@@ -396,6 +418,9 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
         "timing": f"best of 3 runs of {steps} calls after 3 warm-up calls",
         "in_place_ms_per_call": per_direct * 1e3,
         "in_place_host_link_GBs": host_bytes / per_direct / 1e9,
+        "host_us_per_call": host_calls,
+        "host_us_per_call_how": "host time of each helm_stream_attn call (issue and any wait "
+                                "inside the HIP runtime), over the 3 timed runs of each mode",
     }
 
 

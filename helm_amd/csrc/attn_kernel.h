@@ -28,6 +28,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "helm_amd.h"
 
 namespace helm {
@@ -537,11 +539,12 @@ struct MaskRow {
     return MaskRow{base + i * (dt == HELM_F32 ? 4 : 2), dt};
   }
   // element i's bits, for an element type known at compile time (K16: a
-  // 16-bit mask, zero-extended); widened where the value is used
+  // 16-bit mask); widened where the value is used
   template <bool K16>
-  __device__ __forceinline__ uint32_t bits(int64_t i) const {
+  __device__ __forceinline__ typename std::conditional<K16, uint16_t, uint32_t>::type bits(
+      int64_t i) const {
     if constexpr (K16) return reinterpret_cast<const uint16_t*>(base)[i];
-    return reinterpret_cast<const uint32_t*>(base)[i];
+    else return reinterpret_cast<const uint32_t*>(base)[i];
   }
   template <bool K16>
   __device__ __forceinline__ float widen(uint32_t x) const {

@@ -479,7 +479,10 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
   struct Blk {
     mf_u32x4 k[4];
     mf_u32x4 v[4];
-    uint32_t mk[4];  // mask elements as loaded (widened when used)
+    // mask elements as loaded, at their width (a 16-bit mask kept as 16-bit
+    // values: zero-extending them would be an instruction on each loaded
+    // register, placed where the next step's loads must have completed)
+    typename std::conditional<kMask16, uint16_t, uint32_t>::type mk[4];
     int ntok;   // valid tokens of the block (0: past the end)
     int tok0;   // HELM token cursor of the block's first token
   };
@@ -673,13 +676,25 @@ __global__ __launch_bounds__(64 * NW) void decode_mfma_kernel(AttnParams p, Src 
     Blk buf[NB];
 #pragma unroll
     for (int i = 0; i < NB - 1; ++i) load_block(wave + i * NW, buf[i]);
-    for (int k = 0; k < nmine; k += NB) {
+    // Whole rounds of NB blocks, then the remaining blocks: an exit inside
+    // the unrolled round would join register states the compiler can only
+    // reconcile by waiting for every load in flight.  The scheduling barrier
+    // keeps each step's loads ahead of its compute, so the wait for the
+    // block computed covers that block's loads only.
+    int k = 0;
+    for (; k + NB <= nmine; k += NB) {
 #pragma unroll
       for (int u = 0; u < NB; ++u) {
-        if (k + u >= nmine) break;
         load_block(wave + (k + u + NB - 1) * NW, buf[(u + NB - 1) % NB]);
+        __builtin_amdgcn_sched_barrier(0);
         compute_block(buf[u]);
       }
+    }
+#pragma unroll
+    for (int u = 0; u < NB - 1; ++u) {
+      if (k + u >= nmine) break;
+      load_block(wave + (k + u + NB - 1) * NW, buf[(u + NB - 1) % NB]);
+      compute_block(buf[u]);
     }
   }
 

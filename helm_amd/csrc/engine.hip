@@ -17,6 +17,8 @@
 #include "front.h"
 #include "helm_amd.h"
 
+extern char** environ;
+
 namespace helm {
 namespace {
 
@@ -68,8 +70,59 @@ int device_cus() {
   return cus;
 }
 
+// The HELM_AMD_* switches, read per call.  getenv scans the whole
+// environment for each name, and one call plans with about ten of them, so
+// every public entry point that plans a launch opens an EnvScope: one pass
+// over the environment keeps this thread's HELM_AMD_* entries, and env_get
+// looks names up among those until the scope closes.  Outside a scope (or
+// with more entries than the table holds) env_get is getenv.
+struct EnvSnap {
+  static constexpr int kMax = 32;
+  bool active = false;
+  int n = 0;
+  const char* entry[kMax];  // "NAME=value" strings of the environment
+};
+thread_local EnvSnap g_env;
+
+class EnvScope {
+ public:
+  EnvScope() : outer_(!g_env.active) {
+    if (!outer_) return;
+    int n = 0;
+    bool fits = true;
+    for (char** e = environ; e && *e; ++e) {
+      if (std::strncmp(*e, "HELM_AMD_", 9) != 0) continue;
+      if (n == EnvSnap::kMax) {
+        fits = false;
+        break;
+      }
+      g_env.entry[n++] = *e;
+    }
+    g_env.n = n;
+    g_env.active = fits;
+  }
+  ~EnvScope() {
+    if (outer_) g_env.active = false;
+  }
+  EnvScope(const EnvScope&) = delete;
+  EnvScope& operator=(const EnvScope&) = delete;
+
+ private:
+  bool outer_;
+};
+
+const char* env_get(const char* name) {
+  if (!g_env.active) return std::getenv(name);
+  const size_t len = std::strlen(name);
+  for (int i = 0; i < g_env.n; ++i) {
+    const char* e = g_env.entry[i];
+    if (std::strncmp(e, name, len) == 0 && e[len] == '=') return e + len + 1;
+  }
+  return nullptr;
+}
+
 int env_int(const char* name, int dflt) {
-  const char* v = std::getenv(name);
+  const char* v = env_get(name);
   if (!v || !*v) return dflt;
   return std::atoi(v);
 }
@@ -119,14 +172,14 @@ int mfma_waves() { return env_int("HELM_AMD_WAVES", 4) == 8 ? 8 : 4; }
 // 11.3, 12.7 vs 13.4, 17.4 vs 17.8.  HELM_AMD_MERGE = fused | kernel forces one.
 constexpr int kFusedMaxSplits = 16;
 int fused_merge(int max_splits) {
-  const char* v = std::getenv("HELM_AMD_MERGE");
+  const char* v = env_get("HELM_AMD_MERGE");
   if (v && !std::strcmp(v, "kernel")) return 0;
   if (v && !std::strcmp(v, "fused")) return 1;
   return max_splits <= kFusedMaxSplits ? 1 : 0;
 }
 
 int kernel_choice() {
-  const char* v = std::getenv("HELM_AMD_KERNEL");
+  const char* v = env_get("HELM_AMD_KERNEL");
   if (!v || !*v || !std::strcmp(v, "auto") || !std::strcmp(v, "mfma")) return 2;
   if (!std::strcmp(v, "valu")) return 1;
   return 0;
@@ -597,6 +650,14 @@ struct helm_engine {
   // per ring slot: its copies are complete (recorded on `copy`) / the launch
   // that reads it is complete (recorded on the caller's stream)
   std::vector<hipEvent_t> slot_ready, slot_free;
+  // per ring slot, how its last reader was ordered: 0 none since the ring was
+  // allocated, 1 slot_free recorded after it, 2 on the caller's stream only
+  std::vector<uint8_t> slot_reader;
+  // the last helm_evict_pages call's copies are complete (each eviction on a
+  // new stream first waits for the previous one, so it covers them all)
+  hipEvent_t evict_done = nullptr;
+  hipStream_t evict_stream = nullptr;
+  bool evict_recorded = false;
   // descriptor uploads (pinned host -> device), a ring so the host can run ahead
   static constexpr int kUp = 8;
   char* up_host[kUp] = {};
@@ -678,6 +739,7 @@ int engine_ensure_ring(helm_engine* e, size_t min_chunk) {
   e->ring = nullptr;
   e->chunk_bytes = align_up(std::max(min_chunk, e->chunk_bytes), 1 << 20);
   HELM_HIP(hipMalloc(&e->ring, e->chunk_bytes * e->ring_slots));
+  e->slot_reader.assign(e->ring_slots, 0);
   return HELM_OK;
 }
 
@@ -691,7 +753,7 @@ int engine_ensure_ring(helm_engine* e, size_t min_chunk) {
 // HELM_AMD_HOST_READ: "copy" stages every host page, "direct" reads every
 // readable one in place, default "auto" decides per call (host_runs_favor_copy).
 int host_read_mode() {
-  const char* e = std::getenv("HELM_AMD_HOST_READ");
+  const char* e = env_get("HELM_AMD_HOST_READ");
   if (e && std::strcmp(e, "copy") == 0) return 0;
   if (e && std::strcmp(e, "direct") == 0) return 2;
   return 1;
@@ -699,17 +761,11 @@ int host_read_mode() {
 
 bool host_read_in_place() { return host_read_mode() != 0; }
 
-// Where a call's staging copies go.  On the engine's side stream
+// Where a call's staging copies go: on the engine's side stream
 // (HELM_AMD_STAGE_STREAM=side) they run while the device pages' launch runs
-// on the caller's stream, but the two joins (side stream after the caller's
-// earlier work, chunk launch after its copies) cost more than that overlap
-// wins here: Qwen3-8B 32k with 50% in host (67 MB of device pages) 1.25 ms
-// per call on one stream, 1.29-1.38 with the side stream (1.86-1.96 inside
-// full bench runs);
-// Llama-2-13B 128k with 75% in host (671 MB) 36.4-37.0 ms on one stream,
-// 36.7-37.4 with the side stream.  So the default is the caller's stream.
+// on the caller's stream, or (the default) on the caller's stream.
 bool stage_on_side_stream() {
-  const char* e = std::getenv("HELM_AMD_STAGE_STREAM");
+  const char* e = env_get("HELM_AMD_STAGE_STREAM");
   return e && std::strcmp(e, "side") == 0;
 }
 
@@ -947,6 +1003,9 @@ int helm_engine_create(int device, size_t chunk_bytes, int ring_slots,
       "hipEventCreate");
   chk(hipEventCreateWithFlags(&e->ev_b, hipEventDisableTiming),
       "hipEventCreate");
+  chk(hipEventCreateWithFlags(&e->evict_done, hipEventDisableTiming),
+      "hipEventCreate");
+  e->slot_reader.assign(e->ring_slots, 0);
   e->slot_ready.assign(e->ring_slots, nullptr);
   e->slot_free.assign(e->ring_slots, nullptr);
   for (int i = 0; i < e->ring_slots; ++i) {
@@ -1013,6 +1072,7 @@ int helm_engine_destroy(helm_engine* e) {
   }
   if (e->ev_a) (void)hipEventDestroy(e->ev_a);
   if (e->ev_b) (void)hipEventDestroy(e->ev_b);
+  if (e->evict_done) (void)hipEventDestroy(e->evict_done);
   for (hipEvent_t ev : e->slot_ready)
     if (ev) (void)hipEventDestroy(ev);
   for (hipEvent_t ev : e->slot_free)
@@ -1062,6 +1122,7 @@ int helm_paged_decode_attn(const void* q, void* out, const void* k_pool,
                            int64_t mask_qstride, int mask_dtype, int kv_dtype, int q_dtype,
                            int pages_per_split, void* workspace,
                            size_t ws_bytes, void* stream) {
+  EnvScope env_scope;
   if (!q || !out || !k_pool || !v_pool || !page_table || !seq_lens ||
       !workspace)
     return fail(HELM_E_INVALID, "null pointer argument");
@@ -1159,6 +1220,7 @@ int helm_paged_decode_attn_static(const void* q, void* out, const void* k_pool,
                                   int64_t mask_bstride, int64_t mask_hstride,
                                   int64_t mask_qstride, int mask_dtype, int kv_dtype, int q_dtype,
                                   int pages_per_split, void* stream) {
+  EnvScope env_scope;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   int dev = -1;
   void* ws = nullptr;
@@ -1188,6 +1250,7 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
                      const void* mask, int64_t mask_bstride,
                      int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int causal,
                      int kv_dtype, int q_dtype, void* stream) {
+  EnvScope env_scope;
   if (!eng || !q || !out || !seq_off)
     return fail(HELM_E_INVALID, "null pointer argument");
   if (B <= 0) return fail(HELM_E_INVALID, "B must be positive");
@@ -1438,18 +1501,25 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   // side stream while the caller's stream runs the device pages' launch and
   // then, chunk by chunk, the launch that reads each one: chunk c's launch
   // waits for chunk c's copies only, so the host link stays busy while the
-  // kernels run.  The side stream first waits for everything queued on the
-  // caller's stream before this call (the evictions that wrote the host
-  // pages, and the earlier calls' readers of the ring), and a slot's next
-  // copy waits for the launch that read it.  Events carry no timestamps.
-  // Without the side stream (the default) every copy is queued on the
-  // caller's stream in launch order.
+  // kernels run.  Once this engine has evicted pages (helm_evict_pages), the
+  // side stream waits only for what its copies depend on: the last eviction
+  // (the copies that wrote host pages) and, per ring slot, the launch that
+  // last read it (in this call or an earlier one), so a call's copies may
+  // start while the earlier calls' kernels still run; host pages written by
+  // other means must then be complete when the call is made.  Before the
+  // first eviction, or when a slot was last read by a launch of the default
+  // mode (which records no event), the side stream first waits for
+  // everything queued on the caller's stream before this call.  Events carry
+  // no timestamps.  Without the side stream (the default) every copy is
+  // queued on the caller's stream in launch order.
   const bool side = stage_on_side_stream();
   const int n_chunks = (int)chunk_runs.size();
   auto issue_copies = [&](int c) -> int {
     const int slot = chunk_slot[c];
     char* dst = eng->ring + (size_t)slot * eng->chunk_bytes;
     hipStream_t cs = side ? eng->copy : st;
+    if (side && eng->slot_reader[slot] == 1)
+      HELM_HIP(hipStreamWaitEvent(eng->copy, eng->slot_free[slot], 0));
     for (const Run& r : chunk_runs[c])
       HELM_HIP(hipMemcpyAsync(dst + r.dst_off, reinterpret_cast<const void*>(r.src), r.bytes,
                               hipMemcpyHostToDevice, cs));
@@ -1458,8 +1528,16 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   };
   int issued = 0;
   if (side) {
-    HELM_HIP(hipEventRecord(eng->ev_a, st));
-    HELM_HIP(hipStreamWaitEvent(eng->copy, eng->ev_a, 0));
+    bool join_all = !eng->evict_recorded;
+    for (int c = 0; c < n_chunks && c < eng->ring_slots; ++c)
+      join_all = join_all || eng->slot_reader[chunk_slot[c]] == 2;
+    if (join_all) {
+      HELM_HIP(hipEventRecord(eng->ev_a, st));
+      HELM_HIP(hipStreamWaitEvent(eng->copy, eng->ev_a, 0));
+      for (int c = 0; c < n_chunks && c < eng->ring_slots; ++c)
+        eng->slot_reader[chunk_slot[c]] = 0;
+    }
+    if (eng->evict_recorded) HELM_HIP(hipStreamWaitEvent(eng->copy, eng->evict_done, 0));
     for (; issued < n_chunks && issued < eng->ring_slots; ++issued) {
       rc = issue_copies(issued);
       if (rc != HELM_OK) return rc;
@@ -1484,10 +1562,12 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
     }
     hipError_t e = dispatch(s, st);
     if (e != hipSuccess) return hip_fail(e, "stream_attn chunk launch");
+    if (L.chunk >= 0) {
+      if (side) HELM_HIP(hipEventRecord(eng->slot_free[slot], st));
+      eng->slot_reader[slot] = side ? 1 : 2;
+    }
     if (side && L.chunk >= 0 && issued < n_chunks) {
       // the next chunk for this slot (chunks take the slots in turn)
-      HELM_HIP(hipEventRecord(eng->slot_free[slot], st));
-      HELM_HIP(hipStreamWaitEvent(eng->copy, eng->slot_free[slot], 0));
       rc = issue_copies(issued++);
       if (rc != HELM_OK) return rc;
     }
@@ -1619,6 +1699,7 @@ int helm_paged_attn_seqs(helm_engine* eng, const void* q, void* out, int B,
                          const void* mask, int64_t mask_bstride,
                          int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int causal,
                          int kv_dtype, int q_dtype, void* stream) {
+  EnvScope env_scope;
   return paged_attn_seqs(eng, q, out, B, Hq, Hkv, q_len, D, seq_pages, seq_npages, seq_tokens,
                          page_tokens, aligned16, scale, softcap, mask, mask_bstride,
                          mask_hstride, mask_qstride, mask_dtype, causal, kv_dtype, q_dtype, nullptr,
@@ -1632,6 +1713,7 @@ int helm_paged_attn_seqs_append(helm_engine* eng, const void* q, void* out, int 
                                 const void* mask, int64_t mask_bstride,
                                 int64_t mask_hstride, int64_t mask_qstride, int mask_dtype, int kv_dtype,
                                 const helm_append_seg* tokens, void* stream) {
+  EnvScope env_scope;
   if (!tokens) return fail(HELM_E_INVALID, "null pointer argument");
   return paged_attn_seqs(eng, q, out, B, Hq, Hkv, 1, D, seq_pages, seq_npages, seq_tokens,
                          page_tokens, aligned16, scale, softcap, mask, mask_bstride,
@@ -1641,6 +1723,7 @@ int helm_paged_attn_seqs_append(helm_engine* eng, const void* q, void* out, int 
 static_assert(sizeof(helm_decode_args) == 744, "helm_decode_args layout (helm_amd/_native.py)");
 
 int helm_decode_step(helm_engine* eng, const helm_decode_args* a) {
+  EnvScope env_scope;
   if (!a) return fail(HELM_E_INVALID, "null pointer argument");
   if (a->B <= 0 || a->B > HELM_DECODE_MAX_SEQS)
     return fail(HELM_E_UNSUPPORTED, "B must be in [1, " +
@@ -1690,6 +1773,7 @@ int helm_upload(helm_engine* eng, void* dst, const void* src, size_t bytes,
 
 int helm_host_pages_in_place(helm_engine* eng, const helm_page* pages, int n,
                              int Hkv, int D, int kv_dtype, uint8_t* in_place) {
+  EnvScope env_scope;
   if (!eng || (n > 0 && (!pages || !in_place)))
     return fail(HELM_E_INVALID, "null pointer argument");
   if (n < 0 || Hkv <= 0 || D <= 0) return fail(HELM_E_INVALID, "bad shape");
@@ -1809,9 +1893,16 @@ int helm_evict_pages(helm_engine* eng, int n, const uint64_t* src_dev,
   if (!eng) return fail(HELM_E_INVALID, "null engine");
   if (n > 0 && (!src_dev || !dst_host || !bytes))
     return fail(HELM_E_INVALID, "null region arrays");
-  return engine_copies(eng, n, src_dev, dst_host, bytes,
-                       hipMemcpyDeviceToHost, sync,
-                       reinterpret_cast<hipStream_t>(stream));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (n > 0 && eng->evict_recorded && st != eng->evict_stream)
+    HELM_HIP(hipStreamWaitEvent(st, eng->evict_done, 0));
+  int rc = engine_copies(eng, n, src_dev, dst_host, bytes, hipMemcpyDeviceToHost, sync, st);
+  if (rc != HELM_OK || n <= 0) return rc;
+  // side-stream staging copies wait for this event, not for the whole stream
+  HELM_HIP(hipEventRecord(eng->evict_done, st));
+  eng->evict_stream = st;
+  eng->evict_recorded = true;
+  return HELM_OK;
 }
 
 int helm_prefetch_pages(helm_engine* eng, int n, const uint64_t* src_host,

@@ -62,6 +62,9 @@ RUNS = collections.OrderedDict([
                   400)),
     ("fetch", (["--pmc", "FETCH_SIZE"], _PMC_DECODE, 150)),
     ("write", (["--pmc", "WRITE_SIZE"], _PMC_DECODE, 150)),
+    ("copies", (["--kernel-trace", "--memory-copy-trace"],
+                ["--no-configs", "--no-runtime", "--no-full-step", "--no-prefill", "--no-gemv",
+                 "--no-cpu", "--offload-steps", "5"], 300)),
     ("pmc_a", (["--pmc"] + _PMC_A, _PREFILL_ONLY, 150)),
     ("pmc_b", (["--pmc"] + _PMC_B, _PREFILL_ONLY, 150)),
 ])
@@ -270,6 +273,39 @@ def traffic(fetch_paths, write_paths, alg_bytes: int, decode: str, merge: str,
             "decode_traffic_over_algorithmic": (dfb + dwb) / alg_bytes}
 
 
+def copy_runs(paths: Iterable[str], min_us: float = 500.0) -> List[dict]:
+    """Runs of large host-to-device copies (at least `min_us` each) from
+    ``*_memory_copy_trace.csv``: consecutive copies on one stream form a run;
+    per run its stream, start (ms after the first large copy), copy count,
+    median copy duration and median start-to-start interval (the call's
+    cycle when each call makes one such copy)."""
+    big = []
+    for path in _csvs(paths, "_memory_copy_trace.csv"):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                a, b = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+                if "HOST_TO_DEVICE" in r["Direction"] and (b - a) / 1e3 >= min_us:
+                    big.append((r["Stream_Id"], a, b))
+    big.sort(key=lambda x: x[1])
+    runs: List[dict] = []
+    for stream, a, b in big:
+        if runs and runs[-1]["stream"] == stream and a - runs[-1]["_last"] < 5e6:
+            runs[-1]["_copies"].append((a, b))
+            runs[-1]["_last"] = a
+        else:
+            runs.append({"stream": stream, "_first": a, "_last": a, "_copies": [(a, b)]})
+    t0 = big[0][1] if big else 0
+    out = []
+    for r in runs:
+        cs = r["_copies"]
+        dur = [(y - x) / 1e3 for x, y in cs]
+        cyc = [(y[0] - x[0]) / 1e3 for x, y in zip(cs, cs[1:])]
+        out.append({"stream": r["stream"], "start_ms": round((r["_first"] - t0) / 1e6, 1),
+                    "copies": len(cs), "copy_us_median": round(statistics.median(dur), 1),
+                    "cycle_us_median": round(statistics.median(cyc), 1) if cyc else None})
+    return out
+
+
 def counters_md(means: dict, kernels: str, title: str, commands: List[str]) -> str:
     lines = [f"# {title}", "", "Commands (repo root `R`, from `/tmp` with `TMPDIR=/tmp`):", "",
              "```", *commands, "```", "",
@@ -358,6 +394,29 @@ def write_all(in_dir: str, out_dir: str, alg_bytes: int = 134242304) -> List[str
               f"* whole call: {t['hbm_bytes_per_launch']:,.0f} B, "
               f"x{t['traffic_over_algorithmic']:.4f}"]
         put("paged_decode_qwen3-8b-32k_traffic.md", "\n".join(md) + "\n")
+    if have("copies"):
+        runs = copy_runs([os.path.join(in_dir, "copies")])
+        md = ["# Host-to-device copies of the Qwen3-8B 32k call with 50% of its pages in "
+              "pinned host memory", "",
+              "Command (repo root `R`, from `/tmp` with `TMPDIR=/tmp`):", "", "```",
+              command_of("copies"), "```", "",
+              "Runs of consecutive large (>= 0.5 ms) host-to-device copies on one stream, in "
+              "the order the bench makes them: the device profile's 64 MiB link probe (its "
+              "own stream), then the offload leg's modes, each call copying its 64 MiB of "
+              "host pages in one copy (3 warm-up calls and 3 timed runs per mode): forced "
+              "staging (HELM_AMD_HOST_READ=copy, copies on the caller's stream), the side "
+              "stream (HELM_AMD_STAGE_STREAM=side: the engine's copy stream), one stream "
+              "(=one, the same as forced staging), the engine default (which stages this "
+              "one-run layout; the in-place mode before it copies nothing), and the bench's "
+              "256 MiB pinned-copy peak.  A call's cycle is its copy plus whatever its "
+              "copy waits for; on one stream that includes the previous call's kernels.  "
+              "`python -m helm_amd.rocprof_report all` on the run directory.", "",
+              "| Stream | Starts (ms) | Copies | Copy (us, median) | Start to start (us, "
+              "median) |", "|---|---:|---:|---:|---:|"]
+        for r in runs:
+            md.append(f"| {r['stream']} | {r['start_ms']} | {r['copies']} | "
+                      f"{r['copy_us_median']} | {r['cycle_us_median']} |")
+        put("offload_qwen3-8b-32k-offload50_copies.md", "\n".join(md) + "\n")
     if have("pmc_a") or have("pmc_b"):
         dirs = [os.path.join(in_dir, d) for d in ("pmc_a", "pmc_b") if have(d)]
         means = counter_means(counter_rows(dirs))

@@ -23,6 +23,7 @@ from __future__ import annotations
 import heapq
 import math
 import os
+import struct
 import threading
 import weakref
 from dataclasses import dataclass
@@ -345,10 +346,28 @@ class LayerKVCache:
                                    f"from the host record ({dev[bad[0]]} vs {host[bad[0]]})")
 
 
+_ENV_DATA = getattr(os.environ, "_data", None)
+_ENV_KEYS: dict = {}
+
+
+def _env_get(name: str) -> Optional[str]:
+    """``os.environ.get(name)`` for the switches read on every decode call,
+    without its per-call key encoding: CPython's ``os.environ`` keeps its
+    entries (every set and delete goes through it) in the ``_data`` dict
+    under encoded keys, so a miss, the common case, is one dict lookup."""
+    if _ENV_DATA is None:
+        return os.environ.get(name)
+    key = _ENV_KEYS.get(name)
+    if key is None:
+        key = _ENV_KEYS[name] = os.environ.encodekey(name)
+    v = _ENV_DATA.get(key)
+    return None if v is None else os.environ.decodevalue(v)
+
+
 def check_records_enabled() -> bool:
     """``HELM_AMD_CHECK_RECORDS`` set (to anything but 0): every launch that
     reads layer records validates them first (``LayerKVCache.check_records``)."""
-    v = os.environ.get("HELM_AMD_CHECK_RECORDS")
+    v = _env_get("HELM_AMD_CHECK_RECORDS")
     return bool(v) and v != "0"
 
 
@@ -869,7 +888,7 @@ def _get_kv_copy_stream(device: torch.device) -> torch.cuda.Stream:
 
 def _async_kv_prefetch_enabled() -> bool:
     """HELM_DISABLE_ASYNC_KV gates the overlapped prefetch (ablations)."""
-    return not bool(os.environ.get("HELM_DISABLE_ASYNC_KV"))
+    return not bool(_env_get("HELM_DISABLE_ASYNC_KV"))
 
 
 # ── native attention ────────────────────────────────────────────────────────────
@@ -1199,27 +1218,31 @@ def _launch_seqs(query: torch.Tensor, addrs, t_max: int, page_tokens: int, align
     return out if out.dtype == query.dtype else out.to(query.dtype)
 
 
-# helm_decode_args word indices (include/helm_amd.h): 8-byte words, then
-# 4-byte words of the same struct
-_DA_Q, _DA_OUT, _DA_MASK, _DA_STREAM, _DA_MBS, _DA_MHS, _DA_MQS = range(7)
-_DA_PAGES, _DA_TOKK, _DA_TOKV, _DA_TOKHS = 7, 23, 39, 55
-_DA_NPAGES, _DA_TOKENS = 142, 158
-(_DA_B, _DA_HQ, _DA_HKV, _DA_D, _DA_PTOK, _DA_AL16, _DA_MDT, _DA_KVDT,
- _DA_APPEND) = range(174, 183)
-_DA_SCALE, _DA_SOFTCAP = 184, 185
+# helm_decode_args (include/helm_amd.h) written with precompiled structs:
+# q, out, mask, stream and the mask strides; the per-sequence arrays; B ..
+# pad, scale, softcap
+_DA_FIELDS = _native.DECODE_ARGS_DTYPE.fields
+_DA_HEAD = struct.Struct("<4Q3q")
+_DA_TAIL = struct.Struct("<10i2f")
+_DA_TAIL_OFF = _DA_FIELDS["B"][1]
+_DA_PAGES, _DA_TOKK, _DA_TOKV, _DA_TOKHS, _DA_NPAGES, _DA_TOKENS = (
+    _DA_FIELDS[f][1] for f in ("seq_pages", "tok_k", "tok_v", "tok_head_stride", "seq_npages",
+                               "seq_tokens"))
+_DA_U64, _DA_I64, _DA_I32 = struct.Struct("<Q"), struct.Struct("<q"), struct.Struct("<i")
+assert _DA_FIELDS["q"][1] == 0 and _DA_FIELDS["seq_pages"][1] == _DA_HEAD.size
+assert _DA_TAIL_OFF + _DA_TAIL.size == _native.DECODE_ARGS_DTYPE.itemsize
 _MASK_CODES = {torch.float32: _native.HELM_F32, torch.bfloat16: _native.HELM_BF16,
                torch.float16: _native.HELM_F16}
 _KV16 = {torch.bfloat16: _native.HELM_BF16, torch.float16: _native.HELM_F16}
 
 
 def _decode_args():
-    """This thread's helm_decode_args block and its word views."""
+    """This thread's helm_decode_args block: (the struct array, its bytes,
+    its address)."""
     a = getattr(_tls, "decode_args", None)
     if a is None:
         arr = np.zeros(1, dtype=_native.DECODE_ARGS_DTYPE)
-        raw = arr.view(np.uint8)
-        a = _tls.decode_args = (arr, raw.view(np.uint64), raw.view(np.int32),
-                                raw.view(np.float32), arr.ctypes.data)
+        a = _tls.decode_args = (arr, arr.view(np.uint8), arr.ctypes.data)
     return a
 
 
@@ -1239,20 +1262,21 @@ def _decode_step_fast(kvcms, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     B, Hq, S, D = q.shape
     kv_code = _KV16.get(q.dtype)
     if (kv_code is None or S != 1 or D != 128 or B > _native.DECODE_MAX_SEQS
-            or Hq > 16 * k.shape[1]             # more than one 16-row tile per KV head
-            or q.device.type != "cuda" or k.dtype is not q.dtype or v.dtype is not q.dtype
+            or not q.is_cuda or k.dtype is not q.dtype or v.dtype is not q.dtype
             or not q.is_contiguous()):
         return None
-    Hkv = k.shape[1]
-    if (k.shape[0] < B or k.shape[2] != 1 or k.stride(3) != 1 or v.stride(3) != 1
-            or k.stride(1) != v.stride(1) or (k.stride(1) * 2) % 16
-            or (k.data_ptr() | v.data_ptr() | (k.stride(0) * 2) | (v.stride(0) * 2)) % 16):
+    kB, Hkv, kS, _ = k.shape
+    ks, vs = k.stride(), v.stride()
+    kp, vp = k.data_ptr(), v.data_ptr()
+    qp = q.data_ptr()
+    if (Hq > 16 * Hkv                           # more than one 16-row tile per KV head
+            or kB < B or kS != 1 or ks[3] != 1 or vs[3] != 1 or ks[1] != vs[1]
+            or (ks[1] * 2) % 16 or (kp | vp | qp | (ks[0] * 2) | (vs[0] * 2)) % 16):
         return None
-    env = os.environ
     if (check_records_enabled() or not _async_kv_prefetch_enabled()
-            or env.get("HELM_AMD_FAST_DECODE") == "0" or env.get("HELM_AMD_FUSED_APPEND") == "0"
-            or env.get("HELM_AMD_KERNEL", "auto") not in ("", "auto", "mfma")
-            or q.data_ptr() % 16):
+            or _env_get("HELM_AMD_FAST_DECODE") == "0"
+            or _env_get("HELM_AMD_FUSED_APPEND") == "0"
+            or _env_get("HELM_AMD_KERNEL") not in (None, "", "auto", "mfma")):
         return None
     device = q.device
     sig = (q.dtype, Hkv, D)
@@ -1275,24 +1299,28 @@ def _decode_step_fast(kvcms, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         layers.append(layer)
     if B > 1 and len({id(layer) for layer in layers}) != B:
         return None
-    mask_code, mbs, mhs, mqs, mptr = _native.HELM_F32, 0, 0, 0, 0
+    mask_code, mbs, mhs, mptr = _native.HELM_F32, 0, 0, 0
     m = attention_mask
     if m is not None:
         mask_code = _MASK_CODES.get(m.dtype)
         t_max = max(l._tail_tok_off + l.tail_page.used_tokens for l in layers) + 1
-        if (mask_code is None or m.device != device or m.dim() != 4 or m.stride(3) != 1
-                or m.shape[0] not in (1, B) or m.shape[1] not in (1, Hq) or m.shape[2] != 1
-                or m.shape[3] < t_max):
+        mshape = m.shape
+        if (mask_code is None or m.device != device or len(mshape) != 4
+                or mshape[0] not in (1, B) or mshape[1] not in (1, Hq) or mshape[2] != 1
+                or mshape[3] < t_max):
+            return None
+        mst = m.stride()
+        if mst[3] != 1:
             return None
         mptr = m.data_ptr()
-        mbs = m.stride(0) if m.shape[0] > 1 else 0
-        mhs = m.stride(1) if m.shape[1] > 1 else 0
+        mbs = mst[0] if mshape[0] > 1 else 0
+        mhs = mst[1] if mshape[1] > 1 else 0
     # HELM's append_decode bookkeeping (kv_cache.py:145-171): the tail gains
     # the token
-    arr, w64, w32, f32, addr = _decode_args()
-    ks0, vs0 = k.stride(0) * 2, v.stride(0) * 2
-    kp, vp = k.data_ptr(), v.data_ptr()
+    _, buf, addr = _decode_args()
+    ks0, vs0, hs = ks[0] * 2, vs[0] * 2, ks[1]
     page_tokens = 0
+    u64, i64, i32 = _DA_U64.pack_into, _DA_I64.pack_into, _DA_I32.pack_into
     for b, layer in enumerate(layers):
         tail = layer.tail_page
         used = tail.used_tokens + 1
@@ -1300,33 +1328,19 @@ def _decode_step_fast(kvcms, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         layer.total_tokens += 1
         n = len(layer.pages)
         layer._rec["used"][n - 1] = used
-        w64[_DA_PAGES + b] = layer._dev.data_ptr()
-        w64[_DA_TOKK + b] = kp + b * ks0
-        w64[_DA_TOKV + b] = vp + b * vs0
-        w64[_DA_TOKHS + b] = k.stride(1)
-        w32[_DA_NPAGES + b] = n
-        w32[_DA_TOKENS + b] = layer._tail_tok_off + used
+        u64(buf, _DA_PAGES + 8 * b, layer._dev.data_ptr())
+        u64(buf, _DA_TOKK + 8 * b, kp + b * ks0)
+        u64(buf, _DA_TOKV + 8 * b, vp + b * vs0)
+        i64(buf, _DA_TOKHS + 8 * b, hs)
+        i32(buf, _DA_NPAGES + 4 * b, n)
+        i32(buf, _DA_TOKENS + 4 * b, layer._tail_tok_off + used)
         if layer._page_tokens > page_tokens:
             page_tokens = layer._page_tokens
     out = torch.empty_like(q)
-    w64[_DA_Q] = q.data_ptr()
-    w64[_DA_OUT] = out.data_ptr()
-    w64[_DA_MASK] = mptr
-    w64[_DA_STREAM] = _engine.stream_ptr(device)
-    w64[_DA_MBS] = mbs
-    w64[_DA_MHS] = mhs
-    w64[_DA_MQS] = mqs
-    w32[_DA_B] = B
-    w32[_DA_HQ] = Hq
-    w32[_DA_HKV] = Hkv
-    w32[_DA_D] = D
-    w32[_DA_PTOK] = page_tokens
-    w32[_DA_AL16] = 1
-    w32[_DA_MDT] = mask_code
-    w32[_DA_KVDT] = kv_code
-    w32[_DA_APPEND] = 1
-    f32[_DA_SCALE] = scale
-    f32[_DA_SOFTCAP] = 0.0
+    _DA_HEAD.pack_into(buf, 0, qp, out.data_ptr(), mptr, _engine.stream_ptr(device),
+                       mbs, mhs, 0)
+    _DA_TAIL.pack_into(buf, _DA_TAIL_OFF, B, Hq, Hkv, D, page_tokens, 1, mask_code, kv_code,
+                       1, 0, scale, 0.0)
     rc = _native.entry("helm_decode_step")(_engine.get_engine(device), addr)
     if rc:
         _native.check("helm_decode_step", rc)

@@ -196,7 +196,14 @@ int helm_paged_decode_attn_static(const void* q, void* out,
  * attended in token-offset order whatever their order in `pages`.  A sequence
  * with no pages yields zeros.  Staged host pages require B == 1
  * (HELM_E_UNSUPPORTED otherwise).  Environment HELM_AMD_HOST_READ=copy stages
- * every host page, =direct reads every readable one in place. */
+ * every host page, =direct reads every readable one in place.
+ * HELM_AMD_STAGE_STREAM=side issues the staging copies on the engine's side
+ * stream instead, each chunk's launch waiting for its copies by event; once
+ * the engine has evicted pages (helm_evict_pages) those copies wait only for
+ * the last eviction and for the launches that last read their ring slots, so
+ * host pages written by any other means must then be complete when the call
+ * is made; before the first eviction they wait for all earlier work on
+ * `stream`. */
 int helm_stream_attn(helm_engine* eng, const void* q, void* out,
                      int B, int Hq, int Hkv, int q_len, int D,
                      const helm_page* pages, const int32_t* seq_off,
@@ -337,7 +344,9 @@ int helm_decode_front(const void* q_proj, const void* k_proj, const void* v_proj
  * queued there; regions adjacent on both sides are merged into one copy.
  * With sync != 0 the call returns after the copies completed (HELM's
  * synchronous move_page, helm/runtime/kv_allocator.py:104-116); otherwise
- * later work on `stream` is ordered after them.  Replaces
+ * later work on `stream` is ordered after them, and so are the engine's
+ * side-stream staging copies (an event recorded after them; an eviction on
+ * another stream than the previous one first waits for it).  Replaces
  * KVAllocator.move_page GPU->CPU. */
 int helm_evict_pages(helm_engine* eng, int n, const uint64_t* src_dev,
                      const uint64_t* dst_host, const uint64_t* bytes,

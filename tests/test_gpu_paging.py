@@ -272,12 +272,18 @@ def test_staging_ring_reuse_many_chunks(host_read, stage_stream):
     _RING_OUTS[(host_read, stage_stream)] = outs[0].cpu()
 
 
+@pytest.mark.parametrize("writer", ["evict", "torch"])
 @pytest.mark.parametrize("chunk_mb,slots", [(1, 2), (64, 2)])
-def test_staged_copies_follow_callers_host_writes(stage_stream, chunk_mb, slots, monkeypatch):
+def test_staged_copies_follow_callers_host_writes(stage_stream, chunk_mb, slots, writer,
+                                                  monkeypatch):
     """Host pages rewritten on the caller's stream just before the call (a
-    device-to-host copy queued behind a long matmul, as an eviction would be)
-    are staged with their new contents: the side stream's copies wait for
-    the caller's earlier work.  Two calls in a row with different contents."""
+    device-to-host copy queued behind a long matmul) are staged with their new
+    contents.  Written by the engine's helm_evict_pages, as the runtime
+    evicts, the side stream's copies wait for that eviction's event (and for
+    the launches that last read their ring slots, here those of the call
+    before); written by a torch copy on an engine that has never evicted,
+    they wait for all of the caller's earlier work.  Two calls in a row with
+    different contents."""
     monkeypatch.setenv("HELM_AMD_HOST_READ", "copy")
     g = torch.Generator().manual_seed(41)
     n_host, n_dev = 96, 32
@@ -302,7 +308,14 @@ def test_staged_copies_follow_callers_host_writes(stage_stream, chunk_mb, slots,
             torch.cuda.synchronize()
             for _ in range(8):            # keep the caller's stream busy for a while
                 a = (a @ a).clamp_(-1, 1)
-            host.copy_(new, non_blocking=True)   # D2H behind the matmuls
+            if writer == "torch":
+                host.copy_(new, non_blocking=True)   # D2H behind the matmuls
+            else:
+                reg = [np.array([x], dtype=np.uint64) for x in
+                       (new.data_ptr(), host.data_ptr(), new.numel() * new.element_size())]
+                _native.call("helm_evict_pages", eng, 1, _native.ptr(reg[0]),
+                             _native.ptr(reg[1]), _native.ptr(reg[2]), 0,
+                             torch.cuda.current_stream().cuda_stream)
             out = torch.empty_like(q)
             _native.call("helm_stream_attn", eng, q.data_ptr(), out.data_ptr(), 1, 32, 8, 1, 128,
                          _native.ptr(pages), _native.ptr(seq_off), 1 / math.sqrt(128), 0.0,

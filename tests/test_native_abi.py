@@ -85,3 +85,47 @@ def test_no_cpu_fallback_symbols():
     lib_syms = os.popen(f"nm -D --defined-only {_native.LIB_PATH}").read()
     exported = set(re.findall(r" T (helm_[a-z_0-9]+)", lib_syms))
     assert exported == set(_declared_functions())
+
+
+def test_decode_step_argument_block_layout():
+    """The fast decode path packs helm_decode_args with precompiled structs;
+    every field lands where the struct (and the numpy record type that
+    mirrors it) has it."""
+    from helm_amd.runtime import kv_cache as KC
+    arr, buf, addr = KC._decode_args()
+    assert addr == arr.ctypes.data and buf.nbytes == 744
+    KC._DA_HEAD.pack_into(buf, 0, 11, 12, 13, 14, 15, -16, 17)
+    KC._DA_TAIL.pack_into(buf, KC._DA_TAIL_OFF, 3, 32, 8, 128, 16, 1, 2, 3, 1, 0, 0.25, 30.0)
+    for b in range(3):
+        KC._DA_U64.pack_into(buf, KC._DA_PAGES + 8 * b, 100 + b)
+        KC._DA_U64.pack_into(buf, KC._DA_TOKK + 8 * b, 200 + b)
+        KC._DA_U64.pack_into(buf, KC._DA_TOKV + 8 * b, 300 + b)
+        KC._DA_I64.pack_into(buf, KC._DA_TOKHS + 8 * b, 400 + b)
+        KC._DA_I32.pack_into(buf, KC._DA_NPAGES + 4 * b, 500 + b)
+        KC._DA_I32.pack_into(buf, KC._DA_TOKENS + 4 * b, 600 + b)
+    r = arr[0]
+    assert [int(r[f]) for f in ("q", "out", "mask", "stream", "mask_bstride", "mask_hstride",
+                                "mask_qstride")] == [11, 12, 13, 14, 15, -16, 17]
+    assert [int(r[f]) for f in ("B", "Hq", "Hkv", "D", "page_tokens", "aligned16", "mask_dtype",
+                                "kv_dtype", "append", "pad")] == [3, 32, 8, 128, 16, 1, 2, 3, 1, 0]
+    assert float(r["scale"]) == 0.25 and float(r["softcap"]) == 30.0
+    for f, base in (("seq_pages", 100), ("tok_k", 200), ("tok_v", 300),
+                    ("tok_head_stride", 400), ("seq_npages", 500), ("seq_tokens", 600)):
+        assert list(r[f][:3]) == [base, base + 1, base + 2]
+
+
+def test_fast_env_lookup_follows_environ(monkeypatch):
+    from helm_amd.runtime import kv_cache as KC
+    name = "HELM_AMD_TEST_SWITCH"
+    monkeypatch.delenv(name, raising=False)
+    assert KC._env_get(name) is None
+    monkeypatch.setenv(name, "0")
+    assert KC._env_get(name) == "0"
+    monkeypatch.setenv(name, "1")
+    assert KC._env_get(name) == "1"
+    monkeypatch.delenv(name)
+    assert KC._env_get(name) is None
+    monkeypatch.setenv("HELM_AMD_CHECK_RECORDS", "1")
+    assert KC.check_records_enabled()
+    monkeypatch.setenv("HELM_AMD_CHECK_RECORDS", "0")
+    assert not KC.check_records_enabled()

@@ -139,3 +139,31 @@ def test_run_script_and_bench_summary(tmp_path):
     out = R.bench_summaries(str(p), str(tmp_path), "python3 bench.py --stamps")
     assert len(out) == 2
     assert "| 256 | 21.5 | 6242.7 | 24.5 |" in open(out[1]).read()
+
+
+def test_copy_runs_group_large_copies_by_stream(tmp_path):
+    """Consecutive large host-to-device copies on one stream form a run; its
+    median copy time and start-to-start cycle; small and device-to-host
+    copies do not count."""
+    cols = ["Kind", "Direction", "Stream_Id", "Source_Agent_Id", "Destination_Agent_Id",
+            "Correlation_Id", "Start_Timestamp", "End_Timestamp"]
+    rows = []
+    t = 0
+    for stream, n, dur, cyc in (("1", 3, 1_170_000, 1_210_000), ("0", 4, 1_177_000, 1_300_000),
+                                ("2", 3, 1_185_000, 1_250_000)):
+        for _ in range(n):
+            rows.append(("MEMORY_COPY", "MEMORY_COPY_HOST_TO_DEVICE", stream, t, t + dur))
+            rows.append(("MEMORY_COPY", "MEMORY_COPY_HOST_TO_DEVICE", stream, t + 10, t + 4000))
+            rows.append(("MEMORY_COPY", "MEMORY_COPY_DEVICE_TO_HOST", stream, t + 20, t + 900_000))
+            t += cyc
+        t += 20_000_000
+    with open(tmp_path / "run_memory_copy_trace.csv", "w", newline="") as f:
+        w = csv.DictWriter(f, cols)
+        w.writeheader()
+        for i, (kind, d, s, a, b) in enumerate(rows):
+            w.writerow({"Kind": kind, "Direction": d, "Stream_Id": s, "Correlation_Id": i,
+                        "Start_Timestamp": a, "End_Timestamp": b})
+    runs = R.copy_runs([str(tmp_path)])
+    assert [(r["stream"], r["copies"]) for r in runs] == [("1", 3), ("0", 4), ("2", 3)]
+    assert runs[1]["copy_us_median"] == 1177.0 and runs[1]["cycle_us_median"] == 1300.0
+    assert runs[2]["cycle_us_median"] == 1250.0 and runs[0]["start_ms"] == 0.0
