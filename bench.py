@@ -768,7 +768,7 @@ def gpu_runtime_decode(args, torch, W, layers=8, steps=25, seed=11):
     dev = torch.device("cuda:0")
     P = w.page_size
     a = KVAllocator(layers, w.Hkv, w.D, page_size=P, dtype=w.dtype)
-    a.reserve_batch(layers * (w.T // P + 4 * steps // P + 4), dev)
+    a.reserve_batch(layers * (w.T // P + (8 * steps + 8) // P + 4), dev)
     random.Random(seed).shuffle(a.gpu_free_pool)
     m = KVCacheManager(a, gpu_high_watermark_bytes=10 ** 13)
     m.initialize_layer_caches(layers)
@@ -796,23 +796,32 @@ def gpu_runtime_decode(args, torch, W, layers=8, steps=25, seed=11):
                 out = _decode_batched([m], q[lid], kn[lid], vn[lid], lid, scale, mask)
 
     res = {"workload": f"qwen3-8b-32k through _decode_batched: {layers} layers of {w.T} "
-                       "tokens rotated, B=1, bf16, one call per layer per step"}
+                       "tokens rotated, B=1, bf16, one call per layer per step",
+           "timing": f"median of 3 runs of {steps} steps per label, masked and unmasked runs "
+                     "interleaved, after 3 warm-up steps of each"}
+    runs = {"masked": [], "unmasked": []}
     for label, masked in (("masked", True), ("unmasked", False)):
-        run(1, masked)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        e0.record(stream)
-        run(steps, masked)
-        e1.record(stream)
-        t_issue = time.perf_counter() - t0
-        torch.cuda.synchronize()
-        wall = (time.perf_counter() - t0) / (steps * layers)
-        gpu = e0.elapsed_time(e1) / 1e3 / (steps * layers)
-        alg = W.algorithmic_bytes(w, [m.layers[0].total_tokens])
+        run(3, masked)
+    for _ in range(3):
+        for label, masked in (("masked", True), ("unmasked", False)):
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record(stream)
+            run(steps, masked)
+            e1.record(stream)
+            t_issue = time.perf_counter() - t0
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+            runs[label].append((wall, e0.elapsed_time(e1) / 1e3, t_issue))
+    n = steps * layers
+    alg = W.algorithmic_bytes(w, [m.layers[0].total_tokens])
+    for label, rr in runs.items():
+        wall, gpu, issue = (sorted(x[i] for x in rr)[1] / n for i in range(3))
         res[label] = {"us_per_call_wall": round(wall * 1e6, 2),
                       "us_per_call_gpu_events": round(gpu * 1e6, 2),
-                      "us_per_call_host_issue": round(t_issue / (steps * layers) * 1e6, 2),
+                      "us_per_call_host_issue": round(issue * 1e6, 2),
+                      "us_per_call_wall_runs": [round(x[0] / n * 1e6, 2) for x in rr],
                       "GBs_wall": round(alg / wall / 1e9, 1),
                       "roofline_frac_wall": round(alg / wall / 1e9 / HBM_PEAK_GBS, 4)}
     # the last call (layer layers-1, unmasked) against the oracle on two KV heads
