@@ -368,9 +368,12 @@ extern "C" int helm_cpu_stream_attn(const void* q, void* out, int B, int Hq, int
     nsplit = nsplit < cap ? nsplit : cap;
   }
   J.nsplit = nsplit;
-  std::vector<float> part;
   if (nsplit > 1) {
-    part.resize((size_t)base * nsplit * J.RT * (J.Dp + 2));
+    // the splits' partial rows: this calling thread's buffer, kept between
+    // calls (every row is written before the merge reads it)
+    thread_local std::vector<float> part;
+    const size_t need = (size_t)base * nsplit * J.RT * (J.Dp + 2);
+    if (part.size() < need) part.resize(need);
     J.part = part.data();
   }
   if (isa == HELM_CPU_ISA_AVX512)
