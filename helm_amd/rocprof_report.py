@@ -64,7 +64,7 @@ RUNS = collections.OrderedDict([
     ("write", (["--pmc", "WRITE_SIZE"], _PMC_DECODE, 150)),
     ("copies", (["--kernel-trace", "--memory-copy-trace"],
                 ["--no-configs", "--no-runtime", "--no-full-step", "--no-prefill", "--no-gemv",
-                 "--no-cpu", "--offload-steps", "5"], 300)),
+                 "--no-cpu"], 300)),
     ("pmc_a", (["--pmc"] + _PMC_A, _PREFILL_ONLY, 150)),
     ("pmc_b", (["--pmc"] + _PMC_B, _PREFILL_ONLY, 150)),
 ])
