@@ -110,7 +110,8 @@ def parse():
 def split_kernel_us(torch, step, steps):
     """HIP-event durations (us) of the attention (split) kernel of `steps`
     calls of `step`, the split merge after it excluded: start / stop events
-    attached to that launch (helm_profile_split_kernels).  Mean and median."""
+    attached to that launch (helm_profile_split_kernels).  Mean, median and
+    the 90th percentile and maximum."""
     from helm_amd import _native
     lib = _native.load()
     _native.call("helm_profile_split_kernels", steps)
@@ -125,7 +126,8 @@ def split_kernel_us(torch, step, steps):
                                f"{_native.load().helm_last_error_string()}")
     finally:
         _native.call("helm_profile_split_kernels", 0)
-    return float(buf.mean()), float(np.median(buf))
+    return (float(buf.mean()), float(np.median(buf)), float(np.percentile(buf, 90)),
+            float(buf.max()))
 
 
 def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=None, steps=None,
@@ -174,9 +176,10 @@ def gpu_headline(args, torch, W, paged, name="qwen3-8b-32k", seed=1, n_pools=Non
     ms_events = e0.elapsed_time(e1)
     per_call_s = ms_events / 1e3 / steps
     # a second pass of the same calls, the attention kernel timed alone
-    kern = split_kernel_us(torch, step, steps) if kernel_timing else (None, None)
+    kern = split_kernel_us(torch, step, steps) if kernel_timing else (None,) * 4
     return {
         "split_kernel_us_mean": kern[0], "split_kernel_us_median": kern[1],
+        "split_kernel_us_p90": kern[2], "split_kernel_us_max": kern[3],
         "w": w, "case": case, "alg_bytes": alg, "kv_bytes": W.kv_bytes(w, lens),
         "per_call_s": per_call_s, "wall_ms_per_step": wall * 1e3 / steps,
         "host_issue_us_per_call": (t_issued - t0) * 1e6 / steps,
@@ -1204,6 +1207,8 @@ def main():
                      "alg_bytes_per_launch": h["alg_bytes"],
                      "avg_launch_us": round(kern_us, 3),
                      "median_launch_us": round(h["split_kernel_us_median"], 3),
+                     "p90_launch_us": round(h["split_kernel_us_p90"], 3),
+                     "max_launch_us": round(h["split_kernel_us_max"], 3),
                      "launch": "decode_mfma_kernel<bf16, PoolSrc, 0, 4>, the dominant kernel "
                                "of one helm_paged_decode_attn call (256 workgroups: 32 splits "
                                "of 64 pages x 8 KV heads; it reads all K/V, q and the page "
