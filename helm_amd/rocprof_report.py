@@ -8,9 +8,9 @@ kernel).  ``commands`` prints them as a shell script that writes every run
 under one directory; ``all`` then writes the summaries (markdown tables and
 the JSON files ``bench.py`` reads) from that directory:
 
-    python -m helm_amd.rocprof_report commands --out gpurun_out/prof > run_prof.sh
+    python -m helm_amd.rocprof_report commands --out rocprof_runs > run_prof.sh
     bash run_prof.sh                      # on the GPU machine
-    python -m helm_amd.rocprof_report all --in gpurun_out/prof --out profiles
+    python -m helm_amd.rocprof_report all --in rocprof_runs --out profiles
 
 Single summaries: ``kernels`` (per kernel and grid: dispatches and durations
 from ``*_kernel_trace.csv``), ``traffic`` (HBM bytes per dispatch from the
@@ -76,7 +76,7 @@ def run_commands(out_dir: str, repo: str = "$R") -> List[str]:
     counter passes under SIGKILL limits (a pass that asks for more counters
     than a block holds hangs)."""
     lines = ["#!/bin/bash", "# rocprofv3 runs behind profiles/ (helm_amd/rocprof_report.py)",
-             f'R="${{GRAFT_REPO_ROOT:-$(pwd)}}"', "cd /tmp && export TMPDIR=/tmp",
+             'R="$(pwd)"   # run from the repository root', "cd /tmp && export TMPDIR=/tmp",
              f"mkdir -p {repo}/{out_dir}"]
     for name, (prof, bench, secs) in RUNS.items():
         kill = "-s KILL" if "--pmc" in prof else "-k 10"
@@ -88,7 +88,7 @@ def run_commands(out_dir: str, repo: str = "$R") -> List[str]:
     return lines
 
 
-def command_of(name: str, out_dir: str = "gpurun_out/prof") -> str:
+def command_of(name: str, out_dir: str = "rocprof_runs") -> str:
     prof, bench, _ = RUNS[name]
     return (f"rocprofv3 {' '.join(prof)} --output-format csv -d $R/{out_dir}/{name} -o run -- "
             f"python3 -u $R/bench.py {' '.join(bench)}")
@@ -346,6 +346,9 @@ def write_all(in_dir: str, out_dir: str, alg_bytes: int = 134242304) -> List[str
     written = []
     os.makedirs(out_dir, exist_ok=True)
 
+    def cmd_of(run):   # the run's command as it wrote under in_dir
+        return command_of(run, os.path.normpath(in_dir))
+
     def put(name, text):
         path = os.path.join(out_dir, name)
         with open(path, "w") as f:
@@ -359,19 +362,19 @@ def write_all(in_dir: str, out_dir: str, alg_bytes: int = 134242304) -> List[str
         st = kernel_stats(kernel_trace([os.path.join(in_dir, "headline")]))
         put("paged_decode_qwen3-8b-32k_kernel_stats.md",
             kernels_md(st, "Kernel time: Qwen3-8B 32k decode attention (the bench headline)",
-                       [command_of("headline")]))
+                       [cmd_of("headline")]))
         put("paged_decode_qwen3-8b-32k_kernel_times.json",
             json.dumps(headline_times(st), indent=1) + "\n")
     if have("configs"):
         st = kernel_stats(kernel_trace([os.path.join(in_dir, "configs")]))
         put("configs_c1_c3_c4_kernel_stats.md",
             kernels_md(st, "Kernel time: the other configurations (C1, C3, C4 and the masked "
-                           "headline)", [command_of("configs")]))
+                           "headline)", [cmd_of("configs")]))
     if have("fullstep"):
         st = kernel_stats(kernel_trace([os.path.join(in_dir, "fullstep")]))
         put("full_step_qwen3-14b-40l-b4-64k_kernel_stats.md",
             kernels_md(st, "Kernel time: the 40-layer Qwen3-14B decode step (B4 x 64k, 64 GB "
-                           "budget)", [command_of("fullstep")]))
+                           "budget)", [cmd_of("fullstep")]))
     if have("fetch") and have("write"):
         t = traffic([os.path.join(in_dir, "fetch")], [os.path.join(in_dir, "write")], alg_bytes,
                     r"^decode_mfma_kernel<bf16, PoolSrc, 0, 4>", r"^merge_splits_d128_kernel")
@@ -380,7 +383,7 @@ def write_all(in_dir: str, out_dir: str, alg_bytes: int = 134242304) -> List[str
         put("paged_decode_qwen3-8b-32k_traffic.json", json.dumps(t, indent=1) + "\n")
         md = ["# HBM traffic per call: Qwen3-8B 32k decode attention", "",
               "Commands (repo root `R`, from `/tmp` with `TMPDIR=/tmp`), one counter per pass:",
-              "", "```", command_of("fetch"), command_of("write"), "```", "",
+              "", "```", cmd_of("fetch"), cmd_of("write"), "```", "",
               "`--copy-calibration` adds three plain 1 GiB device copies; each counter's scale "
               "to bytes is what it reads for them (`python -m helm_amd.rocprof_report traffic`).",
               "", f"* FETCH_SIZE: x{t['fetch_scale']:.5f} KiB; WRITE_SIZE: "
@@ -399,7 +402,7 @@ def write_all(in_dir: str, out_dir: str, alg_bytes: int = 134242304) -> List[str
         md = ["# Host-to-device copies of the Qwen3-8B 32k call with 50% of its pages in "
               "pinned host memory", "",
               "Command (repo root `R`, from `/tmp` with `TMPDIR=/tmp`):", "", "```",
-              command_of("copies"), "```", "",
+              cmd_of("copies"), "```", "",
               "Runs of consecutive large (>= 0.5 ms) host-to-device copies on one stream, in "
               "the order the bench makes them: the device profile's 64 MiB link probe (its "
               "own stream), then the offload leg's modes, each call copying its 64 MiB of "
@@ -423,7 +426,7 @@ def write_all(in_dir: str, out_dir: str, alg_bytes: int = 134242304) -> List[str
         put("paged_decode_and_prefill_chunk_counters.md",
             counters_md(means, r"^(decode_mfma_kernel|chunk32_mfma_kernel|merge_)",
                         "SQ counters: decode kernel (Qwen3-8B 32k) and prefill chunk kernel "
-                        "(512 tokens over 32k)", [command_of("pmc_a"), command_of("pmc_b")]))
+                        "(512 tokens over 32k)", [cmd_of("pmc_a"), cmd_of("pmc_b")]))
     return written
 
 
@@ -492,7 +495,7 @@ def main(argv: Optional[List[str]] = None) -> int:
     ap = argparse.ArgumentParser(prog="python -m helm_amd.rocprof_report")
     sub = ap.add_subparsers(dest="cmd", required=True)
     c = sub.add_parser("commands", help="the rocprofv3 runs as a shell script")
-    c.add_argument("--out", default="gpurun_out/prof")
+    c.add_argument("--out", default="rocprof_runs")
     a = sub.add_parser("all", help="every summary from a directory of runs")
     a.add_argument("--in", dest="in_dir", required=True)
     a.add_argument("--out", default="profiles")

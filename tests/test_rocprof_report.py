@@ -111,11 +111,11 @@ def test_counter_ratios(tmp_path):
 
 
 def test_run_script_and_bench_summary(tmp_path):
-    lines = R.run_commands("gpurun_out/prof")
+    lines = R.run_commands("rocprof_runs")
     body = "\n".join(lines)
     assert lines[0] == "#!/bin/bash" and "cd /tmp && export TMPDIR=/tmp" in body
     for name in R.RUNS:
-        assert f"-d $R/gpurun_out/prof/{name} " in body
+        assert f"-d $R/rocprof_runs/{name} " in body
     # every counter pass under a SIGKILL time limit, the program after --
     for ln in lines:
         if "--pmc" in ln:
