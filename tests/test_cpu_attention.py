@@ -492,3 +492,25 @@ def test_tiny_llama_on_cpu_greedy_matches_hf():
             tok = logits[:, -1].argmax(-1, keepdim=True)
     mgr.restore()
     assert out_tokens == ref_tokens
+
+
+def test_scratch_kept_between_calls_of_other_shapes():
+    """Each thread's scratch and the split partials are kept between calls and
+    grown, never cleared: calls of different shapes in turn (a decode step, a
+    prompt chunk, a ragged batch, on several thread counts) give the bits
+    each gives alone."""
+    w = W.WORKLOADS["qwen3-0.6b-2k"]
+    dec, a1, o1 = _case(w, seed=11)
+    chk, a2, o2 = _case(w, seed=12, lens=[700], S=24)
+    wr = W.WORKLOADS["qwen3-14b-ragged-b8"]
+    rag, a3, o3 = _case(wr, seed=13, lens=[1500, 37, 900, 64, 16, 300, 1000, 5])
+    calls = [lambda t: _call(dec["q"], a1, o1, w.Hkv, w.dtype, threads=t),
+             lambda t: _call(chk["q"], a2, o2, w.Hkv, w.dtype, causal=1, threads=t),
+             lambda t: _call(rag["q"], a3, o3, wr.Hkv, wr.dtype, threads=t)]
+    for t in (3, 8):
+        alone = [f(t) for f in calls]
+        for _ in range(2):
+            for f, want in zip(calls, alone):
+                assert torch.equal(f(t), want)
+    _check(dec, calls[0](8), w)
+    _check(rag, calls[2](8), wr)
