@@ -10,7 +10,7 @@ the slot stride is ``2*Hkv*page*D`` elements and one page's head tile is
 from __future__ import annotations
 
 import math
-from typing import Dict, Optional, Sequence, Tuple
+from typing import Dict, Optional, Sequence
 
 import numpy as np
 import torch
