@@ -351,7 +351,7 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
         host time of each call of every run (issue, including any wait
         inside it) is kept under `label`."""
         saved = {k: os.environ.pop(k, None)
-                 for k in ("HELM_AMD_HOST_READ", "HELM_AMD_STAGE_STREAM")}
+                 for k in ("HELM_AMD_HOST_READ", "HELM_AMD_STAGE_STREAM", "HELM_AMD_SIDE_AHEAD")}
         os.environ.update(env)
         try:
             for _ in range(3):
@@ -385,12 +385,16 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
     # host pages staged through the device ring by hipMemcpyAsync (copies on
     # the engine's side stream, which wait only for the eviction and for the
     # earlier readers of their ring slots, overlapped with the device pages'
-    # launch and the earlier calls' kernels; or on the caller's stream after
+    # launch and the earlier calls' kernels, the host at most two calls ahead,
+    # or with no bound on that; or on the caller's stream after
     # the device pages' launch), read in place by the kernel over the
     # host link, and the engine's default (per call: pages in long address
     # runs are staged, copies on the caller's stream)
     per_staged = timed("staged", HELM_AMD_HOST_READ="copy")
     per_side = timed("staged_side_stream", HELM_AMD_HOST_READ="copy", HELM_AMD_STAGE_STREAM="side")
+    # the same without the engine's bound on how far the host queues ahead
+    per_side_unb = timed("staged_side_stream_unbounded", HELM_AMD_HOST_READ="copy",
+                         HELM_AMD_STAGE_STREAM="side", HELM_AMD_SIDE_AHEAD="0")
     per_one = timed("staged_one_stream", HELM_AMD_HOST_READ="copy", HELM_AMD_STAGE_STREAM="one")
     per_direct = timed("in_place", HELM_AMD_HOST_READ="direct")
     per = timed("default")
@@ -417,6 +421,7 @@ def gpu_offload(args, torch, W, name="qwen3-8b-32k-offload50", seed=2, steps=Non
         "staged_host_link_GBs": host_bytes / per_staged / 1e9,
         "staged_side_stream_ms_per_call": per_side * 1e3,
         "staged_side_stream_frac_of_measured_h2d": host_bytes / per_side / 1e9 / peak,
+        "staged_side_stream_unbounded_ms_per_call": per_side_unb * 1e3,
         "staged_one_stream_ms_per_call": per_one * 1e3,
         "timing": f"best of 3 runs of {steps} calls after 3 warm-up calls",
         "in_place_ms_per_call": per_direct * 1e3,
@@ -1139,7 +1144,10 @@ def main():
         log("offload: qwen3-8b-32k, oldest 50% in pinned host")
         off = gpu_offload(args, torch, W)
         log(f"offload {off['ms_per_call']:.3f} ms/call, host link {off['host_link_GBs']:.1f} GB/s "
-            f"({off['frac_of_measured_h2d'] * 100:.1f}% of measured {off['measured_h2d_GBs']:.1f})")
+            f"({off['frac_of_measured_h2d'] * 100:.1f}% of measured {off['measured_h2d_GBs']:.1f}); "
+            f"side stream {off['staged_side_stream_ms_per_call']:.3f} ms/call "
+            f"({off['staged_side_stream_frac_of_measured_h2d'] * 100:.1f}%), unbounded "
+            f"{off['staged_side_stream_unbounded_ms_per_call']:.3f}")
 
     gemv = None
     if not args.no_gemv:

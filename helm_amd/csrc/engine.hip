@@ -658,6 +658,12 @@ struct helm_engine {
   hipEvent_t evict_done = nullptr;
   hipStream_t evict_stream = nullptr;
   bool evict_recorded = false;
+  // the ends of the last side-stream calls (recorded on the caller's stream),
+  // by call count modulo kSideRing: the next such call waits on the host for
+  // the one HELM_AMD_SIDE_AHEAD calls back
+  static constexpr int kSideRing = 4;
+  hipEvent_t side_done[kSideRing] = {};
+  long long side_calls = 0;
   // descriptor uploads (pinned host -> device), a ring so the host can run ahead
   static constexpr int kUp = 8;
   char* up_host[kUp] = {};
@@ -767,6 +773,17 @@ bool host_read_in_place() { return host_read_mode() != 0; }
 bool stage_on_side_stream() {
   const char* e = env_get("HELM_AMD_STAGE_STREAM");
   return e && std::strcmp(e, "side") == 0;
+}
+
+// How many side-stream calls may be queued ahead of the host: a call first
+// waits until the one this many calls back has completed on its stream
+// (HELM_AMD_SIDE_AHEAD, 0..4, 0 = no bound).  Unbounded, the host ran 3-6
+// calls ahead and hipMemcpyAsync itself then held the calling thread for
+// 5-16 ms at a time (the copies queued behind the earlier calls' kernels),
+// after which the link and the kernels both waited for the host; two calls
+// keep the side stream's copies one call ahead of the kernels without that.
+int side_calls_ahead() {
+  return std::min(helm_engine::kSideRing, std::max(0, env_int("HELM_AMD_SIDE_AHEAD", 2)));
 }
 
 // The staging copies reach the link's rate only in large runs: hipMemcpyAsync
@@ -1005,6 +1022,8 @@ int helm_engine_create(int device, size_t chunk_bytes, int ring_slots,
       "hipEventCreate");
   chk(hipEventCreateWithFlags(&e->evict_done, hipEventDisableTiming),
       "hipEventCreate");
+  for (int i = 0; i < helm_engine::kSideRing; ++i)
+    chk(hipEventCreateWithFlags(&e->side_done[i], hipEventDisableTiming), "hipEventCreate");
   e->slot_reader.assign(e->ring_slots, 0);
   e->slot_ready.assign(e->ring_slots, nullptr);
   e->slot_free.assign(e->ring_slots, nullptr);
@@ -1073,6 +1092,8 @@ int helm_engine_destroy(helm_engine* e) {
   if (e->ev_a) (void)hipEventDestroy(e->ev_a);
   if (e->ev_b) (void)hipEventDestroy(e->ev_b);
   if (e->evict_done) (void)hipEventDestroy(e->evict_done);
+  for (hipEvent_t ev : e->side_done)
+    if (ev) (void)hipEventDestroy(ev);
   for (hipEvent_t ev : e->slot_ready)
     if (ev) (void)hipEventDestroy(ev);
   for (hipEvent_t ev : e->slot_free)
@@ -1454,6 +1475,15 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   rc = engine_ensure_ws(eng, pl.total(), st);
   if (rc != HELM_OK) return rc;
 
+  // ---- bounded run-ahead of side-stream calls (before any HIP copy call) ----
+  const bool side = n_host > 0 && stage_on_side_stream();
+  if (side) {
+    const int ahead = side_calls_ahead();
+    if (ahead > 0 && eng->side_calls >= ahead)
+      HELM_HIP(hipEventSynchronize(
+          eng->side_done[(eng->side_calls - ahead) % helm_engine::kSideRing]));
+  }
+
   // ---- upload descriptors + sequence offsets --------------------------------
   const size_t dbytes = n_desc * sizeof(helm_page);
   const size_t blob_bytes = align_up(dbytes, 16) + (B + 1) * sizeof(int32_t);
@@ -1512,7 +1542,6 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   // everything queued on the caller's stream before this call.  Events carry
   // no timestamps.  Without the side stream (the default) every copy is
   // queued on the caller's stream in launch order.
-  const bool side = stage_on_side_stream();
   const int n_chunks = (int)chunk_runs.size();
   auto issue_copies = [&](int c) -> int {
     const int slot = chunk_slot[c];
@@ -1574,6 +1603,10 @@ int helm_stream_attn(helm_engine* eng, const void* q, void* out, int B,
   }
   hipError_t e = launch_merge(s, 1, Hkv, st);
   if (e != hipSuccess) return hip_fail(e, "merge launch");
+  if (side) {
+    HELM_HIP(hipEventRecord(eng->side_done[eng->side_calls % helm_engine::kSideRing], st));
+    ++eng->side_calls;
+  }
   return engine_mark_upload_consumed(eng, st);
 }
 

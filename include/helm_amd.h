@@ -203,7 +203,9 @@ int helm_paged_decode_attn_static(const void* q, void* out,
  * the last eviction and for the launches that last read their ring slots, so
  * host pages written by any other means must then be complete when the call
  * is made; before the first eviction they wait for all earlier work on
- * `stream`. */
+ * `stream`.  A call of that mode with staged pages first waits on the host
+ * until the call of that mode HELM_AMD_SIDE_AHEAD (0..4, default 2, 0 = no
+ * wait) such calls earlier has completed on its stream. */
 int helm_stream_attn(helm_engine* eng, const void* q, void* out,
                      int B, int Hq, int Hkv, int q_len, int D,
                      const helm_page* pages, const int32_t* seq_off,

@@ -334,6 +334,75 @@ def test_staged_copies_follow_callers_host_writes(stage_stream, chunk_mb, slots,
         assert (out[0].double() - ref).abs().max().item() <= 1e-2
 
 
+_QUEUED_ONE = {}
+
+
+@pytest.mark.parametrize("ahead", ["0", "1", "2", "4"])
+def test_side_stream_calls_queued_back_to_back(ahead, monkeypatch):
+    """Six calls queued without a host wait, the host pages rewritten by
+    helm_evict_pages on the caller's stream before each (1 MiB chunks, two
+    ring slots: every slot is reused within a call and across calls).  With
+    the copies on the side stream, whatever bound HELM_AMD_SIDE_AHEAD puts on
+    how far the host runs ahead (0 = none), every call gives the bits of the
+    same call with its copies on the caller's stream, and those equal the
+    oracle."""
+    monkeypatch.setenv("HELM_AMD_HOST_READ", "copy")
+    g = torch.Generator().manual_seed(43)
+    n_host, n_dev, calls = 96, 32, 6
+    host = torch.zeros(n_host, 2, 8, 16, 128, dtype=torch.bfloat16).pin_memory()
+    dev_pool = torch.randn(n_dev, 2, 8, 16, 128, generator=g).bfloat16().to(DEV)
+    q = torch.randn(1, 32, 1, 128, generator=g).bfloat16().to(DEV)
+    news = [torch.randn(n_host, 2, 8, 16, 128, generator=g).bfloat16().to(DEV)
+            for _ in range(calls)]
+    slot_b = 2 * 8 * 16 * 128 * 2
+    pages = np.zeros(n_host + n_dev, dtype=_native.PAGE_DTYPE)
+    for j in range(n_host + n_dev):
+        if j < n_host:
+            base, flags = host.data_ptr() + j * slot_b, _native.HELM_PAGE_HOST
+        else:
+            base, flags = dev_pool.data_ptr() + (j - n_host) * slot_b, 0
+        pages[j] = (base, base + slot_b // 2, 16, 16 * j, 16 * 128, flags)
+    seq_off = np.array([0, len(pages)], dtype=np.int32)
+    stream = torch.cuda.current_stream().cuda_stream
+    reg_dst = np.array([host.data_ptr()], dtype=np.uint64)
+    reg_n = np.array([news[0].numel() * news[0].element_size()], dtype=np.uint64)
+
+    def run(mode):
+        monkeypatch.setenv("HELM_AMD_STAGE_STREAM", mode)
+        monkeypatch.setenv("HELM_AMD_SIDE_AHEAD", ahead)
+        lib, eng = _ring_engine(1 << 20, 2)
+        outs = []
+        try:
+            torch.cuda.synchronize()
+            for new in news:
+                src = np.array([new.data_ptr()], dtype=np.uint64)
+                _native.call("helm_evict_pages", eng, 1, _native.ptr(src), _native.ptr(reg_dst),
+                             _native.ptr(reg_n), 0, stream)
+                out = torch.empty_like(q)
+                _native.call("helm_stream_attn", eng, q.data_ptr(), out.data_ptr(), 1, 32, 8, 1,
+                             128, _native.ptr(pages), _native.ptr(seq_off), 1 / math.sqrt(128),
+                             0.0, None, 0, 0, 0, _native.HELM_F32, 0, _native.HELM_BF16,
+                             _native.HELM_BF16, stream)
+                outs.append(out)
+            torch.cuda.synchronize()
+        finally:
+            lib.helm_engine_destroy(eng)
+        return [o.cpu() for o in outs]
+
+    if "one" not in _QUEUED_ONE:
+        one = run("one")
+        for out, new in zip(one, news):
+            allp = torch.cat([new.cpu(), dev_pool.cpu()])
+            K = allp[:, 0].permute(1, 0, 2, 3).reshape(8, -1, 128).float()
+            V = allp[:, 1].permute(1, 0, 2, 3).reshape(8, -1, 128).float()
+            ref = A.attention_fp64_batched(q[0].cpu(), K, V)
+            assert (out[0].double() - ref).abs().max().item() <= 1e-2
+        _QUEUED_ONE["one"] = one
+    side = run("side")
+    for a, b in zip(side, _QUEUED_ONE["one"]):
+        assert torch.equal(a, b)
+
+
 def _kv_records(parts, Hkv, D, P):
     """helm_page records over [(slots tensor, slot index, host flag)], in order."""
     slot_b = 2 * Hkv * P * D * 2
