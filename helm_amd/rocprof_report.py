@@ -408,8 +408,9 @@ def write_all(in_dir: str, out_dir: str, alg_bytes: int = 134242304) -> List[str
               "own stream), then the offload leg's modes, each call copying its 64 MiB of "
               "host pages in one copy (3 warm-up calls and 3 timed runs per mode): forced "
               "staging (HELM_AMD_HOST_READ=copy, copies on the caller's stream), the side "
-              "stream (HELM_AMD_STAGE_STREAM=side: the engine's copy stream), one stream "
-              "(=one, the same as forced staging), the engine default (which stages this "
+              "stream (HELM_AMD_STAGE_STREAM=side: the engine's copy stream, the host at "
+              "most two calls ahead), the same with no such bound (HELM_AMD_SIDE_AHEAD=0), "
+              "one stream (=one, the same as forced staging), the engine default (which stages this "
               "one-run layout; the in-place mode before it copies nothing), and the bench's "
               "256 MiB pinned-copy peak.  A call's cycle is its copy plus whatever its "
               "copy waits for; on one stream that includes the previous call's kernels.  "
