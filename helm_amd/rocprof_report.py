@@ -39,8 +39,14 @@ from typing import Dict, Iterable, List, Optional
 # ── the runs ──────────────────────────────────────────────────────────────────
 _BENCH_QUIET = ["--no-full-step", "--no-offload", "--no-gemv", "--no-cpu", "--no-configs",
                 "--no-runtime", "--no-prefill"]
+# the headline's decode call and the prefill chunk, with the calibration copies
 _PMC_DECODE = ["--steps", "20", "--warmup", "4", "--no-cpu", "--no-offload", "--no-full-step",
-               "--no-prefill", "--no-configs", "--no-runtime", "--no-gemv", "--copy-calibration"]
+               "--no-configs", "--no-runtime", "--no-gemv", "--copy-calibration"]
+# algorithmic bytes of the prefill leg's chunk call (Qwen3-8B shape, 512 query
+# tokens over 32,768 cached, bf16): K and V once, the queries read, the output
+# written
+PREFILL_READ_BYTES = 32768 * 8 * 128 * 2 * 2 + 512 * 32 * 128 * 2
+PREFILL_ALG_BYTES = PREFILL_READ_BYTES + 512 * 32 * 128 * 2
 _PMC_A = ["SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VMEM_RD",
           "SQ_WAVES", "SQ_BUSY_CYCLES", "SQ_VALU_MFMA_BUSY_CYCLES"]
 _PMC_B = ["SQ_WAVE_CYCLES", "SQ_WAIT_INST_ANY", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_ANY",
@@ -397,6 +403,29 @@ def write_all(in_dir: str, out_dir: str, alg_bytes: int = 134242304) -> List[str
               f"* whole call: {t['hbm_bytes_per_launch']:,.0f} B, "
               f"x{t['traffic_over_algorithmic']:.4f}"]
         put("paged_decode_qwen3-8b-32k_traffic.md", "\n".join(md) + "\n")
+        try:
+            c = traffic([os.path.join(in_dir, "fetch")], [os.path.join(in_dir, "write")],
+                        PREFILL_ALG_BYTES, r"^chunk32_mfma_kernel<bf16, DescSrc, 4, 8>",
+                        r"^merge_rows_d128_kernel")
+        except ValueError:
+            c = None          # runs made without the prefill leg
+        if c is not None:
+            md = ["# HBM traffic per call: the prefill chunk (512 tokens over 32k, Qwen3-8B "
+                  "shape)", "",
+                  "The same two counter passes as the decode call's traffic:", "", "```",
+                  cmd_of("fetch"), cmd_of("write"), "```", "",
+                  f"* chunk kernel `chunk32_mfma_kernel<bf16, DescSrc, 4, 8>`: "
+                  f"{c['decode_fetch_bytes']:,.0f} B read, {c['decode_write_bytes']:,.0f} B "
+                  f"written per dispatch (the written bytes are the splits' partials)",
+                  f"* merge `merge_rows_d128_kernel`: {c['merge_fetch_bytes']:,.0f} B read, "
+                  f"{c['merge_write_bytes']:,.0f} B written",
+                  f"* algorithmic bytes (K and V once, queries, output): {PREFILL_ALG_BYTES:,}, "
+                  f"of which {PREFILL_READ_BYTES:,} read; the chunk kernel reads "
+                  f"x{c['decode_fetch_bytes'] / PREFILL_READ_BYTES:.4f} of those: the eight "
+                  "workgroups that share a KV head's split run on one XCD and share its L2, so "
+                  "each K/V byte crosses from HBM about once",
+                  f"* whole call: {c['hbm_bytes_per_launch']:,.0f} B"]
+            put("prefill_chunk32_qwen3-8b-512x32k_traffic.md", "\n".join(md) + "\n")
     if have("copies"):
         runs = copy_runs([os.path.join(in_dir, "copies")])
         md = ["# Host-to-device copies of the Qwen3-8B 32k call with 50% of its pages in "
