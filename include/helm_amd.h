@@ -50,7 +50,7 @@ enum helm_dtype { HELM_F16 = 0, HELM_BF16 = 1, HELM_F32 = 2 };
 enum helm_status {
   HELM_OK = 0,
   HELM_E_INVALID = -1,     /* bad argument (shape, pointer, size)          */
-  HELM_E_UNSUPPORTED = -2, /* valid request this build does not implement  */
+  HELM_E_UNSUPPORTED = -2, /* valid request the library does not implement */
   HELM_E_WORKSPACE = -3,   /* caller workspace smaller than required        */
 };
 

@@ -1,8 +1,8 @@
 """CPU oracle for HELM's streaming attention — TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import this module, and only as the checker (or, in bench.py, as the timed
-CPU baseline).  The product (helm_amd) never imports it: its own host-CPU
+import this module, and only as the reference results are compared with (or,
+in bench.py, as the timed CPU baseline).  The product (helm_amd) never imports it: its own host-CPU
 attention (helm_cpu_stream_attn in libhelm_cpu.so) is checked against it.
 
 Three independent statements of the same arithmetic:

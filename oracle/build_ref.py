@@ -1,6 +1,6 @@
 """Builds HELM's own fp16 GEMV (helm/kernels/fp16_gemv.cpp) from the reference
-tree into oracle/_ref/ — TEST INFRASTRUCTURE ONLY (a checker and the CPU
-baseline of the GEMV leg, never part of the product).
+tree into oracle/_ref/ — TEST INFRASTRUCTURE ONLY (a reference for the GEMV
+tests and the CPU baseline of the GEMV leg, never part of the product).
 
 One g++ command on the one source file where it lies, against the installed
 torch (the file is a torch extension: torch/extension.h + pybind11).  HELM

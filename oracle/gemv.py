@@ -2,7 +2,7 @@
 INFRASTRUCTURE ONLY.
 
 Only tests/ and bench.py's cpu_baseline leg may import this module, and only
-as the checker.  It states what helm_fp16_linear computes on its decode fast
+as the reference results are compared with.  It states what helm_fp16_linear computes on its decode fast
 path, in float64 numpy, without the kernel's structure:
 
     y = fp16( sum_j W[i, j] * x[j]  +  bias[i] )      (fp16_gemv.cpp:101-108, :137-151)

@@ -1,7 +1,7 @@
 """CPU model of HELM's page management — TEST INFRASTRUCTURE ONLY.
 
 Only tests/ (and __graft_entry__.smoke()) may import this module, as the
-checker of helm_amd.runtime's page bookkeeping.  It restates, over plain
+reference for helm_amd.runtime's page bookkeeping.  It restates, over plain
 Python objects and numpy payloads, the semantics of:
 
 * KVAllocator pools (helm/runtime/kv_allocator.py:6-163): LIFO free pools,
