@@ -97,6 +97,40 @@ def test_traffic_scales_from_the_calibration_copies(tmp_path):
         R.traffic([str(w)], [str(w)], 1, r"^decode_mfma", r"^merge_splits")
 
 
+CHK = "void helm::chunk32_mfma_kernel<helm::bf16_t, helm::DescSrc, 4, 8>(helm::AttnParams, X)"
+MRW = "void helm::merge_rows_d128_kernel<helm::bf16_t>(helm::AttnParams)"
+
+
+@pytest.mark.parametrize("with_chunk", [True, False])
+def test_prefill_traffic_summary_from_the_same_passes(tmp_path, with_chunk):
+    """The traffic passes that include the prefill leg also give the chunk
+    kernel's bytes (scaled like the decode kernel's) and its ratio to the K,
+    V and query bytes; passes without the prefill leg write no such file."""
+    gib = 1 << 30
+    runs = tmp_path / "runs"
+    f, w = runs / "fetch", runs / "write"
+    f.mkdir(parents=True)
+    w.mkdir()
+    chunk_f = [(CHK, "FETCH_SIZE", 74000.0), (MRW, "FETCH_SIZE", 16700.0)] if with_chunk else []
+    chunk_w = [(CHK, "WRITE_SIZE", 33284.0), (MRW, "WRITE_SIZE", 4096.0)] if with_chunk else []
+    _ctr(f / "run_counter_collection.csv",
+         [(COPY, "FETCH_SIZE", gib / 2048)] * 3 +
+         [(DEC, "FETCH_SIZE", 65000.0), (MRG, "FETCH_SIZE", 300.0)] + chunk_f)
+    _ctr(w / "run_counter_collection.csv",
+         [(COPY, "WRITE_SIZE", gib / 1024)] * 3 +
+         [(DEC, "WRITE_SIZE", 520.0), (MRG, "WRITE_SIZE", 8.0)] + chunk_w)
+    out = tmp_path / "out"
+    written = [str(x) for x in R.write_all(str(runs), str(out))]
+    name = "prefill_chunk32_qwen3-8b-512x32k_traffic.md"
+    assert any(x.endswith("paged_decode_qwen3-8b-32k_traffic.md") for x in written)
+    assert any(x.endswith(name) for x in written) == with_chunk
+    if with_chunk:
+        md = (out / name).read_text()
+        assert f"{74000 * 1024 * 2:,} B read, {33284 * 1024:,} B written" in md
+        assert f"x{74000 * 1024 * 2 / R.PREFILL_READ_BYTES:.4f}" in md
+        assert R.PREFILL_READ_BYTES == 32768 * 4096 + 512 * 32 * 256
+
+
 def test_counter_ratios(tmp_path):
     rows = [("void helm::chunk32_mfma_kernel<helm::bf16_t, helm::DescSrc, 4, 8>(A, B)", c, v)
             for c, v in (("SQ_INSTS_MFMA", 1000.0), ("SQ_INSTS_VALU", 5500.0),
