@@ -75,6 +75,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--pools", type=int, default=8, help="rotated KV pools (MALL hygiene)")
     ap.add_argument("--offload-steps", type=int, default=20)
+    ap.add_argument("--offload-idle", type=float, default=0.0, metavar="SECONDS",
+                    help="idle this long before the offload leg (after the heavy legs, "
+                         "copies that overlap kernels run at half rate for a while)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-offload", action="store_true")
@@ -1141,6 +1144,9 @@ def main():
 
     off = None
     if not args.no_offload:
+        if args.offload_idle > 0:
+            log(f"idle {args.offload_idle:g} s before the offload leg")
+            time.sleep(args.offload_idle)
         log("offload: qwen3-8b-32k, oldest 50% in pinned host")
         off = gpu_offload(args, torch, W)
         log(f"offload {off['ms_per_call']:.3f} ms/call, host link {off['host_link_GBs']:.1f} GB/s "
