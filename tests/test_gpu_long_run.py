@@ -47,7 +47,7 @@ def _model(arch: str, dtype):
     return cls(cfg).eval().to(device=DEV, dtype=dtype)
 
 
-def _greedy(model, prompt, watermark):
+def _greedy(model, prompt, watermark, steps=STEPS):
     """HELM's pipeline over the paged cache: chunked prefill, then greedy
     decode; returns the decode tokens, the logits each came from (CPU, fp32),
     the paging counters and the last layer's page states."""
@@ -74,7 +74,7 @@ def _greedy(model, prompt, watermark):
                                cache_position=torch.arange(past, total, device=DEV),
                                use_cache=False).logits
                 past = total
-            for t in range(STEPS):
+            for t in range(steps):
                 seen.append(logits[0, -1].float().cpu())
                 tok = logits[:, -1].argmax(-1, keepdim=True)
                 toks.append(int(tok))
@@ -110,3 +110,20 @@ def test_greedy_tokens_identical_with_and_without_offload(arch, dtype):
     assert (lg_res - lg_off).abs().max().item() <= LOGIT_TOL[dtype]
     # the run is not degenerate: it visits many tokens
     assert len(set(offload)) > 10, sorted(set(offload))
+
+
+def test_greedy_2048_tokens_as_helm_reports():
+    """HELM's own count: 2,048 greedy tokens (Qwen3, bf16) identical with and
+    without offload after the same 32,700-token prompt; the decode steps cross
+    128 page boundaries while every full page but the newest lives in pinned
+    host memory."""
+    model = _model("qwen3", torch.bfloat16)
+    g = torch.Generator().manual_seed(11)
+    prompt = torch.randint(0, VOCAB, (1, PROMPT), generator=g).to(DEV)
+    resident, lg_res, _, _ = _greedy(model, prompt, 1 << 40, steps=2048)
+    offload, lg_off, st_off, states_off = _greedy(model, prompt, 1024, steps=2048)
+    assert states_off.count("CPU") >= len(states_off) - 2 and st_off["pages_evicted"] > 0
+    first = next((i for i, (a, b) in enumerate(zip(resident, offload)) if a != b), None)
+    assert first is None, f"first differing token at decode step {first}"
+    assert len(offload) == 2048
+    assert (lg_res - lg_off).abs().max().item() <= LOGIT_TOL[torch.bfloat16]
